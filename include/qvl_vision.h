@@ -1,0 +1,199 @@
+/*
+ * qvl_vision.h — C ABI of the MI355X (gfx950) Qwen3-VL vision-tower library (libqvl.so).
+ *
+ * Drop-in replacement for the reference's `Qwen3VLModel.encode_vision` hot path
+ * (/root/reference/model.py:940-944 -> Qwen3VisionTransformer.__call__, model.py:801-851).
+ * Each entry replaces one reference function; the citation is on each declaration.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only. Device pointers are marked `d_`, host pointers `h_`.
+ *   - Every device entry is asynchronous on the caller's `stream` (a hipStream_t; NULL = the
+ *     default stream) and never allocates: scratch comes in through `workspace`.
+ *   - Return 0 (QVL_OK) or a negative QVL_ERR_* code; `qvl_last_error()` returns a message for
+ *     the last failure on the calling thread. No other global mutable state: entries are
+ *     re-entrant and may be called concurrently from several host threads on different streams.
+ *   - Activations are row-major [tokens, features]. "Packed" dense weights are [n_out, k_in]
+ *     row-major (the transpose of the reference's Flax kernel [in, out], model.py:1152-1153),
+ *     with n_out and k_in zero-padded to multiples of 64; biases and LayerNorm affine
+ *     parameters are float32 vectors (holding bf16-representable values in the bf16 mode).
+ *   - Token order is the reference's 2x2 merge-block order (sample.py:112-119).
+ */
+#ifndef QVL_VISION_H
+#define QVL_VISION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QVL_OK 0
+#define QVL_ERR_INVALID_ARG (-1)   /* bad shape / pointer / grid (e.g. odd h or w) */
+#define QVL_ERR_UNSUPPORTED (-2)   /* a shape or dtype this build has no kernel for */
+#define QVL_ERR_MISALIGNED (-3)    /* a pointer or leading dimension is not 16-byte aligned */
+#define QVL_ERR_WORKSPACE (-4)     /* workspace too small */
+#define QVL_ERR_LAUNCH (-5)        /* a HIP launch failed */
+
+#define QVL_DTYPE_F32 0
+#define QVL_DTYPE_BF16 1
+
+/* Epilogues of qvl_dense (all accumulate in fp32 and round once to the output dtype). */
+#define QVL_EPI_BIAS 0            /* y = x W^T + b                         (nn.Dense)          */
+#define QVL_EPI_BIAS_GELU 1       /* y = gelu_tanh(x W^T + b)              (Dense -> jax.nn.gelu) */
+#define QVL_EPI_BIAS_RESIDUAL 2   /* y = x W^T + b + r   (r may alias y)   (Dense -> residual add) */
+
+const char* qvl_last_error(void);
+const char* qvl_status_string(int status);
+int qvl_version(void);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Host-side integer metadata, built once per grid_thw.                                        */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Token and segment counts of a grid: n_tokens = sum t*h*w, n_segments = sum t.
+ * Replaces the shape arithmetic of model.py:825-834. Rejects h or w not divisible by `merge`. */
+int qvl_grid_counts(const int32_t* h_grid_thw, int64_t n_grids, int32_t merge,
+                    int64_t* n_tokens, int64_t* n_segments);
+
+/* Integer metadata of the tower, bit-exact with the reference:
+ *   h_cu_seqlens [n_segments+1] int32  model.py:831-834 (one segment per frame)
+ *   h_pos_hw     [n_tokens, 2]  int32  model.py:686-693 ((h, w) rotary ids, merge-block order)
+ *   h_tap_idx    [4, n_tokens]  int32  model.py:713-739, 761-764 (bilinear taps into the
+ *   h_tap_w      [4, n_tokens]  f32    learned table, incl. the jnp.repeat frame quirk);
+ *                                      weights rounded to bf16 when dtype == QVL_DTYPE_BF16
+ *                                      (model.py:749 casts them to the tower dtype).
+ * Any output pointer may be NULL to skip it. */
+int qvl_vision_metadata(const int32_t* h_grid_thw, int64_t n_grids, int32_t merge,
+                        int32_t num_position_embeddings, int32_t dtype,
+                        int32_t* h_cu_seqlens, int32_t* h_pos_hw, int32_t* h_tap_idx, float* h_tap_w);
+
+/* Attention work list for qvl_vision_attention / qvl_encode_vision: one int32 triple
+ * (segment start, segment end, first query) per query tile of the kernel's tile height,
+ * longest segment first. Replaces the per-segment Python loop of model.py:585-598.
+ * With h_tiles == NULL only *n_tiles is written. */
+int qvl_attention_worklist(const int32_t* h_cu_seqlens, int64_t n_segments, int32_t* h_tiles,
+                           int64_t capacity, int64_t* n_tiles);
+
+/* Rotary inverse frequencies theta^(-2j/(head_dim/2)), j < head_dim/4, float32
+ * (VisionRotaryEmbedding, model.py:540-546 with dim = head_dim/2, model.py:672). */
+int qvl_rotary_inv_freq(int32_t head_dim, float theta, float* h_inv_freq);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Device stages.                                                                              */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Pack a reference Flax kernel [k_in, n_out] (float32, row-major) into the GEMM layout
+ * [n_pad, k_pad] of `dtype` (n_pad, k_pad = round-up to 64, zero-filled).
+ * Load-time counterpart of model.py:1152-1153 (HF weight.T) + the Dense promotion to dtype. */
+int qvl_pack_dense_weight(void* stream, int32_t dtype, const float* d_kernel, int64_t k_in,
+                          int64_t n_out, void* d_packed);
+
+/* Cast float32 -> dtype (bf16 rounds to nearest even). Replaces `x.astype(dtype)` (model.py:556). */
+int qvl_cast(void* stream, int32_t dtype, const float* d_x, void* d_y, int64_t n);
+
+/* y[M, N] = epilogue(x[M, K] . W[N, K]^T + bias)  — nn.Dense call sites model.py:556, 570, 601,
+ * 611-613, 655-656 with their following activation / residual add fused in.
+ * K must be a multiple of 64 (packed weights are zero-padded); lda/ldc/ldr in elements. */
+int qvl_dense(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, int64_t lda,
+              const void* d_w, const float* d_bias, const void* d_residual, int64_t ldr,
+              void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k);
+
+/* LayerNorm over the last axis: fp32 mean / biased variance / rsqrt(var + eps), affine, cast
+ * back (model.py:375-388). cols must be a multiple of 8 and <= 8192. */
+int qvl_layer_norm(void* stream, int32_t dtype, const void* d_x, int64_t ldx, const float* d_gamma,
+                   const float* d_beta, void* d_y, int64_t ldy, int64_t rows, int64_t cols, float eps);
+
+/* Bilinear pos-embed: y[n, :] = sum_j w[j, n] * table[idx[j, n], :] (model.py:751-764).
+ * `d_table` is [num_position_embeddings, dim] in dtype. */
+int qvl_pos_embed(void* stream, int32_t dtype, const void* d_table, const int32_t* d_tap_idx,
+                  const float* d_tap_w, void* d_y, int64_t n_tokens, int64_t dim);
+
+/* Rotary table cs[n, j] = (cos, sin)(pos * inv_freq) as float2 [n_tokens, head_dim/2], with
+ * pos = pos_hw[n, 0] for j < head_dim/4 else pos_hw[n, 1] (model.py:694-698, 821-823);
+ * values rounded to bf16 when dtype == QVL_DTYPE_BF16 (`.astype(self.dtype)`, model.py:823). */
+int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* d_pos_hw, int64_t n_tokens,
+                     int32_t head_dim, float theta, void* d_cos_sin);
+
+/* Packed varlen vision attention with 2D rotary (model.py:569-600 between the qkv and proj
+ * Dense): q/k/v are [n_tokens, num_heads*head_dim] views (row stride ld_qkv elements, e.g. the
+ * three column blocks of the qkv Dense output), rotated in-kernel with `d_cos_sin`
+ * (qvl_rotary_table), then softmax(q k^T / sqrt(head_dim)) v per cu_seqlens segment
+ * (block-diagonal, non-causal, fp32 online softmax). Output [n_tokens, num_heads*head_dim]
+ * row stride ld_out. `d_tiles` is the qvl_attention_worklist output (device copy).
+ * Workspace: qvl_vision_attention_workspace_size(). head_dim in {64, 72}. */
+int qvl_vision_attention_workspace_size(int64_t n_tokens, int32_t num_heads, int32_t head_dim,
+                                        size_t* bytes);
+int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const void* d_k,
+                         const void* d_v, int64_t ld_qkv, const void* d_cos_sin,
+                         const int32_t* d_tiles, int64_t n_tiles, void* d_out, int64_t ld_out,
+                         int64_t n_tokens, int32_t num_heads, int32_t head_dim,
+                         void* d_workspace, size_t workspace_bytes);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Whole tower: Qwen3VisionTransformer.__call__ (model.py:801-851) / encode_vision (940-944).   */
+/* ------------------------------------------------------------------------------------------ */
+
+typedef struct qvl_vision_config {
+  int32_t hidden_size;              /* D                                   */
+  int32_t out_hidden_size;          /* merger output width                 */
+  int32_t depth;
+  int32_t num_heads;
+  int32_t intermediate_size;        /* I (unpadded)                        */
+  int32_t patch_volume;             /* C * Tp * P * P                      */
+  int32_t spatial_merge_size;       /* must be 2                           */
+  int32_t num_position_embeddings;
+  int32_t n_deepstack;
+  int32_t deepstack_indexes[8];
+  float ln_eps;                     /* 1e-6                                */
+  float rope_theta;                 /* 10000                               */
+  int32_t dtype;                    /* QVL_DTYPE_BF16                      */
+} qvl_vision_config;
+
+typedef struct qvl_block_weights {           /* blocks_{i} (model.py:617-630)          */
+  const float* norm1_w; const float* norm1_b;
+  const float* norm2_w; const float* norm2_b;
+  const void* qkv_w;  const float* qkv_b;    /* packed [3D, D]                        */
+  const void* proj_w; const float* proj_b;   /* packed [D, D]                         */
+  const void* fc1_w;  const float* fc1_b;    /* packed [I_pad, D]                     */
+  const void* fc2_w;  const float* fc2_b;    /* packed [D, I_pad]                     */
+} qvl_block_weights;
+
+typedef struct qvl_merger_weights {          /* merger / deepstack_mergers_{j} (633-656) */
+  const float* norm_w; const float* norm_b;  /* [D] (main) or [4D] (deepstack)         */
+  const void* fc1_w; const float* fc1_b;     /* packed [4D, 4D]                        */
+  const void* fc2_w; const float* fc2_b;     /* packed [Dout_pad, 4D]                  */
+} qvl_merger_weights;
+
+typedef struct qvl_vision_weights {
+  const void* patch_w; const float* patch_b; /* packed [D, patch_volume] (model.py:1136-1139) */
+  const void* pos_table;                     /* [num_position_embeddings, D] in dtype         */
+  const qvl_block_weights* blocks;           /* HOST array [depth]                             */
+  qvl_merger_weights merger;
+  const qvl_merger_weights* deepstack;       /* HOST array [n_deepstack]                       */
+} qvl_vision_weights;
+
+/* Device metadata of one grid (qvl_vision_metadata / qvl_attention_worklist, copied to the GPU). */
+typedef struct qvl_vision_metadata_dev {
+  int64_t n_tokens;
+  int64_t n_tiles;
+  const int32_t* pos_hw;    /* [n_tokens, 2]  */
+  const int32_t* tap_idx;   /* [4, n_tokens]  */
+  const float* tap_w;       /* [4, n_tokens]  */
+  const int32_t* tiles;     /* [n_tiles, 3]   */
+} qvl_vision_metadata_dev;
+
+int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tokens, size_t* bytes);
+
+/* tokens [n_tokens/4, out_hidden_size] and deepstack[j] [n_tokens/4, out_hidden_size] in dtype
+ * (the VisionEmbeddings pytree, model.py:27-31); `d_deepstack` is a HOST array of n_deepstack
+ * device pointers. pixel_values: [n_tokens, patch_volume] float32 (model.py:556 input). */
+int qvl_encode_vision(void* stream, const qvl_vision_config* cfg, const qvl_vision_weights* weights,
+                      const qvl_vision_metadata_dev* meta, const float* d_pixel_values,
+                      void* d_tokens, void* const* d_deepstack, void* d_workspace,
+                      size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QVL_VISION_H */

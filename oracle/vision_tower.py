@@ -35,13 +35,16 @@ from . import indices as ix
 def bf16_round(x) -> np.ndarray:
     """Round float32 values to the nearest bfloat16 (ties to even); returned as float32."""
     x = np.ascontiguousarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    r = ((u >> 16) & 1) + 0x7FFF
-    out = ((u + r) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    u = x.view(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u                      # uint32 wrap-around only for NaN payloads, restored below
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
     nan = np.isnan(x)
     if nan.any():
-        out = np.where(nan, np.float32(np.nan), out)
-    return out.reshape(x.shape)
+        out[nan] = np.float32(np.nan)
+    return out
 
 
 class _P:
@@ -121,15 +124,16 @@ def attention_varlen(q, k, v, cu_seqlens, p: _P):
         s, e = int(cu[i]), int(cu[i + 1])
         if s >= e:
             continue
-        qw = p.f(q[s:e]).transpose(1, 0, 2)
-        kw = p.f(k[s:e]).transpose(1, 0, 2)
-        vw = p.f(v[s:e]).transpose(1, 0, 2)
+        qw = np.ascontiguousarray(p.f(q[s:e]).transpose(1, 0, 2))
+        kw = np.ascontiguousarray(p.f(k[s:e]).transpose(1, 0, 2))
+        vw = np.ascontiguousarray(p.f(v[s:e]).transpose(1, 0, 2))
         for hh in range(h):
-            sc = (qw[hh] @ kw[hh].T) * scale
-            sc = sc - sc.max(axis=-1, keepdims=True)
-            w = np.exp(sc)
-            w = w / w.sum(axis=-1, keepdims=True)
-            out[s:e, hh] = w @ vw[hh]
+            sc = qw[hh] @ kw[hh].T
+            sc *= scale
+            sc -= sc.max(axis=-1, keepdims=True)
+            np.exp(sc, out=sc)                          # softmax (jax.nn.softmax, model.py:596)
+            sc /= sc.sum(axis=-1, keepdims=True)
+            out[s:e, hh] = sc @ vw[hh]
     return p.r(out)
 
 

@@ -1,0 +1,430 @@
+// Host side of libqvl: error plumbing, integer metadata (bit-exact with the reference's numpy),
+// the C-ABI stage entries and the whole-tower orchestration (Qwen3VisionTransformer.__call__).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "qvl_kernels.h"
+
+namespace qvl {
+
+static thread_local char g_err[512];
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(QVL_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return QVL_OK;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+constexpr int kAttnTileM = 128;   // query tile height of attn_fwd_hd64_kernel
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Float32 value of bf16(x) with round-to-nearest-even (host).
+static float host_round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u) return x;   // inf / nan unchanged
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
+}
+
+}  // namespace qvl
+
+using namespace qvl;
+
+extern "C" {
+
+const char* qvl_last_error(void) { return g_err; }
+
+const char* qvl_status_string(int status) {
+  switch (status) {
+    case QVL_OK: return "ok";
+    case QVL_ERR_INVALID_ARG: return "invalid argument";
+    case QVL_ERR_UNSUPPORTED: return "unsupported";
+    case QVL_ERR_MISALIGNED: return "misaligned";
+    case QVL_ERR_WORKSPACE: return "workspace too small";
+    case QVL_ERR_LAUNCH: return "launch failure";
+  }
+  return "unknown";
+}
+
+int qvl_version(void) { return 1; }
+
+// ---------------------------------------------------------------------------------------------
+// metadata
+// ---------------------------------------------------------------------------------------------
+int qvl_grid_counts(const int32_t* grid, int64_t n_grids, int32_t merge, int64_t* n_tokens, int64_t* n_segments) {
+  if (!grid && n_grids > 0) return set_error(QVL_ERR_INVALID_ARG, "grid_thw is NULL");
+  if (merge <= 0) return set_error(QVL_ERR_INVALID_ARG, "merge=%d", merge);
+  int64_t nt = 0, ns = 0;
+  for (int64_t i = 0; i < n_grids; ++i) {
+    const int64_t t = grid[3 * i], h = grid[3 * i + 1], w = grid[3 * i + 2];
+    if (t <= 0 || h <= 0 || w <= 0)
+      return set_error(QVL_ERR_INVALID_ARG, "grid %lld: non-positive (t,h,w)=(%lld,%lld,%lld)", (long long)i,
+                       (long long)t, (long long)h, (long long)w);
+    if (h % merge || w % merge)
+      return set_error(QVL_ERR_INVALID_ARG, "grid %lld: h=%lld, w=%lld not divisible by merge %d", (long long)i,
+                       (long long)h, (long long)w, merge);
+    nt += t * h * w;
+    ns += t;
+  }
+  if (nt > (int64_t)INT32_MAX) return set_error(QVL_ERR_INVALID_ARG, "too many tokens: %lld", (long long)nt);
+  if (n_tokens) *n_tokens = nt;
+  if (n_segments) *n_segments = ns;
+  return QVL_OK;
+}
+
+// model.py:686-693 (rotary ids), 713-739 + 761-764 (pos-embed taps), 831-834 (cu_seqlens).
+int qvl_vision_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int32_t num_pos, int32_t dtype,
+                        int32_t* cu, int32_t* pos_hw, int32_t* tap_idx, float* tap_w) {
+  int64_t N = 0, S = 0;
+  int rc = qvl_grid_counts(grid, n_grids, merge, &N, &S);
+  if (rc) return rc;
+  const int num_grid = (int)sqrt((double)num_pos);
+  if (num_grid * num_grid != num_pos && (tap_idx || tap_w))
+    return set_error(QVL_ERR_INVALID_ARG, "num_position_embeddings=%d is not a square", num_pos);
+  if (cu) {
+    int64_t s = 0, acc = 0;
+    cu[s++] = 0;
+    for (int64_t i = 0; i < n_grids; ++i)
+      for (int32_t f = 0; f < grid[3 * i]; ++f) {
+        acc += (int64_t)grid[3 * i + 1] * grid[3 * i + 2];
+        cu[s++] = (int32_t)acc;
+      }
+  }
+  const int mm = merge * merge;
+  int64_t off = 0;
+  std::vector<double> hs, ws;
+  std::vector<int32_t> hf, wf;
+  for (int64_t i = 0; i < n_grids; ++i) {
+    const int t = grid[3 * i], h = grid[3 * i + 1], w = grid[3 * i + 2];
+    const int bw = w / merge;
+    // np.linspace(0, num_grid-1, n, dtype=float32): float64 k*step, last = stop, cast to f32.
+    auto linspace = [&](int n, std::vector<double>& val, std::vector<int32_t>& fl) {
+      val.resize(n); fl.resize(n);
+      const double stop = (double)(num_grid - 1);
+      const double step = n > 1 ? stop / (double)(n - 1) : 0.0;
+      for (int k = 0; k < n; ++k) {
+        double y = (n > 1) ? (double)k * step : 0.0;
+        if (n > 1 && k == n - 1) y = stop;
+        const float y32 = (float)y;
+        fl[k] = (int32_t)y32;                 // astype(int32): truncation
+        val[k] = (double)y32 - (double)fl[k]; // f32 - int32 -> float64 (numpy promotion)
+      }
+    };
+    if (tap_idx || tap_w) { linspace(h, hs, hf); linspace(w, ws, wf); }
+    const int64_t hw = (int64_t)h * w;
+    for (int64_t n = 0; n < (int64_t)t * hw; ++n) {
+      const int64_t f = n / hw, r = n % hw, g = r / mm;
+      const int hb = (int)(g / bw), wb = (int)(g % bw);
+      const int mi = (int)((r % mm) / merge), mj = (int)(r % merge);
+      const int row = merge * hb + mi, col = merge * wb + mj;
+      const int64_t tok = off + n;
+      if (pos_hw) { pos_hw[2 * tok] = row; pos_hw[2 * tok + 1] = col; }
+      if (tap_idx || tap_w) {
+        // jnp.repeat(.., t, axis=0) frame expansion: raster row (f*h*w + row*w + col) // t.
+        const int64_t src = (f * hw + (int64_t)row * w + col) / t;
+        const int pr = (int)(src / w), pc = (int)(src % w);
+        const int h0 = hf[pr], w0 = wf[pc];
+        const int h1 = std::min(h0 + 1, num_grid - 1), w1 = std::min(w0 + 1, num_grid - 1);
+        const double dh = hs[pr], dw = ws[pc];
+        if (tap_idx) {
+          tap_idx[0 * N + tok] = h0 * num_grid + w0;
+          tap_idx[1 * N + tok] = h0 * num_grid + w1;
+          tap_idx[2 * N + tok] = h1 * num_grid + w0;
+          tap_idx[3 * N + tok] = h1 * num_grid + w1;
+        }
+        if (tap_w) {
+          const double wv[4] = {(1.0 - dh) * (1.0 - dw), (1.0 - dh) * dw, dh * (1.0 - dw), dh * dw};
+          for (int j = 0; j < 4; ++j) {
+            float v = (float)wv[j];
+            if (dtype == QVL_DTYPE_BF16) v = host_round_bf16(v);
+            tap_w[j * N + tok] = v;
+          }
+        }
+      }
+    }
+    off += (int64_t)t * hw;
+  }
+  return QVL_OK;
+}
+
+int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t* tiles, int64_t capacity, int64_t* n_tiles) {
+  if (!cu || !n_tiles) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens / n_tiles is NULL");
+  std::vector<std::pair<int32_t, int32_t>> segs;
+  for (int64_t i = 0; i < n_seg; ++i) {
+    if (cu[i + 1] < cu[i]) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens not monotone at %lld", (long long)i);
+    if (cu[i + 1] > cu[i]) segs.push_back({cu[i], cu[i + 1]});
+  }
+  std::stable_sort(segs.begin(), segs.end(),
+                   [](const std::pair<int32_t, int32_t>& a, const std::pair<int32_t, int32_t>& b) {
+                     return (a.second - a.first) > (b.second - b.first);
+                   });
+  int64_t n = 0;
+  for (auto& s : segs) n += (s.second - s.first + kAttnTileM - 1) / kAttnTileM;
+  *n_tiles = n;
+  if (!tiles) return QVL_OK;
+  if (capacity < n) return set_error(QVL_ERR_INVALID_ARG, "worklist capacity %lld < %lld", (long long)capacity, (long long)n);
+  int64_t k = 0;
+  for (auto& s : segs)
+    for (int32_t q0 = s.first; q0 < s.second; q0 += kAttnTileM) {
+      tiles[3 * k] = s.first; tiles[3 * k + 1] = s.second; tiles[3 * k + 2] = q0;
+      ++k;
+    }
+  return QVL_OK;
+}
+
+int qvl_rotary_inv_freq(int32_t head_dim, float theta, float* inv) {
+  if (head_dim <= 0 || head_dim % 4 || head_dim > 128 || !inv)
+    return set_error(QVL_ERR_INVALID_ARG, "head_dim=%d", head_dim);
+  const int dim = head_dim / 2;
+  // 1.0 / (theta ** (arange(0, dim, 2, f32) / dim)) (model.py:544): the f32 exponent as the
+  // reference forms it, the power in double, one rounding to f32 (XLA's f32 pow is not
+  // reproducible bit for bit on the host; this is within 1 ulp of it and of numpy's).
+  for (int j = 0; j < head_dim / 4; ++j) {
+    const float e = (float)(2 * j) / (float)dim;
+    inv[j] = (float)(1.0 / pow((double)theta, (double)e));
+  }
+  return QVL_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// device stages
+// ---------------------------------------------------------------------------------------------
+int qvl_pack_dense_weight(void* stream, int32_t dtype, const float* w, int64_t k_in, int64_t n_out, void* out) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "pack: dtype %d", dtype);
+  if (!w || !out || k_in <= 0 || n_out <= 0) return set_error(QVL_ERR_INVALID_ARG, "pack: bad args");
+  return pack_weight_bf16(w, k_in, n_out, (bf16*)out, (hipStream_t)stream);
+}
+
+int qvl_cast(void* stream, int32_t dtype, const float* x, void* y, int64_t n) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "cast: dtype %d", dtype);
+  if (n < 0 || (n > 0 && (!x || !y))) return set_error(QVL_ERR_INVALID_ARG, "cast: bad args");
+  if (!aligned16(x) || !aligned16(y)) return set_error(QVL_ERR_MISALIGNED, "cast: pointers must be 16-byte aligned");
+  return cast_f32_bf16(x, (bf16*)y, n, (hipStream_t)stream);
+}
+
+int qvl_dense(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w, const float* bias,
+              const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense: dtype %d", dtype);
+  if (epi < QVL_EPI_BIAS || epi > QVL_EPI_BIAS_RESIDUAL) return set_error(QVL_ERR_INVALID_ARG, "dense: epilogue %d", epi);
+  if (m < 0 || n <= 0 || k <= 0) return set_error(QVL_ERR_INVALID_ARG, "dense: m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  if (m == 0) return QVL_OK;
+  if (k % 64) return set_error(QVL_ERR_INVALID_ARG, "dense: k=%lld must be a multiple of 64 (pad the weights)", (long long)k);
+  if (n % 4) return set_error(QVL_ERR_INVALID_ARG, "dense: n=%lld must be a multiple of 4", (long long)n);
+  if (!x || !w || !bias || !y || (epi == QVL_EPI_BIAS_RESIDUAL && !res))
+    return set_error(QVL_ERR_INVALID_ARG, "dense: NULL operand");
+  if (lda < k || ldc < n || (epi == QVL_EPI_BIAS_RESIDUAL && ldr < n))
+    return set_error(QVL_ERR_INVALID_ARG, "dense: leading dimension too small");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || lda % 8 || ldc % 4 ||
+      (epi == QVL_EPI_BIAS_RESIDUAL && (((uintptr_t)res & 7) || ldr % 4)))
+    return set_error(QVL_ERR_MISALIGNED, "dense: operands must be 16-byte aligned (lda % 8 == 0, ldc % 4 == 0)");
+  if (m * lda * 2 >= (int64_t)UINT32_MAX || n * k * 2 >= (int64_t)UINT32_MAX)
+    return set_error(QVL_ERR_UNSUPPORTED, "dense: operand larger than 4 GiB");
+  GemmParams p{};
+  p.x = (const bf16*)x; p.lda = lda; p.w = (const bf16*)w; p.bias = bias;
+  p.res = (const bf16*)res; p.ldr = ldr; p.y = (bf16*)y; p.ldc = ldc;
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  return gemm_bf16(p, epi, (hipStream_t)stream);
+}
+
+int qvl_layer_norm(void* stream, int32_t dtype, const void* x, int64_t ldx, const float* g, const float* b, void* y,
+                   int64_t ldy, int64_t rows, int64_t cols, float eps) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "layer_norm: dtype %d", dtype);
+  if (rows < 0 || cols <= 0 || cols % 8 || cols > 8192 || ldx < cols || ldy < cols)
+    return set_error(QVL_ERR_INVALID_ARG, "layer_norm: rows=%lld cols=%lld", (long long)rows, (long long)cols);
+  if (!x || !g || !b || !y) return set_error(QVL_ERR_INVALID_ARG, "layer_norm: NULL operand");
+  if (!aligned16(x) || !aligned16(y) || !aligned16(g) || !aligned16(b) || ldx % 8 || ldy % 8)
+    return set_error(QVL_ERR_MISALIGNED, "layer_norm: operands must be 16-byte aligned");
+  return layer_norm_bf16((const bf16*)x, ldx, g, b, (bf16*)y, ldy, (int)rows, (int)cols, eps, (hipStream_t)stream);
+}
+
+int qvl_pos_embed(void* stream, int32_t dtype, const void* table, const int32_t* idx, const float* w, void* y,
+                  int64_t n_tokens, int64_t dim) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "pos_embed: dtype %d", dtype);
+  if (n_tokens < 0 || dim <= 0 || dim % 8) return set_error(QVL_ERR_INVALID_ARG, "pos_embed: dim=%lld", (long long)dim);
+  if (!table || !idx || !w || !y) return set_error(QVL_ERR_INVALID_ARG, "pos_embed: NULL operand");
+  if (!aligned16(table) || !aligned16(y)) return set_error(QVL_ERR_MISALIGNED, "pos_embed: operands must be 16-byte aligned");
+  return pos_embed_bf16((const bf16*)table, idx, w, (bf16*)y, (int)n_tokens, (int)dim, (hipStream_t)stream);
+}
+
+int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* pos_hw, int64_t n_tokens, int32_t head_dim, float theta,
+                     void* cs) {
+  if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_INVALID_ARG, "rotary: dtype %d", dtype);
+  float inv[32];
+  int rc = qvl_rotary_inv_freq(head_dim, theta, inv);
+  if (rc) return rc;
+  if (n_tokens < 0 || (n_tokens > 0 && (!pos_hw || !cs))) return set_error(QVL_ERR_INVALID_ARG, "rotary: bad args");
+  return rotary_table(pos_hw, (int)n_tokens, head_dim, inv, dtype == QVL_DTYPE_BF16, (f32x2*)cs, (hipStream_t)stream);
+}
+
+static int64_t attn_np(int64_t n) { return round_up(std::max<int64_t>(n, 1), 64); }
+
+int qvl_vision_attention_workspace_size(int64_t n_tokens, int32_t num_heads, int32_t head_dim, size_t* bytes) {
+  if (!bytes || n_tokens < 0 || num_heads <= 0) return set_error(QVL_ERR_INVALID_ARG, "attention ws: bad args");
+  if (head_dim != 64) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (this build: 64)", head_dim);
+  *bytes = (size_t)3 * num_heads * attn_np(n_tokens) * 64 * sizeof(bf16);
+  return QVL_OK;
+}
+
+int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void* k, const void* v, int64_t ld,
+                         const void* cs, const int32_t* tiles, int64_t n_tiles, void* out, int64_t ld_out,
+                         int64_t n_tokens, int32_t H, int32_t hd, void* ws, size_t ws_bytes) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
+  size_t need = 0;
+  int rc = qvl_vision_attention_workspace_size(n_tokens, H, hd, &need);
+  if (rc) return rc;
+  if (ws_bytes < need || !ws) return set_error(QVL_ERR_WORKSPACE, "attention: workspace %zu < %zu", ws_bytes, need);
+  if (n_tokens == 0) return QVL_OK;
+  if (!q || !k || !v || !cs || !out || (n_tiles > 0 && !tiles)) return set_error(QVL_ERR_INVALID_ARG, "attention: NULL operand");
+  if (ld < (int64_t)H * hd || ld_out < (int64_t)H * hd || ld_out % 4)
+    return set_error(QVL_ERR_INVALID_ARG, "attention: leading dimensions");
+  if (((uintptr_t)out & 7) || !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "attention: alignment");
+  const int64_t Np = attn_np(n_tokens);
+  bf16* Qb = (bf16*)ws;
+  bf16* Kb = Qb + (size_t)H * Np * 64;
+  bf16* Vb = Kb + (size_t)H * Np * 64;
+  const float qscale = (1.0f / sqrtf((float)hd)) * kLog2e;
+  rc = attention_relayout_hd64((const bf16*)q, (const bf16*)k, (const bf16*)v, ld, (const f32x2*)cs, (int)n_tokens,
+                               (int)Np, H, qscale, Qb, Kb, Vb, (hipStream_t)stream);
+  if (rc) return rc;
+  return attention_hd64(Qb, Kb, Vb, tiles, n_tiles, (int)Np, H, (bf16*)out, ld_out, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// whole tower
+// ---------------------------------------------------------------------------------------------
+struct TowerLayout {
+  int64_t N, Np, D, I_pad, PV, hd, H;
+  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, total;
+};
+
+static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
+  if (!c) return set_error(QVL_ERR_INVALID_ARG, "config is NULL");
+  if (c->dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: dtype %d", c->dtype);
+  if (c->spatial_merge_size != 2) return set_error(QVL_ERR_UNSUPPORTED, "spatial_merge_size=%d", c->spatial_merge_size);
+  if (c->num_heads <= 0 || c->hidden_size % c->num_heads) return set_error(QVL_ERR_INVALID_ARG, "hidden/heads");
+  const int64_t hd = c->hidden_size / c->num_heads;
+  if (hd != 64) return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: head_dim=%lld (this build: 64)", (long long)hd);
+  if (c->hidden_size % 128 || c->patch_volume % 64 || c->out_hidden_size % 64)
+    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden %% 128, patch_volume %% 64, out %% 64 required");
+  if (c->n_deepstack < 0 || c->n_deepstack > 8) return set_error(QVL_ERR_INVALID_ARG, "n_deepstack=%d", c->n_deepstack);
+  if (N % 4) return set_error(QVL_ERR_INVALID_ARG, "n_tokens=%lld not a multiple of 4", (long long)N);
+  L->N = N; L->Np = attn_np(N); L->D = c->hidden_size; L->I_pad = round_up(c->intermediate_size, 64);
+  L->PV = c->patch_volume; L->hd = hd; L->H = c->num_heads;
+  const int64_t hcols = std::max<int64_t>({L->I_pad, L->PV, (int64_t)c->hidden_size});
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t r = o; o += round_up((int64_t)bytes, 256); return r; };
+  L->off_x = take((size_t)N * L->D * 2);
+  L->off_xn = take((size_t)N * L->D * 2);
+  L->off_q = take((size_t)L->H * L->Np * hd * 2);
+  L->off_k = take((size_t)L->H * L->Np * hd * 2);
+  L->off_vt = take((size_t)L->H * L->Np * hd * 2);
+  L->off_h = take((size_t)N * hcols * 2);
+  L->off_cs = take((size_t)N * (hd / 2) * 8);
+  L->total = o;
+  return QVL_OK;
+}
+
+int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tokens, size_t* bytes) {
+  TowerLayout L;
+  int rc = tower_layout(cfg, n_tokens, &L);
+  if (rc) return rc;
+  if (!bytes) return set_error(QVL_ERR_INVALID_ARG, "bytes is NULL");
+  *bytes = L.total;
+  return QVL_OK;
+}
+
+#define QVL_TRY(expr) do { int _rc = (expr); if (_rc) return _rc; } while (0)
+
+// VisionPatchMerger.__call__ (model.py:648-656): main (LN over D then view [N/4, 4D]) or
+// deepstack (view [N/4, 4D] then LN over 4D); fc1 + GELU-tanh; fc2.
+static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLayout& L, const qvl_merger_weights& mw,
+                      bool postshuffle, const bf16* x, bf16* xn, bf16* h, void* out) {
+  const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
+  if (postshuffle)
+    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
+  else
+    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
+  QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4));
+  QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out, c->out_hidden_size,
+                    N / 4, c->out_hidden_size, D4));
+  return QVL_OK;
+}
+
+int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision_weights* W,
+                      const qvl_vision_metadata_dev* meta, const float* px, void* tokens, void* const* deepstack,
+                      void* ws, size_t ws_bytes) {
+  if (!W || !meta) return set_error(QVL_ERR_INVALID_ARG, "encode_vision: NULL weights/metadata");
+  TowerLayout L;
+  QVL_TRY(tower_layout(c, meta->n_tokens, &L));
+  if (!ws || ws_bytes < L.total) return set_error(QVL_ERR_WORKSPACE, "encode_vision: workspace %zu < %zu", ws_bytes, L.total);
+  if (!aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "encode_vision: workspace alignment");
+  if (L.N == 0) return QVL_OK;
+  if (!px || !tokens || (c->n_deepstack > 0 && !deepstack)) return set_error(QVL_ERR_INVALID_ARG, "encode_vision: NULL io");
+  if (!W->blocks || (c->n_deepstack > 0 && !W->deepstack)) return set_error(QVL_ERR_INVALID_ARG, "encode_vision: NULL weight arrays");
+  hipStream_t st = (hipStream_t)stream;
+  char* base = (char*)ws;
+  bf16* x = (bf16*)(base + L.off_x);
+  bf16* xn = (bf16*)(base + L.off_xn);
+  bf16* Qb = (bf16*)(base + L.off_q);
+  bf16* Kb = (bf16*)(base + L.off_k);
+  bf16* Vb = (bf16*)(base + L.off_vt);
+  bf16* h = (bf16*)(base + L.off_h);
+  f32x2* cs = (f32x2*)(base + L.off_cs);
+  const int64_t N = L.N, D = L.D, I = L.I_pad;
+
+  // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823)
+  QVL_TRY(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
+  QVL_TRY(qvl_rotary_table(st, QVL_DTYPE_BF16, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
+  QVL_TRY(qvl_pos_embed(st, QVL_DTYPE_BF16, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
+  QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV));
+
+  const float qscale = (1.0f / sqrtf((float)L.hd)) * kLog2e;
+  int ds_next = 0;
+  for (int i = 0; i < c->depth; ++i) {
+    const qvl_block_weights& B = W->blocks[i];
+    // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
+    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
+    {
+      GemmParams p{};
+      p.x = xn; p.lda = D; p.w = (const bf16*)B.qkv_w; p.bias = B.qkv_b;
+      p.M = (int)N; p.N = (int)(3 * D); p.K = (int)D;
+      p.q = Qb; p.k = Kb; p.vt = Vb; p.cs = cs; p.Np = (int)L.Np; p.D = (int)D; p.qscale = qscale;
+      QVL_TRY(gemm_bf16(p, kEpiQkvRope, st));
+    }
+    QVL_TRY(attention_hd64(Qb, Kb, Vb, meta->tiles, meta->n_tiles, (int)L.Np, (int)L.H, xn, D, st));
+    QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D));
+    // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
+    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
+    QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D));
+    QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I));
+    // deepstack tap (model.py:841-843)
+    for (int j = 0; j < c->n_deepstack; ++j)
+      if (c->deepstack_indexes[j] == i) {
+        QVL_TRY(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, deepstack[ds_next]));
+        ++ds_next;
+      }
+  }
+  QVL_TRY(run_merger(st, c, L, W->merger, false, x, xn, h, tokens));
+  return QVL_OK;
+}
+
+}  // extern "C"

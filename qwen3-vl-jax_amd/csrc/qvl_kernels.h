@@ -1,0 +1,37 @@
+// Launchers of the gfx950 kernels (each .hip file defines its own), shared with the host entries.
+#pragma once
+#include "qvl_common.h"
+
+namespace qvl {
+
+enum : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiBiasResidual = 2, kEpiQkvRope = 3 };
+
+struct GemmParams {
+  const bf16* x; int64_t lda;
+  const bf16* w;                 // [N, K] (ldw == K)
+  const float* bias;             // [N]
+  const bf16* res; int64_t ldr;  // residual, may alias y
+  bf16* y; int64_t ldc;
+  int M, N, K;
+  // kEpiQkvRope: q/k written [H][Np][64] (rotated; q scaled by qscale), v written [H][64][Np].
+  bf16* q; bf16* k; bf16* vt;
+  const f32x2* cs;               // [M, 32] (cos, sin)
+  int Np, D;
+  float qscale;
+};
+
+int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream);
+int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
+                   int H, bf16* out, int64_t ldo, hipStream_t stream);
+int attention_relayout_hd64(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
+                            int H, float qscale, bf16* Qo, bf16* Ko, bf16* Vto, hipStream_t stream);
+int layer_norm_bf16(const bf16* x, int64_t ldx, const float* g, const float* b, bf16* y, int64_t ldy, int rows,
+                    int cols, float eps, hipStream_t stream);
+int pos_embed_bf16(const bf16* table, const int* idx, const float* wts, bf16* y, int n_tok, int dim,
+                   hipStream_t stream);
+int rotary_table(const int* pos_hw, int n_tok, int head_dim, const float* inv_freq, int round16, f32x2* cs,
+                 hipStream_t stream);
+int cast_f32_bf16(const float* x, bf16* y, int64_t n, hipStream_t stream);
+int pack_weight_bf16(const float* w, int64_t k_in, int64_t n_out, bf16* out, hipStream_t stream);
+
+}  // namespace qvl

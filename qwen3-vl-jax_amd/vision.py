@@ -1,0 +1,476 @@
+"""Host-side mirror of the reference's vision-tower interface, running on libqvl (HIP, gfx950).
+
+Mirrors /root/reference/model.py:
+  VisionEmbeddings              27-64    output pytree (tokens + deepstack), concatenate/cast/with_batch_dim
+  VisionBackboneSpec            84-98    shape/config
+  Qwen3VisionTransformer        659-851  the tower; `__call__(pixel_values, grid_thw) -> (tokens, deepstack)`
+  Qwen3VLModel.encode_vision    940-944  `apply({"params": params}, pixel_values, grid_thw, method="encode_vision")`
+
+Parameters use the reference's Flax tree (`{"visual": {"patch_embed": {"proj": {"kernel", "bias"}}, ...}}`,
+kernels [in, out]); they are packed once onto the device ([out, in] bf16, zero-padded to 64) when
+the tower is bound to them. torch supplies device memory and the stream; every computation is a
+libqvl kernel launched through the C ABI (no torch math on the product path).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Dict, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import capi
+
+
+def _torch():
+    import torch
+    return torch
+
+
+# ---------------------------------------------------------------------------------------------
+# spec (model.py:84-98) and the two BASELINE shapes
+# ---------------------------------------------------------------------------------------------
+@dataclass
+class VisionBackboneSpec:
+    hidden_size: int
+    out_hidden_size: int
+    depth: int
+    num_heads: int
+    intermediate_size: int
+    patch_size: int = 16
+    temporal_patch_size: int = 2
+    spatial_merge_size: int = 2
+    window_size: int = 32
+    in_channels: int = 3
+    fullatt_block_indexes: Sequence[int] = ()
+    num_position_embeddings: Optional[int] = 2304
+    deepstack_visual_indexes: Sequence[int] = ()
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads
+
+    @property
+    def patch_volume(self) -> int:
+        return self.in_channels * self.temporal_patch_size * self.patch_size ** 2
+
+
+def spec_2b() -> VisionBackboneSpec:
+    """Qwen3-VL-2B vision tower shape."""
+    return VisionBackboneSpec(hidden_size=1024, out_hidden_size=2048, depth=24, num_heads=16, intermediate_size=4096,
+                              fullatt_block_indexes=tuple(range(24)), deepstack_visual_indexes=(5, 11, 17))
+
+
+def spec_8b() -> VisionBackboneSpec:
+    """Qwen3-VL-8B vision tower shape."""
+    return VisionBackboneSpec(hidden_size=1152, out_hidden_size=4096, depth=27, num_heads=16, intermediate_size=4304,
+                              fullatt_block_indexes=tuple(range(27)), deepstack_visual_indexes=(8, 16, 24))
+
+
+def random_params(spec: VisionBackboneSpec, seed: int = 0, std: float = 0.02) -> Dict:
+    """Random-init Flax-tree params: Dense kernels and the pos-embed table N(0, std), biases 0,
+    LayerNorm weight 1 / bias 0 (the BASELINE synthetic-weights recipe)."""
+    rng = np.random.default_rng(seed)
+    D, I, Do = spec.hidden_size, spec.intermediate_size, spec.out_hidden_size
+    M4 = D * spec.spatial_merge_size ** 2
+
+    def dense(i, o):
+        return {"kernel": (rng.standard_normal((i, o), dtype=np.float32) * np.float32(std)),
+                "bias": np.zeros(o, np.float32)}
+
+    def ln(d):
+        return {"weight": np.ones(d, np.float32), "bias": np.zeros(d, np.float32)}
+
+    v = {"patch_embed": {"proj": dense(spec.patch_volume, D)},
+         "pos_embed": {"embedding": rng.standard_normal((spec.num_position_embeddings, D), dtype=np.float32) * np.float32(std)}}
+    for i in range(spec.depth):
+        v[f"blocks_{i}"] = {"norm1": ln(D), "norm2": ln(D),
+                            "attn": {"qkv": dense(D, 3 * D), "proj": dense(D, D)},
+                            "mlp": {"linear_fc1": dense(D, I), "linear_fc2": dense(I, D)}}
+    v["merger"] = {"norm": ln(D), "linear_fc1": dense(M4, M4), "linear_fc2": dense(M4, Do)}
+    for j in range(len(spec.deepstack_visual_indexes)):
+        v[f"deepstack_mergers_{j}"] = {"norm": ln(M4), "linear_fc1": dense(M4, M4), "linear_fc2": dense(M4, Do)}
+    return {"visual": v}
+
+
+# ---------------------------------------------------------------------------------------------
+# VisionEmbeddings (model.py:27-64)
+# ---------------------------------------------------------------------------------------------
+@dataclass
+class VisionEmbeddings:
+    """Container for vision tower outputs: tokens [N/4, Dout] + deepstack features."""
+    tokens: "object"
+    deepstack: Tuple = ()
+
+    @classmethod
+    def concatenate(cls, embeds: Sequence["VisionEmbeddings"]) -> "VisionEmbeddings":
+        torch = _torch()
+        if not embeds:
+            return cls(tokens=torch.zeros((0, 0), dtype=torch.float32), deepstack=())
+        base = len(embeds[0].deepstack)
+        for e in embeds[1:]:
+            if len(e.deepstack) != base:
+                raise ValueError("All VisionEmbeddings must have same deepstack length")
+        return cls(tokens=torch.cat([e.tokens for e in embeds], 0),
+                   deepstack=tuple(torch.cat([e.deepstack[i] for e in embeds], 0) for i in range(base)))
+
+    def cast(self, dtype) -> "VisionEmbeddings":
+        return VisionEmbeddings(tokens=self.tokens.to(dtype), deepstack=tuple(f.to(dtype) for f in self.deepstack))
+
+    def with_batch_dim(self, batch: int) -> "VisionEmbeddings":
+        tokens = self.tokens if self.tokens.ndim == 3 else self.tokens[None, ...]
+        if tokens.shape[0] == 1 and batch > 1:
+            tokens = tokens.repeat(batch, 1, 1)
+        ds = []
+        for f in self.deepstack:
+            f = f if f.ndim == 3 else f[None, ...]
+            if f.shape[0] == 1 and batch > 1:
+                f = f.repeat(batch, 1, 1)
+            ds.append(f)
+        return VisionEmbeddings(tokens=tokens, deepstack=tuple(ds))
+
+
+# ---------------------------------------------------------------------------------------------
+# host metadata (C ABI)
+# ---------------------------------------------------------------------------------------------
+def _i32p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+def _f32p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+@dataclass
+class GridMetadata:
+    """Host integer metadata of one grid_thw (qvl_vision_metadata + qvl_attention_worklist)."""
+    n_tokens: int
+    cu_seqlens: np.ndarray
+    pos_hw: np.ndarray
+    tap_idx: np.ndarray
+    tap_w: np.ndarray
+    tiles: np.ndarray
+
+
+def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
+                  dtype: int = capi.QVL_DTYPE_BF16) -> GridMetadata:
+    g = np.ascontiguousarray(np.asarray(grid_thw, dtype=np.int32).reshape(-1, 3))
+    lib = capi.load()
+    nt, ns = C.c_int64(), C.c_int64()
+    capi.check(lib.qvl_grid_counts(_i32p(g), g.shape[0], merge, C.byref(nt), C.byref(ns)), "qvl_grid_counts")
+    N, S = nt.value, ns.value
+    cu = np.zeros(S + 1, np.int32)
+    pos = np.zeros((N, 2), np.int32)
+    idx = np.zeros((4, N), np.int32)
+    w = np.zeros((4, N), np.float32)
+    capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, num_position_embeddings, dtype, _i32p(cu),
+                                       _i32p(pos), _i32p(idx), _f32p(w)), "qvl_vision_metadata")
+    nti = C.c_int64()
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, None, 0, C.byref(nti)), "qvl_attention_worklist")
+    tiles = np.zeros((max(nti.value, 1), 3), np.int32)
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, _i32p(tiles), nti.value, C.byref(nti)),
+               "qvl_attention_worklist")
+    return GridMetadata(N, cu, pos, idx, w, tiles[: nti.value])
+
+
+# ---------------------------------------------------------------------------------------------
+# the tower (model.py:659-851)
+# ---------------------------------------------------------------------------------------------
+def _ptr(t) -> int:
+    return t.data_ptr() if t is not None else 0
+
+
+class Qwen3VisionTransformer:
+    """The vision tower on libqvl. Bind params once (`bind`), then call like the reference module:
+    `tokens, deepstack = tower(pixel_values, grid_thw)`."""
+
+    def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0"):
+        if dtype != "bfloat16":
+            raise NotImplementedError("this build runs the tower in bfloat16 only")
+        if spec.spatial_merge_size != 2:
+            raise NotImplementedError("spatial_merge_size must be 2")
+        self.spec = spec
+        self.dtype = dtype
+        self.qdtype = capi.QVL_DTYPE_BF16
+        self.device = device
+        self._lib = capi.load()
+        self._w = None
+        self._keep = []
+        self._meta_cache: Dict[tuple, tuple] = {}
+        self._ws = None
+        cfg = capi.VisionConfig()
+        cfg.hidden_size = spec.hidden_size
+        cfg.out_hidden_size = spec.out_hidden_size
+        cfg.depth = spec.depth
+        cfg.num_heads = spec.num_heads
+        cfg.intermediate_size = spec.intermediate_size
+        cfg.patch_volume = spec.patch_volume
+        cfg.spatial_merge_size = spec.spatial_merge_size
+        cfg.num_position_embeddings = spec.num_position_embeddings or 0
+        ds = tuple(spec.deepstack_visual_indexes)
+        if len(ds) > 8:
+            raise ValueError("at most 8 deepstack taps")
+        cfg.n_deepstack = len(ds)
+        for j, d in enumerate(ds):
+            cfg.deepstack_indexes[j] = d
+        cfg.ln_eps = 1e-6
+        cfg.rope_theta = 10000.0
+        cfg.dtype = self.qdtype
+        self._cfg = cfg
+
+    # -- weights --------------------------------------------------------------------------------
+    def _stream(self):
+        return _torch().cuda.current_stream().cuda_stream
+
+    def _pack_dense(self, p):
+        torch = _torch()
+        k = np.ascontiguousarray(np.asarray(p["kernel"], np.float32))
+        kin, nout = k.shape
+        kp, npad = -(-kin // 64) * 64, -(-nout // 64) * 64
+        src = torch.from_numpy(k).to(self.device)
+        out = torch.empty((npad, kp), dtype=torch.bfloat16, device=self.device)
+        capi.check(self._lib.qvl_pack_dense_weight(self._stream(), self.qdtype, src.data_ptr(), kin, nout,
+                                                   out.data_ptr()), "qvl_pack_dense_weight")
+        b = np.zeros(npad, np.float32)
+        b[:nout] = np.asarray(p["bias"], np.float32)
+        bias = torch.from_numpy(b).to(self.device).to(torch.bfloat16).to(torch.float32)
+        self._keep += [out, bias]
+        return out, bias
+
+    def _vec(self, v):
+        torch = _torch()
+        t = torch.from_numpy(np.ascontiguousarray(np.asarray(v, np.float32))).to(self.device)
+        t = t.to(torch.bfloat16).to(torch.float32)      # LayerNorm params live in the tower dtype
+        self._keep.append(t)
+        return t
+
+    def bind(self, params: Dict) -> "Qwen3VisionTransformer":
+        """Pack a Flax-tree param dict onto the device (load-time, model.py:1105-1160 layout)."""
+        torch = _torch()
+        v = params.get("visual", params)
+        s = self.spec
+        self._keep = []
+        W = capi.VisionWeights()
+        pw, pb = self._pack_dense(v["patch_embed"]["proj"])
+        W.patch_w, W.patch_b = pw.data_ptr(), pb.data_ptr()
+        tab = torch.from_numpy(np.ascontiguousarray(v["pos_embed"]["embedding"], np.float32)).to(self.device)
+        tab = tab.to(torch.bfloat16).contiguous()
+        self._keep.append(tab)
+        W.pos_table = tab.data_ptr()
+        blocks = (capi.BlockWeights * s.depth)()
+        for i in range(s.depth):
+            b = v[f"blocks_{i}"]
+            bw = blocks[i]
+            bw.norm1_w, bw.norm1_b = self._vec(b["norm1"]["weight"]).data_ptr(), self._vec(b["norm1"]["bias"]).data_ptr()
+            bw.norm2_w, bw.norm2_b = self._vec(b["norm2"]["weight"]).data_ptr(), self._vec(b["norm2"]["bias"]).data_ptr()
+            for name, key in (("qkv", ("attn", "qkv")), ("proj", ("attn", "proj")),
+                              ("fc1", ("mlp", "linear_fc1")), ("fc2", ("mlp", "linear_fc2"))):
+                w, bias = self._pack_dense(b[key[0]][key[1]])
+                setattr(bw, name + "_w", w.data_ptr())
+                setattr(bw, name + "_b", bias.data_ptr())
+        W.blocks = blocks
+
+        def merger(m):
+            mw = capi.MergerWeights()
+            mw.norm_w, mw.norm_b = self._vec(m["norm"]["weight"]).data_ptr(), self._vec(m["norm"]["bias"]).data_ptr()
+            w1, b1 = self._pack_dense(m["linear_fc1"])
+            w2, b2 = self._pack_dense(m["linear_fc2"])
+            mw.fc1_w, mw.fc1_b, mw.fc2_w, mw.fc2_b = w1.data_ptr(), b1.data_ptr(), w2.data_ptr(), b2.data_ptr()
+            return mw
+
+        W.merger = merger(v["merger"])
+        nds = len(s.deepstack_visual_indexes)
+        ds = (capi.MergerWeights * max(nds, 1))()
+        for j in range(nds):
+            ds[j] = merger(v[f"deepstack_mergers_{j}"])
+        W.deepstack = ds
+        self._blocks_arr, self._ds_arr = blocks, ds
+        self._w = W
+        torch.cuda.current_stream().synchronize()
+        return self
+
+    # -- per-grid metadata ----------------------------------------------------------------------
+    def metadata(self, grid_thw):
+        """Device copy of the grid's integer metadata, built once per grid and cached."""
+        torch = _torch()
+        g = np.asarray(grid_thw, dtype=np.int32).reshape(-1, 3)
+        key = tuple(map(tuple, g.tolist()))
+        hit = self._meta_cache.get(key)
+        if hit is not None:
+            return hit
+        m = grid_metadata(g, self.spec.spatial_merge_size, self.spec.num_position_embeddings, self.qdtype)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
+        tens = {"cu_seqlens": dev(m.cu_seqlens), "pos_hw": dev(m.pos_hw), "tap_idx": dev(m.tap_idx),
+                "tap_w": dev(m.tap_w), "tiles": dev(m.tiles if len(m.tiles) else np.zeros((1, 3), np.int32))}
+        md = capi.VisionMetadataDev()
+        md.n_tokens = m.n_tokens
+        md.n_tiles = len(m.tiles)
+        md.pos_hw, md.tap_idx, md.tap_w, md.tiles = (tens["pos_hw"].data_ptr(), tens["tap_idx"].data_ptr(),
+                                                     tens["tap_w"].data_ptr(), tens["tiles"].data_ptr())
+        entry = (m, tens, md)
+        self._meta_cache[key] = entry
+        return entry
+
+    def workspace(self, n_tokens: int):
+        torch = _torch()
+        nb = C.c_size_t()
+        capi.check(self._lib.qvl_encode_vision_workspace_size(C.byref(self._cfg), n_tokens, C.byref(nb)),
+                   "qvl_encode_vision_workspace_size")
+        if self._ws is None or self._ws.numel() < nb.value:
+            self._ws = torch.empty(max(nb.value, 256), dtype=torch.uint8, device=self.device)
+        return self._ws, nb.value
+
+    # -- forward (model.py:801-851) ---------------------------------------------------------------
+    def __call__(self, pixel_values, grid_thw):
+        torch = _torch()
+        if self._w is None:
+            raise RuntimeError("bind(params) first")
+        m, tens, md = self.metadata(grid_thw)
+        N = m.n_tokens
+        px = pixel_values
+        if not isinstance(px, torch.Tensor):
+            px = torch.from_numpy(np.ascontiguousarray(np.asarray(px, np.float32)))
+        px = px.to(device=self.device, dtype=torch.float32).contiguous()
+        if tuple(px.shape) != (N, self.spec.patch_volume):
+            raise ValueError(f"pixel_values shape {tuple(px.shape)} != ({N}, {self.spec.patch_volume})")
+        s = self.spec
+        tokens = torch.empty((N // 4, s.out_hidden_size), dtype=torch.bfloat16, device=self.device)
+        ds = [torch.empty((N // 4, s.out_hidden_size), dtype=torch.bfloat16, device=self.device)
+              for _ in s.deepstack_visual_indexes]
+        ds_ptrs = (C.c_void_p * max(len(ds), 1))(*[t.data_ptr() for t in ds])
+        ws, nbytes = self.workspace(N)
+        capi.check(self._lib.qvl_encode_vision(self._stream(), C.byref(self._cfg), C.byref(self._w), C.byref(md),
+                                               px.data_ptr(), tokens.data_ptr(), ds_ptrs, ws.data_ptr(), nbytes),
+                   "qvl_encode_vision")
+        return tokens, tuple(ds)
+
+
+    # -- staged forward: one C-ABI stage entry per reference op, with per-layer taps -------------
+    def _staged_ctx(self, grid_thw):
+        torch = _torch()
+        m, tens, md = self.metadata(grid_thw)
+        s = self.spec
+        N, D, H, hd = m.n_tokens, s.hidden_size, s.num_heads, s.head_dim
+        I = -(-s.intermediate_size // 64) * 64
+        dev = dict(device=self.device)
+        bf = torch.bfloat16
+        cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, **dev)
+        capi.check(self._lib.qvl_rotary_table(self._stream(), self.qdtype, tens["pos_hw"].data_ptr(), N, hd, 10000.0,
+                                              cs.data_ptr()), "qvl_rotary_table")
+        nb = C.c_size_t()
+        capi.check(self._lib.qvl_vision_attention_workspace_size(N, H, hd, C.byref(nb)), "attention ws")
+        return dict(m=m, tens=tens, md=md, N=N, D=D, H=H, hd=hd, I=I, cs=cs, aws_bytes=nb.value,
+                    aws=torch.empty(max(nb.value, 256), dtype=torch.uint8, **dev),
+                    xn=torch.empty((N, D), dtype=bf, **dev), qkv=torch.empty((N, 3 * D), dtype=bf, **dev),
+                    o=torch.empty((N, D), dtype=bf, **dev), h=torch.empty((N, I), dtype=bf, **dev))
+
+    def block_staged(self, i: int, x, ctx) -> None:
+        """VisionBlock i (model.py:627-630) applied in place to the bf16 residual stream x [N, D],
+        one C-ABI stage entry per reference op (qkv Dense, rotary + varlen attention, proj Dense +
+        residual, LayerNorms, fc1 + GELU, fc2 + residual)."""
+        lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
+        N, D, H, hd, I = ctx["N"], ctx["D"], ctx["H"], ctx["hd"], ctx["I"]
+        xn, qkv, o, h = ctx["xn"], ctx["qkv"], ctx["o"], ctx["h"]
+        B = self._blocks_arr[i]
+        ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS, xn.data_ptr(), D, B.qkv_w, B.qkv_b, None, 0, qkv.data_ptr(),
+                         3 * D, N, 3 * D, D), "qkv")
+        ck(lib.qvl_vision_attention(st, dt, qkv.data_ptr(), qkv.data_ptr() + 2 * D, qkv.data_ptr() + 4 * D, 3 * D,
+                                    ctx["cs"].data_ptr(), ctx["tens"]["tiles"].data_ptr(), ctx["md"].n_tiles,
+                                    o.data_ptr(), D, N, H, hd, ctx["aws"].data_ptr(), ctx["aws_bytes"]), "attention")
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D,
+                         x.data_ptr(), D, N, D, D), "proj")
+        ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm2_w, B.norm2_b, xn.data_ptr(), D, N, D, 1e-6), "ln2")
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_GELU, xn.data_ptr(), D, B.fc1_w, B.fc1_b, None, 0, h.data_ptr(),
+                         I, N, I, D), "fc1")
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D,
+                         x.data_ptr(), D, N, D, I), "fc2")
+
+    def merger_staged(self, x, ctx, which: int = -1):
+        """VisionPatchMerger (model.py:648-656) on the residual stream x: main merger (which=-1) or
+        deepstack merger `which` (postshuffle LayerNorm over 4D)."""
+        torch = _torch()
+        lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
+        N, D = ctx["N"], ctx["D"]
+        s = self.spec
+        D4 = 4 * D
+        mw = self._w.merger if which < 0 else self._ds_arr[which]
+        dev = dict(device=self.device)
+        xm = torch.empty((N // 4, D4), dtype=torch.bfloat16, **dev)
+        if which >= 0:
+            ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D4, mw.norm_w, mw.norm_b, xm.data_ptr(), D4, N // 4, D4,
+                                  1e-6), "merger ln")
+        else:
+            ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, mw.norm_w, mw.norm_b, xm.data_ptr(), D, N, D, 1e-6),
+               "merger ln")
+        hm = torch.empty((N // 4, D4), dtype=torch.bfloat16, **dev)
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_GELU, xm.data_ptr(), D4, mw.fc1_w, mw.fc1_b, None, 0, hm.data_ptr(),
+                         D4, N // 4, D4, D4), "merger fc1")
+        out = torch.empty((N // 4, s.out_hidden_size), dtype=torch.bfloat16, **dev)
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS, hm.data_ptr(), D4, mw.fc2_w, mw.fc2_b, None, 0, out.data_ptr(),
+                         s.out_hidden_size, N // 4, s.out_hidden_size, D4), "merger fc2")
+        return out
+
+    def embed_staged(self, pixel_values, ctx):
+        """Patch embed + learned pos-embed (model.py:802-806) via qvl_cast / qvl_pos_embed / qvl_dense."""
+        torch = _torch()
+        lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
+        N, D = ctx["N"], ctx["D"]
+        s = self.spec
+        px = pixel_values if isinstance(pixel_values, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(np.asarray(pixel_values, np.float32)))
+        px = px.to(device=self.device, dtype=torch.float32).contiguous()
+        W = self._w
+        x16 = torch.empty((N, s.patch_volume), dtype=torch.bfloat16, device=self.device)
+        ck(lib.qvl_cast(st, dt, px.data_ptr(), x16.data_ptr(), px.numel()), "qvl_cast")
+        pos = torch.empty((N, D), dtype=torch.bfloat16, device=self.device)
+        ck(lib.qvl_pos_embed(st, dt, W.pos_table, ctx["tens"]["tap_idx"].data_ptr(), ctx["tens"]["tap_w"].data_ptr(),
+                             pos.data_ptr(), N, D), "qvl_pos_embed")
+        x = torch.empty((N, D), dtype=torch.bfloat16, device=self.device)
+        ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, x16.data_ptr(), s.patch_volume, W.patch_w, W.patch_b,
+                         pos.data_ptr(), D, x.data_ptr(), D, N, D, s.patch_volume), "qvl_dense(patch)")
+        return x
+
+    def forward_staged(self, pixel_values, grid_thw, keep_layers: bool = False):
+        """Same tower, driven stage by stage through the per-op C-ABI entries — the sequence a
+        per-stage FFI registration runs. Returns (tokens, deepstack, layers) where `layers[i]` is
+        the residual stream after block i when keep_layers (model.py:838-843)."""
+        if self._w is None:
+            raise RuntimeError("bind(params) first")
+        ctx = self._staged_ctx(grid_thw)
+        x = self.embed_staged(pixel_values, ctx)
+        layers, feats = [], []
+        taps = tuple(self.spec.deepstack_visual_indexes)
+        for i in range(self.spec.depth):
+            self.block_staged(i, x, ctx)
+            if keep_layers:
+                layers.append(x.clone())
+            if i in taps:
+                feats.append(self.merger_staged(x, ctx, len(feats)))
+        return self.merger_staged(x, ctx), tuple(feats), layers
+
+
+class Qwen3VLModel:
+    """The `encode_vision` entry of the reference model (model.py:940-944)."""
+
+    def __init__(self, vision_spec: Optional[VisionBackboneSpec], dtype: str = "bfloat16", device: str = "cuda:0"):
+        self.vision_spec = vision_spec
+        self.visual = Qwen3VisionTransformer(vision_spec, dtype, device) if vision_spec is not None else None
+        self._bound = None
+
+    def encode_vision(self, pixel_values, grid_thw) -> VisionEmbeddings:
+        if self.visual is None:
+            raise ValueError("Vision backbone not configured")
+        tokens, deepstack = self.visual(pixel_values, grid_thw)
+        return VisionEmbeddings(tokens=tokens, deepstack=deepstack)
+
+    def apply(self, variables: Dict, pixel_values, grid_thw, method="encode_vision") -> VisionEmbeddings:
+        """`model.apply({"params": params}, pixel_values, grid_thw, method=model.encode_vision)`."""
+        if self.visual is None:
+            raise ValueError("Vision backbone not configured")
+        params = variables["params"]
+        if self._bound is not params:
+            self.visual.bind(params)
+            self._bound = params
+        fn = method if callable(method) else getattr(self, method)
+        return fn(pixel_values, grid_thw)

