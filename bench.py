@@ -1,0 +1,153 @@
+#!/usr/bin/env python3
+"""Benchmark: encode_vision patches/s on one MI355X.
+
+Workload (one "step"): the Qwen3-VL-2B vision tower, bf16, on a batch of 8 synthetic 768x768
+images, grid_thw = 8 x (1, 48, 48) -> 18432 patches packed by cu_seqlens, random-init weights
+N(0, 0.02), zero biases, patches N(0, 1); deepstack taps after blocks 5/11/17. Inputs are
+resident in HBM before the timed region; the per-grid integer metadata is built once and cached.
+
+Prints ONE JSON line (rank 0): metric/value/unit, timing, `roofline` for the dominant kernel
+(algorithmic FLOPs per launch / average launch time, timed with HIP events on the launch
+stream) and `cpu_baseline` (the numpy oracle on a bounded sample, same process, host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "vision patches/sec for encode_vision (2B tower, bf16, 1 GPU); % MFMA peak"
+PEAK_BF16_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (AMD published)
+PEAK_HBM_GBS = 8000.0
+
+
+def tower_flops(n_tokens, seg_lens, D=1024, I=4096, depth=24, n_ds=3, Dout=2048, pv=1536):
+    """Algorithmic MFMA FLOPs of one encode_vision (GEMMs + attention QK^T and PV)."""
+    f = n_tokens * 2 * pv * D
+    f += depth * (n_tokens * 2 * (3 * D * D + D * D + 2 * D * I) + sum(4 * L * L * D for L in seg_lens))
+    f += (n_tokens // 4) * (1 + n_ds) * 2 * (4 * D * 4 * D + 4 * D * Dout)
+    return f
+
+
+def cpu_baseline(params, px_one, grid_one, depth=24):
+    """The numpy oracle (fp32, the reference's default dtype) on one image of the workload."""
+    from oracle import vision_tower as vt
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    ospec = vt.VisionSpec(depth=depth)
+    vt.encode_vision(params, px_one[:16], [(1, 4, 4)], vt.VisionSpec(depth=1), "fp32")   # warm
+    t0 = time.perf_counter()
+    vt.encode_vision(params, px_one, grid_one, ospec, "fp32")
+    dt = time.perf_counter() - t0
+    n = px_one.shape[0]
+    return {"value": n / dt, "unit": "patches/s", "cores": int(threads), "kind": "port",
+            "sample": f"1 of the 8 images (grid 1x48x48, {n} patches), full 24-block tower + mergers, "
+                      f"numpy oracle in fp32 (the reference's default dtype), 1 run of {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the tower shards by segment with no communication until a final all-gather, "
+              "which is not part of this single-GPU build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from __graft_entry__ import load_package
+    pkg = load_package()
+    cp = pkg.capi
+    lib = cp.load()
+
+    spec = pkg.spec_2b()
+    grids = np.array([(1, 48, 48)] * 8, np.int32)
+    N = int(grids[:, 0].dot(grids[:, 1] * grids[:, 2]))
+    params = pkg.random_params(spec, seed=0)
+    px_host = np.random.default_rng(1).standard_normal((N, spec.patch_volume), dtype=np.float32)
+    tower = pkg.Qwen3VisionTransformer(spec).bind(params)
+    px = torch.from_numpy(px_host).to("cuda:0")
+    tower.metadata(grids)
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        tower(px, grids)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(args.steps):
+        tower(px, grids)
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    value = N / (ms / 1e3)
+    flops = tower_flops(N, [2304] * 8)
+    step_tflops = flops / (ms / 1e3) / 1e12
+
+    # Dominant kernel: the fc1 GEMM (bias + GELU epilogue), [18432 x 1024] . [1024 x 4096]^T.
+    D, I = spec.hidden_size, spec.intermediate_size
+    xk = torch.randn((N, D), device="cuda:0").to(torch.bfloat16)
+    wk = tower._blocks_arr[0]
+    hk = torch.empty((N, I), dtype=torch.bfloat16, device="cuda:0")
+
+    def fc1():
+        cp.check(lib.qvl_dense(st.cuda_stream, cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, wk.fc1_w,
+                               wk.fc1_b, None, 0, hk.data_ptr(), I, N, I, D), "fc1")
+
+    for _ in range(3):
+        fc1()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record(st)
+    for _ in range(args.kernel_reps):
+        fc1()
+    k1.record(st)
+    torch.cuda.synchronize()
+    k_ms = k0.elapsed_time(k1) / args.kernel_reps
+    k_flops = 2.0 * N * D * I
+    k_tflops = k_flops / (k_ms / 1e3) / 1e12
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "patches/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights N(0,0.02), patches N(0,1))",
+        "config": {"workload": "BASELINE config 2: 2B vision tower, 8 x 768x768 images, grid (1,48,48) each, "
+                               "18432 patches in 8 cu_seqlens segments, deepstack after blocks 5/11/17",
+                   "global_batch": 8, "patches": N, "parallelism": "single GPU"},
+        "mfma_frac_step": round(step_tflops / PEAK_BF16_TFLOPS, 4),
+        "step_tflops": round(step_tflops, 1),
+        "roofline": {"kernel": "gemm_bf16_kernel<256,256,BIAS_GELU> (fc1, 18432x4096x1024)", "bound": "mfma",
+                     "achieved": round(k_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_launch_ms": round(k_ms, 4), "flops_per_launch": k_flops},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu:
+        one = np.array([(1, 48, 48)], np.int32)
+        out["cpu_baseline"] = cpu_baseline(params, px_host[:2304], one)
+        out["gpu_over_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
