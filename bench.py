@@ -105,27 +105,61 @@ def main():
     flops = tower_flops(N, [2304] * 8)
     step_tflops = flops / (ms / 1e3) / 1e12
 
-    # Dominant kernel: the fc1 GEMM (bias + GELU epilogue), [18432 x 1024] . [1024 x 4096]^T.
-    D, I = spec.hidden_size, spec.intermediate_size
-    xk = torch.randn((N, D), device="cuda:0").to(torch.bfloat16)
-    wk = tower._blocks_arr[0]
-    hk = torch.empty((N, I), dtype=torch.bfloat16, device="cuda:0")
-
-    def fc1():
-        cp.check(lib.qvl_dense(st.cuda_stream, cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, wk.fc1_w,
-                               wk.fc1_b, None, 0, hk.data_ptr(), I, N, I, D), "fc1")
-
-    for _ in range(3):
-        fc1()
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(st)
-    for _ in range(args.kernel_reps):
-        fc1()
-    k1.record(st)
-    torch.cuda.synchronize()
-    k_ms = k0.elapsed_time(k1) / args.kernel_reps
-    k_flops = 2.0 * N * D * I
-    k_tflops = k_flops / (k_ms / 1e3) / 1e12
+    # Per-kernel timing (HIP events on the launch stream, over `kernel_reps` back-to-back
+    # launches of each kernel class at the workload's shapes, inputs resident in HBM).
+    D, I, H = spec.hidden_size, spec.intermediate_size, spec.num_heads
+    m, tens, md = tower.metadata(grids)
+    blk = tower._blocks_arr[0]
+    dev = "cuda:0"
+    xk = torch.randn((N, D), device=dev).to(torch.bfloat16)
+    hk = torch.randn((N, I), device=dev).to(torch.bfloat16)
+    yk = torch.empty((N, D), dtype=torch.bfloat16, device=dev)
+    hout = torch.empty((N, I), dtype=torch.bfloat16, device=dev)
+    Np = -(-N // 64) * 64
+    qb = torch.empty((H, Np, 64), dtype=torch.bfloat16, device=dev)
+    kb, vb = torch.empty_like(qb), torch.empty_like(qb)
+    cs = torch.empty((N, 32, 2), dtype=torch.float32, device=dev)
+    cp.check(lib.qvl_rotary_table(st.cuda_stream, cp.QVL_DTYPE_BF16, tens["pos_hw"].data_ptr(), N, 64, 10000.0,
+                                  cs.data_ptr()), "rotary")
+    s_ = st.cuda_stream
+    BF = cp.QVL_DTYPE_BF16
+    seg = [2304] * 8
+    kernels = {
+        # name: (callable, algorithmic FLOPs per launch, launches per step)
+        "fc1 (gemm 256x256, bias+GELU) 18432x4096x1024": (
+            lambda: lib.qvl_dense(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
+                                  hout.data_ptr(), I, N, I, D), 2.0 * N * D * I, spec.depth),
+        "fc2 (gemm 256x128, bias+residual) 18432x1024x4096": (
+            lambda: lib.qvl_dense(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), I, blk.fc2_w, blk.fc2_b,
+                                  yk.data_ptr(), D, yk.data_ptr(), D, N, D, I), 2.0 * N * I * D, spec.depth),
+        "proj (gemm 256x128, bias+residual) 18432x1024x1024": (
+            lambda: lib.qvl_dense(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, xk.data_ptr(), D, blk.proj_w, blk.proj_b,
+                                  yk.data_ptr(), D, yk.data_ptr(), D, N, D, D), 2.0 * N * D * D, spec.depth),
+        "qkv+rotary (gemm 256x256) 18432x3072x1024": (
+            lambda: lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(),
+                                             qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H),
+            2.0 * N * D * 3 * D, spec.depth),
+        "attention (varlen, 8 x 2304 tokens, 16x64)": (
+            lambda: lib.qvl_attention_headmajor(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
+                                                tens["tiles"].data_ptr(), md.n_tiles, N, H, 64, yk.data_ptr(), D),
+            float(sum(4 * L * L * D for L in seg)), spec.depth),
+    }
+    kstats = {}
+    for name, (fn, fl, per_step) in kernels.items():
+        for _ in range(3):
+            cp.check(fn(), name)
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        k0.record(st)
+        for _ in range(args.kernel_reps):
+            fn()
+        k1.record(st)
+        torch.cuda.synchronize()
+        k_ms = k0.elapsed_time(k1) / args.kernel_reps
+        kstats[name] = {"avg_launch_ms": round(k_ms, 4), "tflops": round(fl / (k_ms / 1e3) / 1e12, 1),
+                        "frac_mfma_peak": round(fl / (k_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                        "ms_per_step": round(k_ms * per_step, 3), "flops_per_launch": fl}
+    dom = max(kstats, key=lambda k: kstats[k]["ms_per_step"])
+    dk = kstats[dom]
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "patches/s", "n_gpus": 1, "steps": args.steps,
@@ -136,10 +170,10 @@ def main():
                    "global_batch": 8, "patches": N, "parallelism": "single GPU"},
         "mfma_frac_step": round(step_tflops / PEAK_BF16_TFLOPS, 4),
         "step_tflops": round(step_tflops, 1),
-        "roofline": {"kernel": "gemm_bf16_kernel<256,256,BIAS_GELU> (fc1, 18432x4096x1024)", "bound": "mfma",
-                     "achieved": round(k_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "avg_launch_ms": round(k_ms, 4), "flops_per_launch": k_flops},
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": dk["tflops"], "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": dk["frac_mfma_peak"], "traffic": None,
+                     "avg_launch_ms": dk["avg_launch_ms"], "flops_per_launch": dk["flops_per_launch"]},
+        "kernels": kstats,
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_cpu:

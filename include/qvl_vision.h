@@ -130,6 +130,21 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const voi
                          int64_t n_tokens, int32_t num_heads, int32_t head_dim,
                          void* d_workspace, size_t workspace_bytes);
 
+/* Fused qkv Dense + rotary (model.py:570-582): one GEMM x[N, D] . Wqkv[3D, D]^T + b whose
+ * epilogue applies the 2D rotary to q and k with `d_cos_sin` and writes the head-major operands
+ * of qvl_attention_headmajor: q (scaled by head_dim^-0.5 * log2(e)) and k as [H][Np][64],
+ * v transposed as [H][64][Np], Np = n_tokens rounded up to 64 (rows [n_tokens, Np) zeroed).
+ * head_dim must be 64 and D a multiple of 128. */
+int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
+                         const float* d_bias, const void* d_cos_sin, void* d_q, void* d_k, void* d_vt,
+                         int64_t n_tokens, int64_t hidden, int32_t num_heads);
+
+/* The varlen attention kernel alone, on the head-major operands qvl_dense_qkv_rotary writes
+ * (model.py:585-600): out[n, h*64 + d] for every n inside a segment of `d_tiles`. */
+int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const void* d_k, const void* d_vt,
+                            const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,
+                            int32_t head_dim, void* d_out, int64_t ld_out);
+
 /* ------------------------------------------------------------------------------------------ */
 /* Whole tower: Qwen3VisionTransformer.__call__ (model.py:801-851) / encode_vision (940-944).   */
 /* ------------------------------------------------------------------------------------------ */

@@ -70,6 +70,8 @@ SIGNATURES = {
     "qvl_vision_attention_workspace_size": (C.c_int, [_i64, _i32, _i32, C.POINTER(_sz)]),
     "qvl_vision_attention": (C.c_int, [_p, _i32, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _i32,
                                        _p, _sz]),
+    "qvl_dense_qkv_rotary": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32]),
+    "qvl_attention_headmajor": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _p, _i64]),
     "qvl_encode_vision_workspace_size": (C.c_int, [C.POINTER(VisionConfig), _i64, C.POINTER(_sz)]),
     "qvl_encode_vision": (C.c_int, [_p, C.POINTER(VisionConfig), C.POINTER(VisionWeights),
                                     C.POINTER(VisionMetadataDev), _p, _p, C.POINTER(_p), _p, _sz]),

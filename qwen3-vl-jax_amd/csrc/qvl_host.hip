@@ -308,6 +308,40 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void*
   return attention_hd64(Qb, Kb, Vb, tiles, n_tiles, (int)Np, H, (bf16*)out, ld_out, (hipStream_t)stream);
 }
 
+int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
+                         const void* cs, void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: dtype %d", dtype);
+  if (H <= 0 || hidden != (int64_t)H * 64) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64");
+  if (hidden % 128) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: hidden %% 128 != 0");
+  if (n_tokens < 0 || lda < hidden || lda % 8) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: n_tokens / lda");
+  if (n_tokens == 0) return QVL_OK;
+  if (!x || !w || !bias || !cs || !q || !k || !vt) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(q) || !aligned16(k) || !aligned16(vt) || ((uintptr_t)cs & 7))
+    return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: alignment");
+  if (n_tokens * lda * 2 >= (int64_t)UINT32_MAX) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: operand > 4 GiB");
+  GemmParams p{};
+  p.x = (const bf16*)x; p.lda = lda; p.w = (const bf16*)w; p.bias = bias;
+  p.M = (int)n_tokens; p.N = (int)(3 * hidden); p.K = (int)hidden;
+  p.q = (bf16*)q; p.k = (bf16*)k; p.vt = (bf16*)vt; p.cs = (const f32x2*)cs;
+  p.Np = (int)attn_np(n_tokens); p.D = (int)hidden;
+  p.qscale = (1.0f / sqrtf(64.0f)) * kLog2e;
+  return gemm_bf16(p, kEpiQkvRope, (hipStream_t)stream);
+}
+
+int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
+                            const int32_t* tiles, int64_t n_tiles, int64_t n_tokens, int32_t H, int32_t hd, void* out,
+                            int64_t ld_out) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
+  if (hd != 64) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (this build: 64)", hd);
+  if (n_tokens < 0 || H <= 0 || n_tiles < 0 || ld_out < (int64_t)H * hd || ld_out % 4)
+    return set_error(QVL_ERR_INVALID_ARG, "attention: bad sizes");
+  if (n_tokens == 0 || n_tiles == 0) return QVL_OK;
+  if (!q || !k || !vt || !tiles || !out) return set_error(QVL_ERR_INVALID_ARG, "attention: NULL operand");
+  if ((uintptr_t)out & 7) return set_error(QVL_ERR_MISALIGNED, "attention: out alignment");
+  return attention_hd64((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, (int)attn_np(n_tokens), H,
+                        (bf16*)out, ld_out, (hipStream_t)stream);
+}
+
 // ---------------------------------------------------------------------------------------------
 // whole tower
 // ---------------------------------------------------------------------------------------------
@@ -397,20 +431,13 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   QVL_TRY(qvl_pos_embed(st, QVL_DTYPE_BF16, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
   QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV));
 
-  const float qscale = (1.0f / sqrtf((float)L.hd)) * kLog2e;
   int ds_next = 0;
   for (int i = 0; i < c->depth; ++i) {
     const qvl_block_weights& B = W->blocks[i];
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
     QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
-    {
-      GemmParams p{};
-      p.x = xn; p.lda = D; p.w = (const bf16*)B.qkv_w; p.bias = B.qkv_b;
-      p.M = (int)N; p.N = (int)(3 * D); p.K = (int)D;
-      p.q = Qb; p.k = Kb; p.vt = Vb; p.cs = cs; p.Np = (int)L.Np; p.D = (int)D; p.qscale = qscale;
-      QVL_TRY(gemm_bf16(p, kEpiQkvRope, st));
-    }
-    QVL_TRY(attention_hd64(Qb, Kb, Vb, meta->tiles, meta->n_tiles, (int)L.Np, (int)L.H, xn, D, st));
+    QVL_TRY(qvl_dense_qkv_rotary(st, QVL_DTYPE_BF16, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H));
+    QVL_TRY(qvl_attention_headmajor(st, QVL_DTYPE_BF16, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H, 64, xn, D));
     QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
     QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
