@@ -1,24 +1,29 @@
 // Packed varlen (cu_seqlens) vision attention for gfx950: block-diagonal, non-causal softmax
 // attention per segment (model.py:585-600), bf16 MFMA with fp32 online softmax.
 //
-// Operand layouts (produced by the qkv GEMM's rotary epilogue or by `attn_relayout_kernel`):
+// Operand layouts (produced by the qkv GEMM's rotary epilogue or by `attn_relayout_hd64_kernel`):
 //   Q [H][Np][64]  rotated, pre-multiplied by head_dim^-0.5 * log2(e)  (scores land in log2 units)
 //   K [H][Np][64]  rotated
-//   Vt[H][64][Np]  V transposed (token axis contiguous)
-// Rows [n_tokens, Np) are zero.
+//   Vt[H][64][Np]  V transposed, token axis contiguous, keys at positions vt_pos(key)
+// Rows / positions [n_tokens, Np) are zero.
 //
 // Each workgroup (4 waves) owns one 128-query tile of one segment and one head; each wave owns
-// 32 queries. The kernel computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a lane holds one
-// query and 16 keys of a 32-key block: the softmax row statistics are in-register except for one
-// exchange with the partner lane (lane ^ 32). The MFMA's C operand is preloaded with -m (the
-// running row max), so the accumulator already holds s - m and p = exp2(acc) costs one
-// instruction per score. The running max is only raised when a tile's partial row sum shows
-// growth beyond 2^64 (or on the first tile): exp2 of a stale max stays finite and the result is
-// unchanged because softmax is shift-invariant; every raise rescales O and l exactly.
-// P (bf16) is then the B operand of O^T += V^T P^T as it sits in registers; the V^T tile is
-// staged in LDS with the matching key permutation (middle 4-key quads of each 16-key group
-// swapped) so each lane reads its 8 keys as one 16-byte chunk.
+// 32 queries. Key tiles of 64 start at the segment start rounded down to 64, so every K / V^T
+// tile is 64-aligned and arrives by LDS DMA (16-byte chunks, XOR swizzle folded into the
+// source address); only the first and last tiles carry keys outside the segment and they are
+// peeled off the steady-state loop, which has no masking.
+//
+// S^T = K Q^T via v_mfma_f32_32x32x16_bf16: a lane holds one query and 16 keys of a 32-key block,
+// so softmax statistics are in-register plus one exchange with lane^32. The MFMA's C operand is
+// preloaded with -m (the running row max), the accumulator already holds s - m, and p = exp2(acc)
+// costs one instruction per score. The max is only raised on the first tile, or when a tile's
+// partial row sum exceeds 2^64 (softmax is shift-invariant; each raise rescales O and l exactly).
+// P is rounded to bf16 pairs for the PV MFMA (its B operand, straight from registers) and the row
+// sum is taken over those same bf16 values with v_dot2_f32_bf16, so the normalisation matches
+// the weights the MFMA applied. V^T's quad-swapped key layout makes each lane's 8 PV keys one
+// 16-byte LDS chunk.
 #include <math.h>
+#include <type_traits>
 #include "qvl_kernels.h"
 
 namespace qvl {
@@ -27,27 +32,33 @@ constexpr int kAttnBM = 128;   // queries per workgroup
 constexpr int kAttnBN = 64;    // keys per K/V tile
 constexpr int kHD = 64;
 
-__device__ __forceinline__ int k_off(int row, int chunk) { return row * kHD + ((chunk ^ (row & 7)) << 3); }
-__device__ __forceinline__ int v_off(int d, int chunk) { return d * kAttnBN + ((chunk ^ (d & 7)) << 3); }
+// LDS offsets of (row, 16-byte chunk) in the 128-byte-row K and V^T tiles. The 16-byte chunk is
+// XOR-swizzled with (row/2) % 8: a 16-byte LDS read serves 16 lanes per clock over 64 banks (two
+// rows' worth), and the 16 rows one such read touches land in 16 distinct bank groups.
+__device__ __forceinline__ int k_off(int row, int chunk) { return row * kHD + ((chunk ^ ((row >> 1) & 7)) << 3); }
+__device__ __forceinline__ int v_off(int d, int chunk) { return d * kAttnBN + ((chunk ^ ((d >> 1) & 7)) << 3); }
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_ones(uint32_t packed, float acc) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), one, acc, false);
+}
 
 __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
     const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo) {
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][kAttnBN * kHD];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][kHD * kAttnBN];
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * kAttnBN * kHD];   // [stage][K | V^T][64][64]
 
   const int tile = blockIdx.x, head = blockIdx.y;
   const int seg_s = tiles[3 * tile], seg_e = tiles[3 * tile + 1], q0 = tiles[3 * tile + 2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
 
   const size_t head_elems = (size_t)Np * kHD;
   const bf16* Qh = Q + head * head_elems;
-  const bf16* Kh = K + head * head_elems;
-  const bf16* Vh = Vt + head * head_elems;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(Qh, (uint32_t)(head_elems * 2));
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kh, (uint32_t)(head_elems * 2));
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vh, (uint32_t)(head_elems * 2));
 
   // Q fragments (B operand of S^T = K Q^T): query row qrow, dims [16ks + 8hh, +8).
   const int qrow = q0 + wave * 32 + l32;
@@ -56,31 +67,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
   for (int ks = 0; ks < 4; ++ks)
     qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * kHD + ks * 16 + hh * 8) * 2)));
 
-  // K/V staging: 4 chunks of 16 bytes per thread per tile (2 of K, 2 of V^T).
-  u32x4 stg[4];
-  auto load_tile = [&](int kb) {
+  // K / V^T tile DMA: each wave fills rows [8w, 8w+8) and [32 + 8w, 32 + 8w + 8) of both tiles
+  // (1 KB per instruction). Lane j lands in row r = R0 + j/8 at physical chunk j%8 and fetches the
+  // logical chunk the read swizzle maps there; (r/2)%8 does not depend on the 32-row half.
+  const int drow = wave * 8 + (lane >> 3);
+  const int lch = (lane & 7) ^ ((drow >> 1) & 7);
+  const u32x4 rk = rsrc_words(K + head * head_elems, (uint32_t)(head_elems * 2));
+  const u32x4 rv = rsrc_words(Vt + head * head_elems, (uint32_t)(head_elems * 2));
+  const uint32_t kv_lane = (uint32_t)((drow * kHD + lch * 8) * 2);
+  const uint32_t vv_lane = (uint32_t)(((int64_t)drow * Np + lch * 8) * 2);
+  const uint32_t lds0 = lds_addr_of(smem);
+  constexpr uint32_t kStageBytes = 2 * kAttnBN * kHD * 2;
+  auto dma_tile = [&](int kb, int stage) {
+    const uint32_t kl = lds0 + stage * kStageBytes, vl = kl + kAttnBN * kHD * 2;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int c = i * 256 + tid;
-      const int row = c >> 3, ch = c & 7;
-      stg[i] = buf_load16(rk, (uint32_t)(((int64_t)(kb + row) * kHD + ch * 8) * 2));
-      stg[2 + i] = buf_load16(rv, (uint32_t)(((int64_t)row * Np + kb + ch * 8) * 2));
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = i * 256 + tid;
-      const int row = c >> 3, ch = c & 7;
-      *reinterpret_cast<u32x4*>(&sK[buf][k_off(row, ch)]) = stg[i];
-      // V^T row `row` (= d), keys [8ch, 8ch+8): quads go to positions that make each lane's
-      // 8 PV keys contiguous. Group g = ch/2; even ch: keys 16g+0..3 -> 16g+0..3,
-      // 16g+4..7 -> 16g+8..11; odd ch: 16g+8..11 -> 16g+4..7, 16g+12..15 -> 16g+12..15.
-      const int g = ch >> 1, odd = ch & 1;
-      const u32x4 v = stg[2 + i];
-      bf16* base = &sV[buf][0];
-      *reinterpret_cast<u32x2*>(base + v_off(row, 2 * g) + 4 * odd) = u32x2{v.x, v.y};
-      *reinterpret_cast<u32x2*>(base + v_off(row, 2 * g + 1) + 4 * odd) = u32x2{v.z, v.w};
+      dma16(rk, kv_lane, (uint32_t)((kb + 32 * i) * kHD * 2), kl + (32 * i + wave * 8) * kHD * 2);
+      dma16(rv, vv_lane, (uint32_t)(((int64_t)32 * i * Np + kb) * 2), vl + (32 * i + wave * 8) * kAttnBN * 2);
     }
   };
 
@@ -88,73 +91,85 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
   float m_run = 0.f, l_run = 0.f;
   f32x16 negm = f32x16{};
 
-  const int n_kt = (seg_e - seg_s + kAttnBN - 1) / kAttnBN;
-  load_tile(seg_s);
-  store_tile(0);
+  const int k_begin = seg_s & ~(kAttnBN - 1);
+  const int n_kt = (seg_e - k_begin + kAttnBN - 1) / kAttnBN;
+  dma_tile(k_begin, 0);
+  wait_dma();
   __syncthreads();
 
-  for (int it = 0; it < n_kt; ++it) {
+  // One key tile. EDGE: the first or last tile (mask keys outside [seg_s, seg_e); the first tile
+  // sets the running max exactly).
+  auto step = [&](auto edge_tag, int it) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
     const int cur = it & 1;
-    const int kb = seg_s + it * kAttnBN;
-    if (it + 1 < n_kt) load_tile(kb + kAttnBN);
+    const int kb = k_begin + it * kAttnBN;
+    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
+    const bf16* sK = smem + cur * (2 * kAttnBN * kHD);
+    const bf16* sV = sK + kAttnBN * kHD;
+    const bool first = EDGE && it == 0;
 
-    // S^T blocks: keys [32b, 32b+32) of this tile, C = -m.
+    // S^T blocks: keys [32b, 32b+32) of this tile, accumulated onto C = -m.
     f32x16 s[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      s[b] = negm;
+      s[b] = first ? f32x16{} : negm;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[cur][k_off(b * 32 + l32, ks * 2 + hh)]);
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k_off(b * 32 + l32, ks * 2 + hh)]);
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
       }
     }
-    // Mask keys past the segment end (last tile only).
-    if (kb + kAttnBN > seg_e) {
+    if constexpr (EDGE) {
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key >= seg_e) s[b][r] = -INFINITY;
+          if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
         }
     }
-    float p[2][16];
-    float ts = 0.f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[b][r] = __builtin_amdgcn_exp2f(s[b][r]);
-        ts += p[b][r];
-      }
-    // Raise the running max on the first tile, or when this tile's partial sum got large
-    // (covers +inf and NaN-free overflow); wave-uniform branch.
-    const bool need = (it == 0) || !(ts <= 0x1p64f);
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    float shift = 0.f;
+    if (first) {
       float mx = -INFINITY;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // s already holds (score - m); raise m by `shift` (first tile: to the tile max).
-      const float shift = (it == 0) ? mx : fmaxf(mx, 0.f);
-      m_run += shift;
-      ts = 0.f;
+      shift = fmaxf(mx, __shfl_xor(mx, 32));
+    }
+    // p = exp2(s - shift) as bf16 pairs; partial row sum over the rounded values.
+    uint32_t pk[2][8];
+    float ts = 0.f, ts2 = 0.f;
+    auto exp_pack = [&](float sh) {
+      ts = 0.f; ts2 = 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          p[b][r] = __builtin_amdgcn_exp2f(s[b][r] - shift);
-          ts += p[b][r];
+        for (int j = 0; j < 8; ++j) {
+          pk[b][j] = pack_bf16x2(__builtin_amdgcn_exp2f(s[b][2 * j] - sh), __builtin_amdgcn_exp2f(s[b][2 * j + 1] - sh));
+          if (j & 1) ts2 = dot2_ones(pk[b][j], ts2); else ts = dot2_ones(pk[b][j], ts);
         }
-      if (it > 0) {   // O and l are still zero on the first tile
-        const float alpha = __builtin_amdgcn_exp2f(-shift);
-        l_run *= alpha;
+      ts += ts2;
+    };
+    exp_pack(shift);
+    if (first) {
+      m_run = shift;
+    } else if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
+      // Some row of this tile outgrew the stale max: raise it (s holds score - m).
+      float mx = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
-      }
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+      const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
+      exp_pack(sh);
+      const float alpha = __builtin_amdgcn_exp2f(-sh);
+      m_run += sh;
+      l_run *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
+    }
+    if (first || !EDGE) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) negm[r] = -m_run;
     }
@@ -165,22 +180,22 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e2 = 0; e2 < 2; ++e2) {
-        uint32_t w0 = pack_bf16x2(p[b][8 * e2 + 0], p[b][8 * e2 + 1]);
-        uint32_t w1 = pack_bf16x2(p[b][8 * e2 + 2], p[b][8 * e2 + 3]);
-        uint32_t w2 = pack_bf16x2(p[b][8 * e2 + 4], p[b][8 * e2 + 5]);
-        uint32_t w3 = pack_bf16x2(p[b][8 * e2 + 6], p[b][8 * e2 + 7]);
-        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{w0, w1, w2, w3});
+        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[b][4 * e2], pk[b][4 * e2 + 1], pk[b][4 * e2 + 2],
+                                                           pk[b][4 * e2 + 3]});
         const int g = 2 * b + e2;   // 16-key group within the tile
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[cur][v_off(db * 32 + l32, 2 * g + hh)]);
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * g + hh)]);
           oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
         }
       }
-
-    if (it + 1 < n_kt) store_tile(cur ^ 1);
+    wait_dma();
     __syncthreads();
-  }
+  };
+
+  step(std::true_type{}, 0);
+  for (int it = 1; it + 1 < n_kt; ++it) step(std::false_type{}, it);
+  if (n_kt > 1) step(std::true_type{}, n_kt - 1);
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l_tot;
@@ -199,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
 }
 
 // Relayout for the standalone attention entry: q/k/v [N, H*hd] (row stride ld) -> rotated,
-// scaled Q / rotated K [H][Np][64] and V^T [H][64][Np]; rows [N, Np) zero-filled.
+// scaled Q / rotated K [H][Np][64] and V^T [H][64][Np] (keys at vt_pos); rows [N, Np) zero-filled.
 // One workgroup = 64 tokens of one head.
 __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t ld,
@@ -232,7 +247,7 @@ __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
   __syncthreads();
   for (int idx = tid; idx < 64 * kHD; idx += 256) {
     const int d = idx / 64, t = idx % 64, n = n0 + t;
-    if (n < Np) Vto[((int64_t)head * kHD + d) * Np + n] = tv[t][d];
+    if (n < Np) Vto[((int64_t)head * kHD + d) * Np + vt_pos(n)] = tv[t][d];
   }
 }
 

@@ -40,24 +40,6 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
-// Raw buffer resource words (base, stride 0, byte range, gfx9 word 3) for the asm DMA below.
-__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, (uint32_t)kBufferRsrcWord3};
-}
-
-// 16 bytes per lane, global -> LDS: lane i writes LDS bytes [M0 + 16 i, M0 + 16 i + 16), M0 = lds.
-__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(rsrc), "s"(soff), "s"(lds) : "memory", "m0");
-}
-
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
   using S = GemmShape<BM, BN, WM, WN>;
@@ -187,11 +169,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
             hi[e] = live ? acc[2 * hp + 1][b][4 * g + e] + p.bias[n + 32] : 0.f;
           }
           if (which == 2) {
-            bf16* vt = p.vt + (int64_t)head * 64 * p.Np;
+            bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              vt[(int64_t)(d + e) * p.Np + m] = (bf16)lo[e];
-              vt[(int64_t)(d + e + 32) * p.Np + m] = (bf16)hi[e];
+              vt[(int64_t)(d + e) * p.Np] = (bf16)lo[e];
+              vt[(int64_t)(d + e + 32) * p.Np] = (bf16)hi[e];
             }
           } else {
             float o1[4], o2[4];

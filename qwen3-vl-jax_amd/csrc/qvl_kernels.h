@@ -20,6 +20,15 @@ struct GemmParams {
   float qscale;
 };
 
+// Position of key m in the V^T layout the attention kernel reads: within each 16-key group
+// (aligned to 16 in the token index) the middle two 4-key quads are swapped, so that the 8 keys a
+// lane needs as the PV MFMA's k-slots are one contiguous 16-byte chunk.
+__host__ __device__ __forceinline__ int vt_pos(int m) {
+  const int q = (m >> 2) & 3;
+  const int qs = (q == 1) ? 2 : (q == 2 ? 1 : q);
+  return (m & ~15) | (qs << 2) | (m & 3);
+}
+
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream);
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
                    int H, bf16* out, int64_t ldo, hipStream_t stream);
