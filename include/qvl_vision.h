@@ -139,8 +139,10 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t l
                          const float* d_bias, const void* d_cos_sin, void* d_q, void* d_k, void* d_vt,
                          int64_t n_tokens, int64_t hidden, int32_t num_heads);
 
-/* The varlen attention kernel alone, on the head-major operands qvl_dense_qkv_rotary writes
- * (model.py:585-600): out[n, h*64 + d] for every n inside a segment of `d_tiles`. */
+/* The varlen attention kernel alone, on head-major operands (model.py:585-600):
+ * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
+ * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][80] (dims 72..79 zero) and
+ * v^T [H][96][Np] (rows 72..95 zero), keys at the same quad-swapped positions. */
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const void* d_k, const void* d_vt,
                             const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,
                             int32_t head_dim, void* d_out, int64_t ld_out);

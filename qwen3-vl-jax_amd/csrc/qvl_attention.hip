@@ -213,6 +213,257 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// General head_dim (72 for the 8B tower): Q/K [H][Np][HDP] with dims [hd, HDP) zero, V^T
+// [H][32*NDB][Np] with rows [hd, 32*NDB) zero (keys at vt_pos). Same softmax pipeline as the hd-64
+// kernel; K / V^T tiles are staged through registers into LDS rows padded to an odd number of
+// 16-byte chunks (HDP + 8 and 64 + 8 elements), which keeps the 16-row fragment reads on 16
+// distinct bank groups without a swizzle.
+// ---------------------------------------------------------------------------------------------
+template <int HDP, int NDB>
+__global__ __launch_bounds__(256, 2) void attn_fwd_general_kernel(
+    const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
+    const int* __restrict__ tiles, int Np, int H, int hd, bf16* __restrict__ O, int64_t ldo) {
+  constexpr int KS = HDP / 16;                 // QK k-steps
+  constexpr int KLD = HDP + 8;                 // LDS row stride of the K tile (elements)
+  constexpr int VLD = kAttnBN + 8;             // LDS row stride of the V^T tile
+  constexpr int VROWS = 32 * NDB;
+  constexpr int KCH = kAttnBN * HDP / 8;       // 16-byte chunks per K tile
+  constexpr int VCH = VROWS * kAttnBN / 8;     // 16-byte chunks per V^T tile
+  constexpr int KPT = (KCH + 255) / 256, VPT = (VCH + 255) / 256;
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][kAttnBN * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][VROWS * VLD];
+
+  const int tile = blockIdx.x, head = blockIdx.y;
+  const int seg_s = tiles[3 * tile], seg_e = tiles[3 * tile + 1], q0 = tiles[3 * tile + 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const size_t qk_head = (size_t)Np * HDP, v_head = (size_t)VROWS * Np;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + head * qk_head, (uint32_t)(qk_head * 2));
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + head * qk_head, (uint32_t)(qk_head * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vt + head * v_head, (uint32_t)(v_head * 2));
+
+  const int qrow = q0 + wave * 32 + l32;
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * HDP + ks * 16 + hh * 8) * 2)));
+
+  u32x4 stk[KPT], stv[VPT];
+  auto load_tile = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int c = i * 256 + tid;
+      const int row = c / (HDP / 8), ch = c % (HDP / 8);
+      if (c < KCH) stk[i] = buf_load16(rk, (uint32_t)(((int64_t)(kb + row) * HDP + ch * 8) * 2));
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = i * 256 + tid;
+      const int row = c >> 3, ch = c & 7;
+      if (c < VCH) stv[i] = buf_load16(rv, (uint32_t)(((int64_t)row * Np + kb + ch * 8) * 2));
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int c = i * 256 + tid;
+      const int row = c / (HDP / 8), ch = c % (HDP / 8);
+      if (c < KCH) *reinterpret_cast<u32x4*>(&sK[buf][row * KLD + ch * 8]) = stk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = i * 256 + tid;
+      const int row = c >> 3, ch = c & 7;
+      if (c < VCH) *reinterpret_cast<u32x4*>(&sV[buf][row * VLD + ch * 8]) = stv[i];
+    }
+  };
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = f32x16{};
+  float m_run = 0.f, l_run = 0.f;
+  f32x16 negm = f32x16{};
+  const int k_begin = seg_s & ~(kAttnBN - 1);
+  const int n_kt = (seg_e - k_begin + kAttnBN - 1) / kAttnBN;
+  load_tile(k_begin);
+  store_tile(0);
+  __syncthreads();
+
+  auto step = [&](auto edge_tag, int it) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    const int cur = it & 1;
+    const int kb = k_begin + it * kAttnBN;
+    const bool more = it + 1 < n_kt;
+    if (more) load_tile(kb + kAttnBN);
+    const bool first = EDGE && it == 0;
+    f32x16 s[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      s[b] = first ? f32x16{} : negm;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[cur][(b * 32 + l32) * KLD + (ks * 2 + hh) * 8]);
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
+      }
+    }
+    if constexpr (EDGE) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
+        }
+    }
+    float shift = 0.f;
+    if (first) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+      shift = fmaxf(mx, __shfl_xor(mx, 32));
+    }
+    uint32_t pk[2][8];
+    float ts = 0.f, ts2 = 0.f;
+    auto exp_pack = [&](float sh) {
+      ts = 0.f; ts2 = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          pk[b][j] = pack_bf16x2(__builtin_amdgcn_exp2f(s[b][2 * j] - sh), __builtin_amdgcn_exp2f(s[b][2 * j + 1] - sh));
+          if (j & 1) ts2 = dot2_ones(pk[b][j], ts2); else ts = dot2_ones(pk[b][j], ts);
+        }
+      ts += ts2;
+    };
+    exp_pack(shift);
+    if (first) {
+      m_run = shift;
+    } else if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+      const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
+      exp_pack(sh);
+      const float alpha = __builtin_amdgcn_exp2f(-sh);
+      m_run += sh;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+    }
+    if (first || !EDGE) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) negm[r] = -m_run;
+    }
+    l_run += ts;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[b][4 * e2], pk[b][4 * e2 + 1], pk[b][4 * e2 + 2],
+                                                           pk[b][4 * e2 + 3]});
+        const int g = 2 * b + e2;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[cur][(db * 32 + l32) * VLD + (2 * g + hh) * 8]);
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
+        }
+      }
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
+  };
+
+  step(std::true_type{}, 0);
+  for (int it = 1; it + 1 < n_kt; ++it) step(std::false_type{}, it);
+  if (n_kt > 1) step(std::true_type{}, n_kt - 1);
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l_tot;
+  if (qrow < seg_e) {
+    bf16* orow = O + (int64_t)qrow * ldo + head * hd;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hh;
+        if (d < hd) {   // hd % 4 == 0: the 4-wide piece is all in or all out
+          u32x2 o = {pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
+                     pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv)};
+          *reinterpret_cast<u32x2*>(orow + d) = o;
+        }
+      }
+  }
+}
+
+// Relayout for the general kernel: q/k/v [N, H*hd] (row stride ld) -> rotated, scaled Q and
+// rotated K [H][Np][HDP] (dims >= hd zero), V^T [H][VROWS][Np] (rows >= hd zero, keys at vt_pos);
+// token rows [N, Np) zero. Rotary pairs (d, d + hd/2) with cs[n][d] (d < hd/2).
+__global__ __launch_bounds__(256) void attn_relayout_general_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t ld,
+    const f32x2* __restrict__ cs, int N, int Np, int hd, int HDP, int VROWS, float qscale,
+    bf16* __restrict__ Qo, bf16* __restrict__ Ko, bf16* __restrict__ Vto) {
+  __shared__ bf16 tv[64][129];
+  const int n0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
+  const int half = hd / 2;
+  for (int idx = tid; idx < 64 * HDP; idx += 256) {
+    const int t = idx / HDP, d = idx % HDP, n = n0 + t;
+    if (n >= Np) continue;
+    float qv = 0.f, kv = 0.f;
+    if (n < N && d < hd) {
+      const int j = d < half ? d : d - half;
+      const f32x2 c = cs[(int64_t)n * half + j];
+      const int64_t base = (int64_t)n * ld + (int64_t)head * hd;
+      const float a = (float)q[base + d], b = (float)k[base + d];
+      const float ap = (float)q[base + (d < half ? d + half : d - half)];
+      const float bp = (float)k[base + (d < half ? d + half : d - half)];
+      // x*cos + rotate_half(x)*sin: rotate_half = [-x2, x1]
+      qv = (d < half ? a * c.x - ap * c.y : a * c.x + ap * c.y) * qscale;
+      kv = d < half ? b * c.x - bp * c.y : b * c.x + bp * c.y;
+    }
+    Qo[((int64_t)head * Np + n) * HDP + d] = (bf16)qv;
+    Ko[((int64_t)head * Np + n) * HDP + d] = (bf16)kv;
+  }
+  for (int idx = tid; idx < 64 * VROWS; idx += 256) {
+    const int t = idx / VROWS, d = idx % VROWS, n = n0 + t;
+    tv[t][d] = (n < N && d < hd) ? v[(int64_t)n * ld + (int64_t)head * hd + d] : (bf16)0.f;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 64 * VROWS; idx += 256) {
+    const int d = idx / 64, t = idx % 64, n = n0 + t;
+    if (n < Np) Vto[((int64_t)head * VROWS + d) * Np + vt_pos(n)] = tv[t][d];
+  }
+}
+
+int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
+                      int H, int hd, bf16* out, int64_t ldo, hipStream_t stream) {
+  if (n_tiles == 0) return QVL_OK;
+  if (hd == 72) {
+    hipLaunchKernelGGL((attn_fwd_general_kernel<80, 3>), dim3((unsigned)n_tiles, (unsigned)H), dim3(256), 0, stream,
+                       Qb, Kb, Vtb, d_tiles, Np, H, hd, out, ldo);
+  } else if (hd == 64) {
+    hipLaunchKernelGGL((attn_fwd_general_kernel<64, 2>), dim3((unsigned)n_tiles, (unsigned)H), dim3(256), 0, stream,
+                       Qb, Kb, Vtb, d_tiles, Np, H, hd, out, ldo);
+  } else {
+    return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
+  }
+  return check_launch("attn_fwd_general");
+}
+
+int attention_relayout_general(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
+                               int H, int hd, int HDP, int VROWS, float qscale, bf16* Qo, bf16* Ko, bf16* Vto,
+                               hipStream_t stream) {
+  if (VROWS > 128) return set_error(QVL_ERR_UNSUPPORTED, "relayout: head_dim too large");
+  hipLaunchKernelGGL(attn_relayout_general_kernel, dim3((unsigned)(Np / 64), (unsigned)H), dim3(256), 0, stream,
+                     q, k, v, ld, cs, N, Np, hd, HDP, VROWS, qscale, Qo, Ko, Vto);
+  return check_launch("attn_relayout_general");
+}
+
 // Relayout for the standalone attention entry: q/k/v [N, H*hd] (row stride ld) -> rotated,
 // scaled Q / rotated K [H][Np][64] and V^T [H][64][Np] (keys at vt_pos); rows [N, Np) zero-filled.
 // One workgroup = 64 tokens of one head.

@@ -14,6 +14,8 @@ namespace qvl {
 
 static thread_local char g_err[512];
 
+#define QVL_TRY_RC(expr) do { int _rc = (expr); if (_rc) return _rc; } while (0)
+
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -277,10 +279,19 @@ int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* pos_hw, int64_t
 
 static int64_t attn_np(int64_t n) { return round_up(std::max<int64_t>(n, 1), 64); }
 
+// Head-major attention operand geometry: Q/K rows of `hdp` dims, V^T of `vrows` rows.
+static int attn_dims(int hd, int* hdp, int* vrows) {
+  if (hd == 64) { *hdp = 64; *vrows = 64; return QVL_OK; }
+  if (hd == 72) { *hdp = 80; *vrows = 96; return QVL_OK; }
+  return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
+}
+
 int qvl_vision_attention_workspace_size(int64_t n_tokens, int32_t num_heads, int32_t head_dim, size_t* bytes) {
   if (!bytes || n_tokens < 0 || num_heads <= 0) return set_error(QVL_ERR_INVALID_ARG, "attention ws: bad args");
-  if (head_dim != 64) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (this build: 64)", head_dim);
-  *bytes = (size_t)3 * num_heads * attn_np(n_tokens) * 64 * sizeof(bf16);
+  int hdp, vrows;
+  int rc = attn_dims(head_dim, &hdp, &vrows);
+  if (rc) return rc;
+  *bytes = (size_t)num_heads * attn_np(n_tokens) * (2 * hdp + vrows) * sizeof(bf16);
   return QVL_OK;
 }
 
@@ -298,14 +309,22 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void*
     return set_error(QVL_ERR_INVALID_ARG, "attention: leading dimensions");
   if (((uintptr_t)out & 7) || !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "attention: alignment");
   const int64_t Np = attn_np(n_tokens);
+  int hdp, vrows;
+  attn_dims(hd, &hdp, &vrows);
   bf16* Qb = (bf16*)ws;
-  bf16* Kb = Qb + (size_t)H * Np * 64;
-  bf16* Vb = Kb + (size_t)H * Np * 64;
+  bf16* Kb = Qb + (size_t)H * Np * hdp;
+  bf16* Vb = Kb + (size_t)H * Np * hdp;
   const float qscale = (1.0f / sqrtf((float)hd)) * kLog2e;
-  rc = attention_relayout_hd64((const bf16*)q, (const bf16*)k, (const bf16*)v, ld, (const f32x2*)cs, (int)n_tokens,
-                               (int)Np, H, qscale, Qb, Kb, Vb, (hipStream_t)stream);
+  if (hd == 64) {
+    rc = attention_relayout_hd64((const bf16*)q, (const bf16*)k, (const bf16*)v, ld, (const f32x2*)cs, (int)n_tokens,
+                                 (int)Np, H, qscale, Qb, Kb, Vb, (hipStream_t)stream);
+    if (rc) return rc;
+    return attention_hd64(Qb, Kb, Vb, tiles, n_tiles, (int)Np, H, (bf16*)out, ld_out, (hipStream_t)stream);
+  }
+  rc = attention_relayout_general((const bf16*)q, (const bf16*)k, (const bf16*)v, ld, (const f32x2*)cs, (int)n_tokens,
+                                  (int)Np, H, hd, hdp, vrows, qscale, Qb, Kb, Vb, (hipStream_t)stream);
   if (rc) return rc;
-  return attention_hd64(Qb, Kb, Vb, tiles, n_tiles, (int)Np, H, (bf16*)out, ld_out, (hipStream_t)stream);
+  return attention_general(Qb, Kb, Vb, tiles, n_tiles, (int)Np, H, hd, (bf16*)out, ld_out, (hipStream_t)stream);
 }
 
 int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
@@ -332,14 +351,19 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const vo
                             const int32_t* tiles, int64_t n_tiles, int64_t n_tokens, int32_t H, int32_t hd, void* out,
                             int64_t ld_out) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
-  if (hd != 64) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (this build: 64)", hd);
+  int hdp, vrows;
+  int rc = attn_dims(hd, &hdp, &vrows);
+  if (rc) return rc;
   if (n_tokens < 0 || H <= 0 || n_tiles < 0 || ld_out < (int64_t)H * hd || ld_out % 4)
     return set_error(QVL_ERR_INVALID_ARG, "attention: bad sizes");
   if (n_tokens == 0 || n_tiles == 0) return QVL_OK;
   if (!q || !k || !vt || !tiles || !out) return set_error(QVL_ERR_INVALID_ARG, "attention: NULL operand");
   if ((uintptr_t)out & 7) return set_error(QVL_ERR_MISALIGNED, "attention: out alignment");
-  return attention_hd64((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, (int)attn_np(n_tokens), H,
-                        (bf16*)out, ld_out, (hipStream_t)stream);
+  if (hd == 64)
+    return attention_hd64((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, (int)attn_np(n_tokens), H,
+                          (bf16*)out, ld_out, (hipStream_t)stream);
+  return attention_general((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, (int)attn_np(n_tokens), H,
+                           hd, (bf16*)out, ld_out, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -347,6 +371,7 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const vo
 // ---------------------------------------------------------------------------------------------
 struct TowerLayout {
   int64_t N, Np, D, I_pad, PV, hd, H;
+  int hdp, vrows;
   size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, total;
 };
 
@@ -356,21 +381,26 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   if (c->spatial_merge_size != 2) return set_error(QVL_ERR_UNSUPPORTED, "spatial_merge_size=%d", c->spatial_merge_size);
   if (c->num_heads <= 0 || c->hidden_size % c->num_heads) return set_error(QVL_ERR_INVALID_ARG, "hidden/heads");
   const int64_t hd = c->hidden_size / c->num_heads;
-  if (hd != 64) return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: head_dim=%lld (this build: 64)", (long long)hd);
-  if (c->hidden_size % 128 || c->patch_volume % 64 || c->out_hidden_size % 64)
-    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden %% 128, patch_volume %% 64, out %% 64 required");
+  int hdp, vrows;
+  QVL_TRY_RC(attn_dims((int)hd, &hdp, &vrows));
+  if (c->hidden_size % 64 || c->patch_volume % 64 || c->out_hidden_size % 64)
+    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden, patch_volume and out_hidden_size must be multiples of 64");
+  if (hd == 64 && c->hidden_size % 128)
+    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden %% 128 != 0 with head_dim 64");
   if (c->n_deepstack < 0 || c->n_deepstack > 8) return set_error(QVL_ERR_INVALID_ARG, "n_deepstack=%d", c->n_deepstack);
   if (N % 4) return set_error(QVL_ERR_INVALID_ARG, "n_tokens=%lld not a multiple of 4", (long long)N);
   L->N = N; L->Np = attn_np(N); L->D = c->hidden_size; L->I_pad = round_up(c->intermediate_size, 64);
-  L->PV = c->patch_volume; L->hd = hd; L->H = c->num_heads;
-  const int64_t hcols = std::max<int64_t>({L->I_pad, L->PV, (int64_t)c->hidden_size});
+  L->PV = c->patch_volume; L->hd = hd; L->H = c->num_heads; L->hdp = hdp; L->vrows = vrows;
+  // h hosts the bf16 pixels, the MLP hidden, the merger hidden and (head_dim != 64) the qkv output.
+  int64_t hcols = std::max<int64_t>({L->I_pad, L->PV, (int64_t)c->hidden_size});
+  if (hd != 64) hcols = std::max<int64_t>(hcols, 3 * (int64_t)c->hidden_size);
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t r = o; o += round_up((int64_t)bytes, 256); return r; };
   L->off_x = take((size_t)N * L->D * 2);
   L->off_xn = take((size_t)N * L->D * 2);
-  L->off_q = take((size_t)L->H * L->Np * hd * 2);
-  L->off_k = take((size_t)L->H * L->Np * hd * 2);
-  L->off_vt = take((size_t)L->H * L->Np * hd * 2);
+  L->off_q = take((size_t)L->H * L->Np * hdp * 2);
+  L->off_k = take((size_t)L->H * L->Np * hdp * 2);
+  L->off_vt = take((size_t)L->H * L->Np * vrows * 2);
   L->off_h = take((size_t)N * hcols * 2);
   L->off_cs = take((size_t)N * (hd / 2) * 8);
   L->total = o;
@@ -386,7 +416,6 @@ int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tok
   return QVL_OK;
 }
 
-#define QVL_TRY(expr) do { int _rc = (expr); if (_rc) return _rc; } while (0)
 
 // VisionPatchMerger.__call__ (model.py:648-656): main (LN over D then view [N/4, 4D]) or
 // deepstack (view [N/4, 4D] then LN over 4D); fc1 + GELU-tanh; fc2.
@@ -394,11 +423,11 @@ static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLay
                       bool postshuffle, const bf16* x, bf16* xn, bf16* h, void* out) {
   const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
   if (postshuffle)
-    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
+    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
   else
-    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
-  QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4));
-  QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out, c->out_hidden_size,
+    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
+  QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4));
+  QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out, c->out_hidden_size,
                     N / 4, c->out_hidden_size, D4));
   return QVL_OK;
 }
@@ -408,7 +437,7 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
                       void* ws, size_t ws_bytes) {
   if (!W || !meta) return set_error(QVL_ERR_INVALID_ARG, "encode_vision: NULL weights/metadata");
   TowerLayout L;
-  QVL_TRY(tower_layout(c, meta->n_tokens, &L));
+  QVL_TRY_RC(tower_layout(c, meta->n_tokens, &L));
   if (!ws || ws_bytes < L.total) return set_error(QVL_ERR_WORKSPACE, "encode_vision: workspace %zu < %zu", ws_bytes, L.total);
   if (!aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "encode_vision: workspace alignment");
   if (L.N == 0) return QVL_OK;
@@ -426,31 +455,40 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   const int64_t N = L.N, D = L.D, I = L.I_pad;
 
   // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823)
-  QVL_TRY(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
-  QVL_TRY(qvl_rotary_table(st, QVL_DTYPE_BF16, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
-  QVL_TRY(qvl_pos_embed(st, QVL_DTYPE_BF16, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
-  QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV));
+  QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
+  QVL_TRY_RC(qvl_rotary_table(st, QVL_DTYPE_BF16, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
+  QVL_TRY_RC(qvl_pos_embed(st, QVL_DTYPE_BF16, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
+  QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV));
 
   int ds_next = 0;
   for (int i = 0; i < c->depth; ++i) {
     const qvl_block_weights& B = W->blocks[i];
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
-    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
-    QVL_TRY(qvl_dense_qkv_rotary(st, QVL_DTYPE_BF16, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H));
-    QVL_TRY(qvl_attention_headmajor(st, QVL_DTYPE_BF16, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H, 64, xn, D));
-    QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D));
+    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
+    if (L.hd == 64) {
+      // qkv Dense with rotary + head-major relayout fused into its epilogue.
+      QVL_TRY_RC(qvl_dense_qkv_rotary(st, QVL_DTYPE_BF16, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H));
+    } else {
+      // qkv Dense into h, then rotary + relayout (head_dim 72 pads Q/K to 80 dims, V^T to 96 rows).
+      QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D, D));
+      QVL_TRY_RC(attention_relayout_general(h, h + D, h + 2 * D, 3 * D, cs, (int)N, (int)L.Np, (int)L.H, (int)L.hd,
+                                           L.hdp, L.vrows, (1.0f / sqrtf((float)L.hd)) * kLog2e, Qb, Kb, Vb, st));
+    }
+    QVL_TRY_RC(qvl_attention_headmajor(st, QVL_DTYPE_BF16, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H,
+                                       (int)L.hd, xn, D));
+    QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
-    QVL_TRY(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
-    QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D));
-    QVL_TRY(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I));
+    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
+    QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D));
+    QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I));
     // deepstack tap (model.py:841-843)
     for (int j = 0; j < c->n_deepstack; ++j)
       if (c->deepstack_indexes[j] == i) {
-        QVL_TRY(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, deepstack[ds_next]));
+        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, deepstack[ds_next]));
         ++ds_next;
       }
   }
-  QVL_TRY(run_merger(st, c, L, W->merger, false, x, xn, h, tokens));
+  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, tokens));
   return QVL_OK;
 }
 

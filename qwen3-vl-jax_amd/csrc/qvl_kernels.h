@@ -34,6 +34,11 @@ int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d
                    int H, bf16* out, int64_t ldo, hipStream_t stream);
 int attention_relayout_hd64(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
                             int H, float qscale, bf16* Qo, bf16* Ko, bf16* Vto, hipStream_t stream);
+int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
+                      int H, int hd, bf16* out, int64_t ldo, hipStream_t stream);
+int attention_relayout_general(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
+                               int H, int hd, int HDP, int VROWS, float qscale, bf16* Qo, bf16* Ko, bf16* Vto,
+                               hipStream_t stream);
 int layer_norm_bf16(const bf16* x, int64_t ldx, const float* g, const float* b, bf16* y, int64_t ldy, int rows,
                     int cols, float eps, hipStream_t stream);
 int pos_embed_bf16(const bf16* table, const int* idx, const float* wts, bf16* y, int n_tok, int dim,

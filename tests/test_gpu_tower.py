@@ -47,7 +47,13 @@ def params2b(pkg):
     return pkg.random_params(pkg.spec_2b(), seed=11)
 
 
-def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b):
+@pytest.fixture(scope="module")
+def params8b(pkg):
+    return pkg.random_params(pkg.spec_8b(), seed=12)
+
+
+@pytest.mark.parametrize("shape", ["2b", "8b"])
+def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, shape):
     """2B shape, all 24 blocks, deepstack taps 5/11/17, two images (352 tokens).
 
     Per layer: each GPU block, fed the oracle's input to that block, matches the oracle's block
@@ -57,7 +63,13 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b):
     not bit-identical to it can sit within 1e-2 of it there. The end-to-end bar is therefore: the
     GPU path is at least as close to the fp32 reference as the reference's bf16 mode is (x1.1),
     and within 2e-2 of the bf16 reference; both for tokens and every deepstack feature."""
-    spec, ospec = specs(pkg)
+    if shape == "2b":
+        spec, ospec = specs(pkg)
+        params = params2b
+    else:   # 8B: depth 27, D 1152, 16 x head_dim 72, I 4304 (padded to 4352), Dout 4096
+        spec, ospec = specs(pkg, depth=27, ds=(8, 16, 24), shape="8b")
+        params = params8b
+    params2b = params
     grids = [(1, 16, 16), (1, 8, 12)]
     px = pixels(grids, 1)
     ref = vt.encode_vision(params2b, px, grids, ospec, "bf16", keep_layers=True)
@@ -120,6 +132,20 @@ def test_config3_video_reduced_depth(pkg, params2b):
     ref = vt.encode_vision(params2b, px, g, ospec, "bf16")
     tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
     tok, ds = tower(px, g)
+    assert rel_l2(to_np(tok), ref.tokens) <= TOL
+    assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
+
+
+def test_config4_grid_reduced_depth(pkg, params8b):
+    """BASELINE config 4's input (one 1344x1344 image, grid 1x84x84 = 7056 patches, one segment) on
+    the 8B-shape tower, first 2 blocks + a deepstack tap after block 1 + the merger: rel-L2 <= 1e-2."""
+    spec, ospec = specs(pkg, depth=2, ds=(1,), shape="8b")
+    grids = [(1, 84, 84)]
+    px = pixels(grids, 6)
+    ref = vt.encode_vision(params8b, px, grids, ospec, "bf16")
+    tower = pkg.Qwen3VisionTransformer(spec).bind(params8b)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    assert tuple(tok.shape) == (1764, 4096)
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
 
