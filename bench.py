@@ -123,21 +123,25 @@ def main():
                                   cs.data_ptr()), "rotary")
     s_ = st.cuda_stream
     BF = cp.QVL_DTYPE_BF16
+    pb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(pb)), "dense ws")
+    part = torch.empty(pb.value, dtype=torch.uint8, device=dev)
+    pp, pn = part.data_ptr(), pb.value
     seg = [2304] * 8
     kernels = {
         # name: (callable, algorithmic FLOPs per launch, launches per step)
-        "fc1 (gemm 256x256, bias+GELU) 18432x4096x1024": (
-            lambda: lib.qvl_dense(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
-                                  hout.data_ptr(), I, N, I, D), 2.0 * N * D * I, spec.depth),
-        "fc2 (gemm 256x128, bias+residual) 18432x1024x4096": (
-            lambda: lib.qvl_dense(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), I, blk.fc2_w, blk.fc2_b,
-                                  yk.data_ptr(), D, yk.data_ptr(), D, N, D, I), 2.0 * N * I * D, spec.depth),
-        "proj (gemm 256x128, bias+residual) 18432x1024x1024": (
-            lambda: lib.qvl_dense(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, xk.data_ptr(), D, blk.proj_w, blk.proj_b,
-                                  yk.data_ptr(), D, yk.data_ptr(), D, N, D, D), 2.0 * N * D * D, spec.depth),
-        "qkv+rotary (gemm 256x256) 18432x3072x1024": (
+        "fc1 (gemm, bias+GELU) 18432x4096x1024": (
+            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
+                                     hout.data_ptr(), I, N, I, D, pp, pn), 2.0 * N * D * I, spec.depth),
+        "fc2 (gemm, bias+residual) 18432x1024x4096": (
+            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), I, blk.fc2_w, blk.fc2_b,
+                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, I, pp, pn), 2.0 * N * I * D, spec.depth),
+        "proj (gemm, bias+residual) 18432x1024x1024": (
+            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, xk.data_ptr(), D, blk.proj_w, blk.proj_b,
+                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, D, pp, pn), 2.0 * N * D * D, spec.depth),
+        "qkv+rotary (gemm) 18432x3072x1024": (
             lambda: lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(),
-                                             qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H),
+                                             qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn),
             2.0 * N * D * 3 * D, spec.depth),
         "attention (varlen, 8 x 2304 tokens, 16x64)": (
             lambda: lib.qvl_attention_headmajor(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),

@@ -99,6 +99,17 @@ int qvl_dense(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, in
               const void* d_w, const float* d_bias, const void* d_residual, int64_t ldr,
               void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k);
 
+/* qvl_dense with a workspace for tail split-K: when the tiles do not fill whole rounds of the
+ * GPU's compute units, the last round's tiles are split along K into fp32 partials in
+ * `d_workspace` and summed by a second kernel before the epilogue (same results up to fp32
+ * summation order). Without enough workspace it behaves exactly like qvl_dense.
+ * qvl_dense_workspace_size gives the bytes that always suffice on the current device. */
+int qvl_dense_workspace_size(size_t* bytes);
+int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, int64_t lda,
+                 const void* d_w, const float* d_bias, const void* d_residual, int64_t ldr,
+                 void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                 void* d_workspace, size_t workspace_bytes);
+
 /* LayerNorm over the last axis: fp32 mean / biased variance / rsqrt(var + eps), affine, cast
  * back (model.py:375-388). cols must be a multiple of 8 and <= 8192. */
 int qvl_layer_norm(void* stream, int32_t dtype, const void* d_x, int64_t ldx, const float* d_gamma,
@@ -134,10 +145,12 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const voi
  * epilogue applies the 2D rotary to q and k with `d_cos_sin` and writes the head-major operands
  * of qvl_attention_headmajor: q (scaled by head_dim^-0.5 * log2(e)) and k as [H][Np][64],
  * v transposed as [H][64][Np], Np = n_tokens rounded up to 64 (rows [n_tokens, Np) zeroed).
- * head_dim must be 64 and D a multiple of 128. */
+ * head_dim must be 64 and D a multiple of 128. The optional workspace (qvl_dense_workspace_size
+ * bytes, may be NULL) enables tail split-K as in qvl_dense_ws. */
 int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
                          const float* d_bias, const void* d_cos_sin, void* d_q, void* d_k, void* d_vt,
-                         int64_t n_tokens, int64_t hidden, int32_t num_heads);
+                         int64_t n_tokens, int64_t hidden, int32_t num_heads,
+                         void* d_workspace, size_t workspace_bytes);
 
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the

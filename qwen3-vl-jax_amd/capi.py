@@ -64,13 +64,15 @@ SIGNATURES = {
     "qvl_pack_dense_weight": (C.c_int, [_p, _i32, _p, _i64, _i64, _p]),
     "qvl_cast": (C.c_int, [_p, _i32, _p, _p, _i64]),
     "qvl_dense": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64]),
+    "qvl_dense_workspace_size": (C.c_int, [C.POINTER(_sz)]),
+    "qvl_dense_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _sz]),
     "qvl_layer_norm": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _f32]),
     "qvl_pos_embed": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64]),
     "qvl_rotary_table": (C.c_int, [_p, _i32, _p, _i64, _i32, _f32, _p]),
     "qvl_vision_attention_workspace_size": (C.c_int, [_i64, _i32, _i32, C.POINTER(_sz)]),
     "qvl_vision_attention": (C.c_int, [_p, _i32, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _i32,
                                        _p, _sz]),
-    "qvl_dense_qkv_rotary": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32]),
+    "qvl_dense_qkv_rotary": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _sz]),
     "qvl_attention_headmajor": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _p, _i64]),
     "qvl_encode_vision_workspace_size": (C.c_int, [C.POINTER(VisionConfig), _i64, C.POINTER(_sz)]),
     "qvl_encode_vision": (C.c_int, [_p, C.POINTER(VisionConfig), C.POINTER(VisionWeights),

@@ -13,6 +13,10 @@
 // double-buffered with one barrier per K step; the LDS layout is XOR-swizzled for the 16-lane,
 // 64-bank fragment reads; fragments are double-buffered across the four 16-deep k-steps and
 // interleaved one read per MFMA.
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
 #include "qvl_kernels.h"
 
 namespace qvl {
@@ -26,9 +30,10 @@ struct GemmShape {
   static constexpr int THREADS = 64 * WM * WN;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int MB = TM / 32, NB = TN / 32;
-  static constexpr int ROWS_PER_PASS = THREADS / 8;     // rows one staging pass covers
-  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "staging must tile the operands");
-  static constexpr int XPT = BM / ROWS_PER_PASS, WPT = BN / ROWS_PER_PASS;
+  static constexpr int ROWS_PER_PASS = THREADS / 8;     // rows one DMA pass (8 per wave) covers
+  static_assert(BM % 8 == 0 && BN % 8 == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
+  // DMA passes per operand; the last pass may cover only part of the waves (predicated per wave).
+  static constexpr int XPT = (BM + ROWS_PER_PASS - 1) / ROWS_PER_PASS, WPT = (BN + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
   static constexpr int LDS_ELEMS = (BM + BN) * kBK;    // one stage
 };
 
@@ -40,14 +45,133 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Epilogue pieces, shared by the GEMM and the split-K reduction.
+// ---------------------------------------------------------------------------------------------
+// Bias (+ GELU | + residual) on 4 consecutive features n..n+3 of token m, one bf16 store.
+template <int EPI>
+__device__ __forceinline__ void epi_store_quad(const GemmParams& p, int m, int n, const float (&acc4)[4]) {
+  if (m >= p.M || n >= p.N) return;
+  const f32x4 bv = *reinterpret_cast<const f32x4*>(p.bias + n);
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = acc4[e] + bv[e];
+  if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+  }
+  if constexpr (EPI == kEpiBiasResidual) {
+    const u32x2 r = *reinterpret_cast<const u32x2*>(p.res + (int64_t)m * p.ldr + n);
+    v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
+  }
+  const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldc + n) = o;
+}
+
+// Rotary epilogue of the qkv GEMM for one pair of quads: features n..n+3 (dims d..d+3 < 32 of a
+// head) and n+32..n+35 of token m. q/k: x*cos + rotate_half(x)*sin, q also scaled; written to
+// [H][Np][64]. v: written transposed to [H][64][Np] at key position vt_pos(m). Tokens in
+// [M, Np) get zeros (the attention kernel's padding).
+__device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n, const float (&lo_acc)[4],
+                                              const float (&hi_acc)[4]) {
+  if (m >= p.Np || n >= p.N) return;
+  const bool live = m < p.M;
+  const int which = n / p.D;                 // 0 = q, 1 = k, 2 = v
+  const int head = (n % p.D) / 64, d = n % 64;
+  float lo[4], hi[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lo[e] = live ? lo_acc[e] + p.bias[n + e] : 0.f;
+    hi[e] = live ? hi_acc[e] + p.bias[n + e + 32] : 0.f;
+  }
+  if (which == 2) {
+    bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vt[(int64_t)(d + e) * p.Np] = (bf16)lo[e];
+      vt[(int64_t)(d + e + 32) * p.Np] = (bf16)hi[e];
+    }
+    return;
+  }
+  float o1[4], o2[4];
+  if (live) {
+    const f32x2* csr = p.cs + (int64_t)m * 32 + d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f32x2 t = csr[e];
+      o1[e] = lo[e] * t.x - hi[e] * t.y;     // x*cos + rotate_half(x)*sin, dims < 32
+      o2[e] = hi[e] * t.x + lo[e] * t.y;     // dims + 32
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o1[e] = 0.f; o2[e] = 0.f; }
+  }
+  const float sc = which == 0 ? p.qscale : 1.0f;
+  bf16* dst = (which == 0 ? p.q : p.k) + ((int64_t)head * p.Np + m) * 64;
+  const u32x2 v1 = {pack_bf16x2(o1[0] * sc, o1[1] * sc), pack_bf16x2(o1[2] * sc, o1[3] * sc)};
+  const u32x2 v2 = {pack_bf16x2(o2[0] * sc, o2[1] * sc), pack_bf16x2(o2[2] * sc, o2[3] * sc)};
+  *reinterpret_cast<u32x2*>(dst + d) = v1;
+  *reinterpret_cast<u32x2*>(dst + d + 32) = v2;
+}
+
+// Epilogue of one wave's accumulators. Block (a, b), register r: feature
+// n = n0 + wn*TN + 32a + 8*(r/4) + 4*hh + r%4, token m = m0 + wm*TM + 32b + l32.
+template <int BM, int BN, int WM, int WN, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
+                                              f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
+                                              int m0, int n0, int wm, int wn, int lane) {
+  using S = GemmShape<BM, BN, WM, WN>;
+  const int l32 = lane & 31, hh = lane >> 5;
+  if constexpr (EPI == kEpiQkvRope) {
+    static_assert(S::TN % 64 == 0, "the rotary epilogue needs whole 64-feature heads per wave");
+    // The wave's TN features are whole heads: blocks (2h, 2h+1) hold dims [0,32) / [32,64).
+#pragma unroll
+    for (int b = 0; b < S::MB; ++b) {
+      const int m = m0 + wm * S::TM + b * 32 + l32;
+#pragma unroll
+      for (int h2 = 0; h2 < S::NB / 2; ++h2)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float lo[4], hi[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
+          epi_rope_pair(p, m, n0 + wn * S::TN + h2 * 64 + 8 * g + 4 * hh, lo, hi);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < S::NB; ++a)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int b = 0; b < S::MB; ++b) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
+          epi_store_quad<EPI>(p, m0 + wm * S::TM + b * 32 + l32, n0 + wn * S::TN + a * 32 + 8 * g + 4 * hh, v);
+        }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
   using S = GemmShape<BM, BN, WM, WN>;
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];   // [2][BM+BN][64]
 
+  // Work assignment: workgroups [0, full_tiles) each own a whole tile (XCD-remapped); the rest
+  // own 1/split of the K range of one of the remaining "tail" tiles and write fp32 partials.
   const int tiles_n = (p.N + BN - 1) / BN;
-  const int tiles_m = (p.M + BM - 1) / BM;
-  const int tile = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int KT = p.K / kBK;
+  int tile, kt0 = 0, kt1 = KT, unit = -1;
+  if ((int)blockIdx.x < p.full_tiles) {
+    tile = xcd_remap(blockIdx.x, p.full_tiles);
+  } else {
+    unit = blockIdx.x - p.full_tiles;
+    tile = p.full_tiles + unit / p.split;
+    const int s = unit % p.split;
+    kt0 = s * KT / p.split;
+    kt1 = (s + 1) * KT / p.split;
+  }
   const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
 
@@ -75,10 +199,12 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
     const uint32_t xa = lds_base + stage * S::LDS_ELEMS * 2, wa = xa + BM * kBK * 2;
 #pragma unroll
     for (int i = 0; i < S::XPT; ++i)
-      dma16(rxw, xv, (uint32_t)((i * S::ROWS_PER_PASS * p.lda + k0) * 2), xa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
+      if (BM % S::ROWS_PER_PASS == 0 || i * S::ROWS_PER_PASS + wave * 8 < BM)   // wave-uniform
+        dma16(rxw, xv, (uint32_t)((i * S::ROWS_PER_PASS * p.lda + k0) * 2), xa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
 #pragma unroll
     for (int i = 0; i < S::WPT; ++i)
-      dma16(rww, wv, (uint32_t)((i * S::ROWS_PER_PASS * p.K + k0) * 2), wa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
+      if (BN % S::ROWS_PER_PASS == 0 || i * S::ROWS_PER_PASS + wave * 8 < BN)
+        dma16(rww, wv, (uint32_t)((i * S::ROWS_PER_PASS * p.K + k0) * 2), wa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
   };
 
   f32x16 acc[S::NB][S::MB];
@@ -111,16 +237,15 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   };
   constexpr int NMF = S::NB * S::MB;
 
-  const int KT = p.K / kBK;
-  dma_stage(0, 0);
+  dma_stage(kt0 * kBK, 0);
   wait_dma();
   __syncthreads();
   read_frags(smem, 0, 0);
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int cur = (kt - kt0) & 1;
     const bf16* xs = smem + cur * S::LDS_ELEMS;
-    const bool more = kt + 1 < KT;
+    const bool more = kt + 1 < kt1;
     if (more) dma_stage((kt + 1) * kBK, cur ^ 1);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
@@ -139,101 +264,102 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
     if (more) read_frags(smem + (cur ^ 1) * S::LDS_ELEMS, 0, 0);
   }
 
-  // ---------------------------------------------------------------------------------------
-  // Epilogue. Block (a, b), register r: n = nbase + 8*(r/4) + 4*hh + r%4, m = mbase + l32.
-  // ---------------------------------------------------------------------------------------
-  if constexpr (EPI == kEpiQkvRope) {
-    static_assert(S::NB == 4, "the rotary epilogue needs 128-feature (two-head) wave tiles");
-    // Wave sub-tile covers TN = 128 features = two heads of 64 (n0 + wn*TN is a multiple of
-    // 128, D a multiple of 128): blocks (0,1) are head hA dims [0,32) / [32,64), (2,3) head hA+1.
-    const int nw = n0 + wn * S::TN;
-    if (nw >= p.N) return;
-    const int which = nw / p.D;                 // 0 = q, 1 = k, 2 = v
-    const int head0 = (nw % p.D) / 64;
+  if (unit >= 0) {
+    // Tail unit: store the fp32 partial row-major within the tile, part[unit][BM][BN].
+    float* dst = p.part + (size_t)unit * BM * BN;
 #pragma unroll
-    for (int b = 0; b < S::MB; ++b) {
-      const int m = m0 + wm * S::TM + b * 32 + l32;
-      if (m >= p.Np) continue;
-      const bool live = m < p.M;
+    for (int a = 0; a < S::NB; ++a)
 #pragma unroll
-      for (int hp = 0; hp < S::NB / 2; ++hp) {
-        const int head = head0 + hp;
+      for (int b = 0; b < S::MB; ++b)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int d = 8 * g + 4 * hh;          // first of 4 consecutive dims in [0, 32)
-          float lo[4], hi[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int n = nw + hp * 64 + d + e;
-            lo[e] = live ? acc[2 * hp][b][4 * g + e] + p.bias[n] : 0.f;
-            hi[e] = live ? acc[2 * hp + 1][b][4 * g + e] + p.bias[n + 32] : 0.f;
-          }
-          if (which == 2) {
-            bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              vt[(int64_t)(d + e) * p.Np] = (bf16)lo[e];
-              vt[(int64_t)(d + e + 32) * p.Np] = (bf16)hi[e];
-            }
-          } else {
-            float o1[4], o2[4];
-            if (live) {
-              const f32x2* csr = p.cs + (int64_t)m * 32 + d;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const f32x2 t = csr[e];
-                o1[e] = lo[e] * t.x - hi[e] * t.y;     // x*cos + rotate_half(x)*sin, d < 32
-                o2[e] = hi[e] * t.x + lo[e] * t.y;     // d + 32
-              }
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) { o1[e] = 0.f; o2[e] = 0.f; }
-            }
-            const float sc = which == 0 ? p.qscale : 1.0f;
-            bf16* dst = (which == 0 ? p.q : p.k) + ((int64_t)head * p.Np + m) * 64;
-            u32x2 v1 = {pack_bf16x2(o1[0] * sc, o1[1] * sc), pack_bf16x2(o1[2] * sc, o1[3] * sc)};
-            u32x2 v2 = {pack_bf16x2(o2[0] * sc, o2[1] * sc), pack_bf16x2(o2[2] * sc, o2[3] * sc)};
-            *reinterpret_cast<u32x2*>(dst + d) = v1;
-            *reinterpret_cast<u32x2*>(dst + d + 32) = v2;
-          }
+          const int mm = wm * S::TM + b * 32 + l32, nn = wn * S::TN + a * 32 + 8 * g + 4 * hh;
+          *reinterpret_cast<f32x4*>(dst + (size_t)mm * BN + nn) =
+              f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
         }
-      }
-    }
-  } else {
+    return;
+  }
+  gemm_epilogue<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane);
+}
+
+// Sums the split-K partials of the tail tiles and applies the epilogue, one thread per 4-feature
+// quad (per quad pair for the rotary epilogue): fully parallel and coalesced over the partials.
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, int tail) {
+  constexpr int QPR = (EPI == kEpiQkvRope) ? BN / 8 : BN / 4;   // work items per tile row
+  const int64_t per_tile = (int64_t)BM * QPR;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)tail * per_tile) return;
+  const int t = (int)(idx / per_tile);
+  const int rem = (int)(idx % per_tile);
+  const int mm = rem / QPR, q = rem % QPR;
+  const int nn = (EPI == kEpiQkvRope) ? (q / 8) * 64 + (q % 8) * 4 : q * 4;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = p.full_tiles + t;
+  const int m = (tile / tiles_n) * BM + mm, n = (tile % tiles_n) * BN + nn;
+  float lo[4] = {0.f, 0.f, 0.f, 0.f}, hi[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.split; ++s) {
+    const float* src = p.part + ((size_t)(t * p.split + s) * BM + mm) * BN + nn;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src);
 #pragma unroll
-    for (int a = 0; a < S::NB; ++a) {
+    for (int e = 0; e < 4; ++e) lo[e] += a[e];
+    if constexpr (EPI == kEpiQkvRope) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(src + 32);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * S::TN + a * 32 + 8 * g + 4 * hh;
-        if (n >= p.N) continue;
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(p.bias + n);
-#pragma unroll
-        for (int b = 0; b < S::MB; ++b) {
-          const int m = m0 + wm * S::TM + b * 32 + l32;
-          if (m >= p.M) continue;
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e] + bv[e];
-          if constexpr (EPI == kEpiBiasGelu) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-          }
-          if constexpr (EPI == kEpiBiasResidual) {
-            const u32x2 r = *reinterpret_cast<const u32x2*>(p.res + (int64_t)m * p.ldr + n);
-            v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
-          }
-          u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldc + n) = o;
-        }
-      }
+      for (int e = 0; e < 4; ++e) hi[e] += b[e];
     }
   }
+  if constexpr (EPI == kEpiQkvRope) epi_rope_pair(p, m, n, lo, hi);
+  else epi_store_quad<EPI>(p, m, n, lo);
+}
+
+int gemm_device_cus() {
+  static int cus[64] = {0};   // per device; benign race (every thread stores the same value)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Work plan for BM x BN tiles, one workgroup per CU (every tile shape takes 96-136 KB of LDS).
+// Cost model, in microseconds: a tile costs BM*BN*K MACs at a per-CU rate `tile_rate`; whole
+// rounds of tiles run as is; the last partial round either runs as is or, with a partials
+// workspace, is split along K so its units fill one round (1/split of a tile) plus the split-K
+// reduction, priced at its fp32 partial traffic (written once, read once) over HBM.
+struct GemmPlan { int full, split, tail; double cost_us; };
+
+constexpr double kHbmBytesPerUs = 4.0e6;     // sustained fp32 partial traffic, bytes per us
+constexpr double kReduceLaunchUs = 4.0;
+
+template <int BM, int BN>
+static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_cu, int split_mode) {
+  const int rows = std::max(p.M, p.Np);      // the rotary epilogue also zero-fills [M, Np)
+  const int tiles = ((rows + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const int KT = p.K / kBK;
+  const double tile_us = (double)BM * BN * p.K / macs_per_us_per_cu;
+  const int rounds = (tiles + cus - 1) / cus;
+  GemmPlan g{tiles, 1, 0, rounds * tile_us};
+  const int tail = tiles % cus;
+  if (tail == 0 || !p.part || split_mode < 0) return g;
+  const int split = std::min(std::min(8, KT), cus / tail);
+  if (split < 2 || (int64_t)tail * split * BM * BN > p.part_elems) return g;
+  const double part_bytes = 2.0 * tail * split * BM * BN * sizeof(float);
+  const double cost = (tiles / cus) * tile_us + tile_us / split + part_bytes / kHbmBytesPerUs + kReduceLaunchUs;
+  if (cost >= g.cost_us && split_mode == 0) return g;
+  g.full = tiles - tail;
+  g.tail = tail;
+  g.split = split;
+  g.cost_us = cost;
+  return g;
 }
 
 template <int BM, int BN, int WM, int WN, int EPI>
-static int launch_gemm(const GemmParams& p, hipStream_t stream) {
+static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
-  const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   const size_t lds = 2 * S::LDS_ELEMS * sizeof(bf16);
   static bool attr_set = false;   // benign race: every thread sets the same value
   if (!attr_set) {
@@ -242,21 +368,60 @@ static int launch_gemm(const GemmParams& p, hipStream_t stream) {
       return set_error(QVL_ERR_LAUNCH, "gemm_bf16: cannot reserve %zu bytes of LDS", lds);
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI>), dim3(tiles), dim3(S::THREADS), lds, stream, p);
-  return check_launch("gemm_bf16");
+  p.full_tiles = g.full;
+  p.split = g.split;
+  const int grid = g.full + g.tail * g.split;
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI>), dim3(grid), dim3(S::THREADS), lds, stream, p);
+  int rc = check_launch("gemm_bf16");
+  if (rc || g.tail == 0) return rc;
+  const int64_t items = (int64_t)g.tail * BM * ((EPI == kEpiQkvRope) ? BN / 8 : BN / 4);
+  hipLaunchKernelGGL((gemm_splitk_reduce_kernel<BM, BN, EPI>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     stream, p, g.tail);
+  return check_launch("gemm_splitk_reduce");
 }
 
-// Tile choice: 256x256 tiles on 8 waves (two per SIMD, 64x128 each) keep LDS traffic per MFMA
-// low while a second wave hides each wave's memory latency; 256x128 tiles (8 waves of 64x64)
-// when 256x256 would leave most CUs idle on the last round of workgroups.
+// Tile choice by the cost model above. Shapes (per-CU MAC rates measured on the tower's GEMMs):
+//   288x256 on 12 waves (three per SIMD, 96x64 each): 64 row tiles cover 18432 tokens, so the
+//     N = 1024 / 3072 / 4096 GEMMs fill exactly 1 / 3 / 4 rounds of 256 CUs;
+//   256x256 on 8 waves (two per SIMD, 64x128 each): the least LDS traffic per MFMA;
+//   256x128 on 8 waves (64x64 each): half the work per tile, for balancing small grids.
+constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.36e6;   // MACs/us/CU
+
+// Test hook: QVL_GEMM_PLAN = "<tile>[:split|:nosplit]" with tile 288x256 | 256x256 | 256x128
+// pins the tile shape (and forces or forbids the tail split) so every variant can be checked
+// against the others; unset, the cost model decides.
+struct ForcedPlan { int tile = 0, split_mode = 0; };   // tile: 0 auto, 1/2/3 as listed
+
+static ForcedPlan forced_plan() {
+  ForcedPlan f;
+  const char* e = getenv("QVL_GEMM_PLAN");
+  if (!e || !*e) return f;
+  if (!strncmp(e, "288x256", 7)) f.tile = 1;
+  else if (!strncmp(e, "256x256", 7)) f.tile = 2;
+  else if (!strncmp(e, "256x128", 7)) f.tile = 3;
+  if (strstr(e, ":nosplit")) f.split_mode = -1;
+  else if (strstr(e, ":split")) f.split_mode = 1;
+  return f;
+}
+
 template <int EPI>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
+  const int cus = gemm_device_cus();
+  const ForcedPlan f = forced_plan();
+  const GemmPlan a = plan_gemm<288, 256>(p, cus, kRate288x256, f.split_mode);
+  const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
+  const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
+  int pick = f.tile;
+  if (EPI == kEpiQkvRope && pick == 3) pick = 2;     // 64-feature heads need TN % 64 == 0
+  if (pick == 0) {
+    pick = (a.cost_us <= b.cost_us && a.cost_us <= c.cost_us) ? 1 : (EPI == kEpiQkvRope || b.cost_us <= c.cost_us) ? 2 : 3;
+  }
+  if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI>(p, a, stream);
   if constexpr (EPI == kEpiQkvRope) {
-    return launch_gemm<256, 256, 4, 2, EPI>(p, stream);
+    return launch_gemm<256, 256, 4, 2, EPI>(p, b, stream);
   } else {
-    const int64_t big = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-    if (big >= 768) return launch_gemm<256, 256, 4, 2, EPI>(p, stream);
-    return launch_gemm<256, 128, 4, 2, EPI>(p, stream);
+    if (pick == 2) return launch_gemm<256, 256, 4, 2, EPI>(p, b, stream);
+    return launch_gemm<256, 128, 4, 2, EPI>(p, c, stream);
   }
 }
 

@@ -223,8 +223,9 @@ int qvl_cast(void* stream, int32_t dtype, const float* x, void* y, int64_t n) {
   return cast_f32_bf16(x, (bf16*)y, n, (hipStream_t)stream);
 }
 
-int qvl_dense(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w, const float* bias,
-              const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
+                      const float* bias, const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n,
+                      int64_t k, void* ws, size_t ws_bytes) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense: dtype %d", dtype);
   if (epi < QVL_EPI_BIAS || epi > QVL_EPI_BIAS_RESIDUAL) return set_error(QVL_ERR_INVALID_ARG, "dense: epilogue %d", epi);
   if (m < 0 || n <= 0 || k <= 0) return set_error(QVL_ERR_INVALID_ARG, "dense: m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
@@ -236,7 +237,7 @@ int qvl_dense(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t l
   if (lda < k || ldc < n || (epi == QVL_EPI_BIAS_RESIDUAL && ldr < n))
     return set_error(QVL_ERR_INVALID_ARG, "dense: leading dimension too small");
   if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || lda % 8 || ldc % 4 ||
-      (epi == QVL_EPI_BIAS_RESIDUAL && (((uintptr_t)res & 7) || ldr % 4)))
+      (epi == QVL_EPI_BIAS_RESIDUAL && (((uintptr_t)res & 7) || ldr % 4)) || (ws && !aligned16(ws)))
     return set_error(QVL_ERR_MISALIGNED, "dense: operands must be 16-byte aligned (lda % 8 == 0, ldc % 4 == 0)");
   if (m * lda * 2 >= (int64_t)UINT32_MAX || n * k * 2 >= (int64_t)UINT32_MAX)
     return set_error(QVL_ERR_UNSUPPORTED, "dense: operand larger than 4 GiB");
@@ -244,7 +245,25 @@ int qvl_dense(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t l
   p.x = (const bf16*)x; p.lda = lda; p.w = (const bf16*)w; p.bias = bias;
   p.res = (const bf16*)res; p.ldr = ldr; p.y = (bf16*)y; p.ldc = ldc;
   p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
   return gemm_bf16(p, epi, (hipStream_t)stream);
+}
+
+int qvl_dense(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w, const float* bias,
+              const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+  return dense_impl(stream, dtype, epi, x, lda, w, bias, res, ldr, y, ldc, m, n, k, nullptr, 0);
+}
+
+int qvl_dense_workspace_size(size_t* bytes) {
+  if (!bytes) return set_error(QVL_ERR_INVALID_ARG, "bytes is NULL");
+  *bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);
+  return QVL_OK;
+}
+
+int qvl_dense_ws(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w, const float* bias,
+                 const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n, int64_t k, void* ws,
+                 size_t ws_bytes) {
+  return dense_impl(stream, dtype, epi, x, lda, w, bias, res, ldr, y, ldc, m, n, k, ws, ws_bytes);
 }
 
 int qvl_layer_norm(void* stream, int32_t dtype, const void* x, int64_t ldx, const float* g, const float* b, void* y,
@@ -328,7 +347,8 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void*
 }
 
 int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
-                         const void* cs, void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H) {
+                         const void* cs, void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H,
+                         void* ws, size_t ws_bytes) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: dtype %d", dtype);
   if (H <= 0 || hidden != (int64_t)H * 64) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64");
   if (hidden % 128) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: hidden %% 128 != 0");
@@ -344,6 +364,8 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda
   p.q = (bf16*)q; p.k = (bf16*)k; p.vt = (bf16*)vt; p.cs = (const f32x2*)cs;
   p.Np = (int)attn_np(n_tokens); p.D = (int)hidden;
   p.qscale = (1.0f / sqrtf(64.0f)) * kLog2e;
+  if (ws && !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: workspace alignment");
+  p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
   return gemm_bf16(p, kEpiQkvRope, (hipStream_t)stream);
 }
 
@@ -372,7 +394,7 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const vo
 struct TowerLayout {
   int64_t N, Np, D, I_pad, PV, hd, H;
   int hdp, vrows;
-  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, total;
+  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, total;
 };
 
 static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
@@ -403,6 +425,8 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   L->off_vt = take((size_t)L->H * L->Np * vrows * 2);
   L->off_h = take((size_t)N * hcols * 2);
   L->off_cs = take((size_t)N * (hd / 2) * 8);
+  L->part_bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);
+  L->off_part = take(L->part_bytes);
   L->total = o;
   return QVL_OK;
 }
@@ -420,15 +444,16 @@ int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tok
 // VisionPatchMerger.__call__ (model.py:648-656): main (LN over D then view [N/4, 4D]) or
 // deepstack (view [N/4, 4D] then LN over 4D); fc1 + GELU-tanh; fc2.
 static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLayout& L, const qvl_merger_weights& mw,
-                      bool postshuffle, const bf16* x, bf16* xn, bf16* h, void* out) {
+                      bool postshuffle, const bf16* x, bf16* xn, bf16* h, void* out, void* part) {
   const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
   if (postshuffle)
     QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
   else
     QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
-  QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4));
-  QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out, c->out_hidden_size,
-                    N / 4, c->out_hidden_size, D4));
+  QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4,
+                          D4, part, L.part_bytes));
+  QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out,
+                          c->out_hidden_size, N / 4, c->out_hidden_size, D4, part, L.part_bytes));
   return QVL_OK;
 }
 
@@ -452,13 +477,16 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   bf16* Vb = (bf16*)(base + L.off_vt);
   bf16* h = (bf16*)(base + L.off_h);
   f32x2* cs = (f32x2*)(base + L.off_cs);
+  void* part = base + L.off_part;
+  const size_t PB = L.part_bytes;
   const int64_t N = L.N, D = L.D, I = L.I_pad;
 
   // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823)
   QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
   QVL_TRY_RC(qvl_rotary_table(st, QVL_DTYPE_BF16, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
   QVL_TRY_RC(qvl_pos_embed(st, QVL_DTYPE_BF16, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
-  QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV));
+  QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
+                          L.PV, part, PB));
 
   int ds_next = 0;
   for (int i = 0; i < c->depth; ++i) {
@@ -467,28 +495,33 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
     if (L.hd == 64) {
       // qkv Dense with rotary + head-major relayout fused into its epilogue.
-      QVL_TRY_RC(qvl_dense_qkv_rotary(st, QVL_DTYPE_BF16, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H));
+      QVL_TRY_RC(qvl_dense_qkv_rotary(st, QVL_DTYPE_BF16, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H,
+                                      part, PB));
     } else {
       // qkv Dense into h, then rotary + relayout (head_dim 72 pads Q/K to 80 dims, V^T to 96 rows).
-      QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D, D));
+      QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D,
+                              D, part, PB));
       QVL_TRY_RC(attention_relayout_general(h, h + D, h + 2 * D, 3 * D, cs, (int)N, (int)L.Np, (int)L.H, (int)L.hd,
                                            L.hdp, L.vrows, (1.0f / sqrtf((float)L.hd)) * kLog2e, Qb, Kb, Vb, st));
     }
     QVL_TRY_RC(qvl_attention_headmajor(st, QVL_DTYPE_BF16, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H,
                                        (int)L.hd, xn, D));
-    QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D));
+    QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D,
+                            part, PB));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
     QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
-    QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D));
-    QVL_TRY_RC(qvl_dense(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I));
+    QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D,
+                            part, PB));
+    QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I,
+                            part, PB));
     // deepstack tap (model.py:841-843)
     for (int j = 0; j < c->n_deepstack; ++j)
       if (c->deepstack_indexes[j] == i) {
-        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, deepstack[ds_next]));
+        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, deepstack[ds_next], part));
         ++ds_next;
       }
   }
-  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, tokens));
+  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, tokens, part));
   return QVL_OK;
 }
 

@@ -18,7 +18,17 @@ struct GemmParams {
   const f32x2* cs;               // [M, 32] (cos, sin)
   int Np, D;
   float qscale;
+  // Tail split-K: fp32 partials workspace (NULL: no splitting) and its capacity in floats; the
+  // launcher fills full_tiles / split.
+  float* part;
+  int64_t part_elems;
+  int full_tiles, split;
 };
+
+// Floats of split-K partial workspace that lets every GEMM of up to 256x256 tiles split its tail
+// on a device with `cus` compute units (one tail unit per CU, at most one tile of partials each).
+inline int64_t gemm_partials_elems(int cus) { return (int64_t)cus * 256 * 256; }
+int gemm_device_cus();
 
 // Position of key m in the V^T layout the attention kernel reads: within each 16-key group
 // (aligned to 16 in the token index) the middle two 4-key quads are swapped, so that the 8 keys a

@@ -215,3 +215,93 @@ def test_attention_hd72_ragged(pkg, lib, grids):
     for i in range(len(cu) - 1):
         s, e = cu[i], cu[i + 1]
         assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (i, s, e)
+
+
+PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x256:split", "256x256:split", "256x128:split"]
+
+
+def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
+    y = res.clone() if epi == 2 else torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    r_ptr = y.data_ptr() if epi == 2 else 0
+    cp.check(lib.qvl_dense_ws(stream(), cp.QVL_DTYPE_BF16, epi, x.data_ptr(), k, w.data_ptr(), bias.data_ptr(),
+                              r_ptr, n, y.data_ptr(), n, m, n, k, ws.data_ptr(), ws.numel()))
+    return to_np(y)
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("m,n,k", [(18432, 1024, 1024), (4600, 2048, 4096), (2304, 4096, 1024), (300, 192, 128),
+                                   (18000, 1152, 4352)])
+def test_dense_tile_plans_agree(pkg, lib, monkeypatch, epi, m, n, k):
+    """Every tile shape (288x256 / 256x256 / 256x128) gives bit-identical results without the
+    tail split (same K order per output); with the split (fp32 partials summed by the reduce
+    kernel) within rel-L2 2e-3 of them; all within rel-L2 4e-3 of torch fp32 on the same bf16
+    operands. Shapes include M not a multiple of any tile height and N not a multiple of 256."""
+    cp = pkg.capi
+    g = torch.Generator(device="cpu").manual_seed(m + n + k + epi)
+    x = torch.randn((m, k), generator=g).to(DEV).to(torch.bfloat16)
+    w = pack(lib, cp, (torch.randn((k, n), generator=g) * 0.05).numpy())
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).float().to(DEV)
+    res = torch.randn((m, n), generator=g).to(DEV).to(torch.bfloat16)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    outs = {}
+    for plan in PLANS:
+        monkeypatch.setenv("QVL_GEMM_PLAN", plan)
+        outs[plan] = dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws)
+    monkeypatch.delenv("QVL_GEMM_PLAN")
+    outs["auto"] = dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws)
+    ref = x.float() @ w[:n, :k].float().T + bias
+    if epi == 1:
+        ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    if epi == 2:
+        ref = ref + res.float()
+    ref = ref.cpu().numpy()
+    base = outs["256x256:nosplit"]
+    for plan, got in outs.items():
+        if plan.endswith(":nosplit"):
+            np.testing.assert_array_equal(got, base, err_msg=plan)
+        else:
+            assert rel_l2(got, base) <= 2e-3, plan
+        assert rel_l2(got, ref) <= 4e-3, plan
+
+
+@pytest.mark.parametrize("grids", [[(1, 48, 48)] * 8, [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
+def test_qkv_rotary_tile_plans_agree(pkg, lib, monkeypatch, grids):
+    """The fused qkv+rotary GEMM writes bit-identical head-major Q/K/V^T (including the zeroed
+    padding rows [N, Np)) with 288x256 and 256x256 tiles; with the tail split within rel-L2 2e-3."""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    N, D, H = m.n_tokens, 1024, 16
+    g = torch.Generator(device="cpu").manual_seed(3)
+    x = torch.randn((N, D), generator=g).to(DEV).to(torch.bfloat16)
+    w = pack(lib, cp, (torch.randn((D, 3 * D), generator=g) * 0.03).numpy())
+    bias = (torch.randn(3 * D, generator=g) * 0.1).to(torch.bfloat16).float().to(DEV)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    cs = torch.empty((N, 32, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, 64, 10000.0, cs.data_ptr()))
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    Np = -(-N // 64) * 64
+    outs = {}
+    for plan in ["256x256:nosplit", "288x256:nosplit", "256x256:split", "288x256:split", None]:
+        if plan:
+            monkeypatch.setenv("QVL_GEMM_PLAN", plan)
+        else:
+            monkeypatch.delenv("QVL_GEMM_PLAN")
+        q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
+        k, vt = q.clone(), q.clone()
+        cp.check(lib.qvl_dense_qkv_rotary(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, w.data_ptr(), bias.data_ptr(),
+                                          cs.data_ptr(), q.data_ptr(), k.data_ptr(), vt.data_ptr(), N, D, H,
+                                          ws.data_ptr(), nb.value))
+        outs[plan] = [to_np(t) for t in (q, k, vt)]
+    base = outs["256x256:nosplit"]
+    for plan, got in outs.items():
+        for a, b in zip(got, base):
+            if plan and plan.endswith(":nosplit"):
+                np.testing.assert_array_equal(a, b, err_msg=plan)
+            else:
+                assert rel_l2(a, b) <= 2e-3, plan
+        q, k, vt = got
+        assert not q[:, N:].any() and not k[:, N:].any(), plan

@@ -151,9 +151,14 @@ def test_config4_grid_reduced_depth(pkg, params8b):
 
 
 def test_config2_full_batch_invariance(pkg, params2b):
-    """Full config 2 (8 x 48x48, 18432 tokens, 24 blocks): each image's merged tokens and
-    deepstack rows equal that image encoded alone — segments never interact, and the kernels'
-    per-row arithmetic does not depend on the batch. Bit-exact."""
+    """Full config 2 (8 x 48x48, 18432 tokens, 24 blocks).
+
+    Determinism: the same batch twice gives bit-identical tokens and deepstack features.
+    Batch invariance: each image's rows match that image encoded alone within the bf16 end-to-end
+    tolerance (rel-L2 <= 2e-2). Not bit-exact: the GEMMs split their last round of tiles along K
+    (tail split-K), so a batch's last tiles are summed in a different fp32 order than the image
+    alone, and one-ulp differences grow through 24 bf16 blocks. Segments never interact, so any
+    cross-segment leakage would show up as O(1) errors."""
     spec, _ = specs(pkg)
     grids = [(1, 48, 48)] * 8
     px = pixels(grids, 4)
@@ -161,12 +166,16 @@ def test_config2_full_batch_invariance(pkg, params2b):
     tok, ds = tower(px, np.array(grids, np.int32))
     tok = to_np(tok); ds = [to_np(d) for d in ds]
     assert np.isfinite(tok).all()
-    for k in (0, 5):
+    tok2, ds2 = tower(px, np.array(grids, np.int32))
+    np.testing.assert_array_equal(to_np(tok2), tok)
+    for a, b in zip(ds2, ds):
+        np.testing.assert_array_equal(to_np(a), b)
+    for k in (0, 5, 7):
         t1, d1 = tower(px[2304 * k: 2304 * (k + 1)], np.array([(1, 48, 48)], np.int32))
         rows = slice(576 * k, 576 * (k + 1))
-        np.testing.assert_array_equal(to_np(t1), tok[rows])
+        assert rel_l2(tok[rows], to_np(t1)) <= 2e-2
         for a, b in zip(d1, ds):
-            np.testing.assert_array_equal(to_np(a), b[rows])
+            assert rel_l2(b[rows], to_np(a)) <= 2e-2
 
 
 def test_encode_vision_api(pkg, params2b):
