@@ -48,6 +48,15 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 // ---------------------------------------------------------------------------------------------
 // Epilogue pieces, shared by the GEMM and the split-K reduction.
 // ---------------------------------------------------------------------------------------------
+// The epilogues round at the reference's cast points (flax Dense in bf16, model.py:556-613):
+// y = bf16(bf16(x.W) + bias); GELU: bf16(gelu(y)); residual: bf16(res + y).
+template <int EPI>
+__device__ __forceinline__ float epi_value(float acc, float bias) {
+  float v = round_bf16(round_bf16(acc) + bias);
+  if constexpr (EPI == kEpiBiasGelu) v = gelu_tanh(v);
+  return v;
+}
+
 // Bias (+ GELU | + residual) on 4 consecutive features n..n+3 of token m, one bf16 store.
 template <int EPI>
 __device__ __forceinline__ void epi_store_quad(const GemmParams& p, int m, int n, const float (&acc4)[4]) {
@@ -55,17 +64,49 @@ __device__ __forceinline__ void epi_store_quad(const GemmParams& p, int m, int n
   const f32x4 bv = *reinterpret_cast<const f32x4*>(p.bias + n);
   float v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = acc4[e] + bv[e];
-  if constexpr (EPI == kEpiBiasGelu) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-  }
+  for (int e = 0; e < 4; ++e) v[e] = epi_value<EPI>(acc4[e], bv[e]);
   if constexpr (EPI == kEpiBiasResidual) {
     const u32x2 r = *reinterpret_cast<const u32x2*>(p.res + (int64_t)m * p.ldr + n);
     v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
   }
   const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
   *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldc + n) = o;
+}
+
+// Same on 8 consecutive features n..n+7 whose products arrive already rounded to bf16 (packed
+// pairs, from the LDS-staged tile): 16-byte loads/stores when the rows are 16-byte aligned.
+template <int EPI>
+__device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n, u32x4 raw, bool vec16) {
+  const f32x4 b0 = *reinterpret_cast<const f32x4*>(p.bias + n);
+  const bool full = n + 8 <= p.N;
+  const f32x4 b1 = full ? *reinterpret_cast<const f32x4*>(p.bias + n + 4) : f32x4{};
+  float v[8] = {bf16_lo(raw.x), bf16_hi(raw.x), bf16_lo(raw.y), bf16_hi(raw.y),
+                bf16_lo(raw.z), bf16_hi(raw.z), bf16_lo(raw.w), bf16_hi(raw.w)};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = epi_value<EPI>(v[e], b0[e]);
+    v[e + 4] = epi_value<EPI>(v[e + 4], b1[e]);
+  }
+  bf16* dst = p.y + (int64_t)m * p.ldc + n;
+  if (vec16 && full) {
+    if constexpr (EPI == kEpiBiasResidual) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(p.res + (int64_t)m * p.ldr + n);
+      v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
+      v[4] += bf16_lo(r.z); v[5] += bf16_hi(r.z); v[6] += bf16_lo(r.w); v[7] += bf16_hi(r.w);
+    }
+    *reinterpret_cast<u32x4*>(dst) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                           pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    return;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1 && !full) break;
+    if constexpr (EPI == kEpiBiasResidual) {
+      const u32x2 r = *reinterpret_cast<const u32x2*>(p.res + (int64_t)m * p.ldr + n + 4 * h);
+      v[4 * h] += bf16_lo(r.x); v[4 * h + 1] += bf16_hi(r.x); v[4 * h + 2] += bf16_lo(r.y); v[4 * h + 3] += bf16_hi(r.y);
+    }
+    *reinterpret_cast<u32x2*>(dst + 4 * h) = u32x2{pack_bf16x2(v[4 * h], v[4 * h + 1]), pack_bf16x2(v[4 * h + 2], v[4 * h + 3])};
+  }
 }
 
 // Rotary epilogue of the qkv GEMM for one pair of quads: features n..n+3 (dims d..d+3 < 32 of a
@@ -81,8 +122,8 @@ __device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n,
   float lo[4], hi[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    lo[e] = live ? lo_acc[e] + p.bias[n + e] : 0.f;
-    hi[e] = live ? hi_acc[e] + p.bias[n + e + 32] : 0.f;
+    lo[e] = live ? epi_value<kEpiBias>(lo_acc[e], p.bias[n + e]) : 0.f;
+    hi[e] = live ? epi_value<kEpiBias>(hi_acc[e], p.bias[n + e + 32]) : 0.f;
   }
   if (which == 2) {
     bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
@@ -99,8 +140,9 @@ __device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const f32x2 t = csr[e];
-      o1[e] = lo[e] * t.x - hi[e] * t.y;     // x*cos + rotate_half(x)*sin, dims < 32
-      o2[e] = hi[e] * t.x + lo[e] * t.y;     // dims + 32
+      // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582)
+      o1[e] = round_bf16(round_bf16(lo[e] * t.x) - round_bf16(hi[e] * t.y));   // dims < 32
+      o2[e] = round_bf16(round_bf16(hi[e] * t.x) + round_bf16(lo[e] * t.y));   // dims + 32
     }
   } else {
 #pragma unroll
@@ -150,6 +192,44 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
           epi_store_quad<EPI>(p, m0 + wm * S::TM + b * 32 + l32, n0 + wn * S::TN + a * 32 + 8 * g + 4 * hh, v);
         }
+  }
+}
+
+// LDS-staged epilogue: each wave writes bf16(acc) of its sub-tile into the (free) LDS as a
+// row-major BM x BN tile whose 16-byte chunks are XOR-swizzled by row (chunk ^ row % (BN/8)),
+// so the 32 rows one ds_write_b64 touches land on distinct chunks; then the workgroup walks the
+// tile row by row, 16 bytes (8 features) per lane, and applies bias / GELU / residual with whole
+// rows per load and store instead of 8-byte pieces of 32 rows.
+template <int BM, int BN, int WM, int WN, int EPI>
+__device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
+                                                  f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
+                                                  int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem) {
+  using S = GemmShape<BM, BN, WM, WN>;
+  constexpr int CH = BN / 8;
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int a = 0; a < S::NB; ++a)
+#pragma unroll
+    for (int b = 0; b < S::MB; ++b)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = wm * S::TM + b * 32 + l32;
+        const int c = (wn * S::TN + a * 32) / 8 + g;
+        const u32x2 v = {pack_bf16x2(acc[a][b][4 * g], acc[a][b][4 * g + 1]),
+                         pack_bf16x2(acc[a][b][4 * g + 2], acc[a][b][4 * g + 3])};
+        *reinterpret_cast<u32x2*>(smem + r * BN + ((c ^ (r % CH)) << 3) + hh * 4) = v;
+      }
+  __syncthreads();
+  const bool vec16 = ((p.ldc | (EPI == kEpiBiasResidual ? p.ldr : 0)) & 7) == 0;
+  constexpr int ITERS = BM * CH / S::THREADS;
+  static_assert(BM * CH % S::THREADS == 0, "epilogue walk");
+#pragma unroll 4
+  for (int i = 0; i < ITERS; ++i) {
+    const int q = i * S::THREADS + tid;
+    const int r = q / CH, c = q % CH;
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(smem + r * BN + ((c ^ (r % CH)) << 3));
+    const int m = m0 + r, n = n0 + c * 8;
+    if (m < p.M && n < p.N) epi_store_oct<EPI>(p, m, n, raw, vec16);
   }
 }
 
@@ -279,7 +359,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         }
     return;
   }
-  gemm_epilogue<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane);
+  if constexpr (EPI == kEpiQkvRope) gemm_epilogue<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane);
+  else gemm_epilogue_lds<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane, tid, smem);
 }
 
 // Sums the split-K partials of the tail tiles and applies the epilogue, one thread per 4-feature
@@ -360,7 +441,7 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 template <int BM, int BN, int WM, int WN, int EPI>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
-  const size_t lds = 2 * S::LDS_ELEMS * sizeof(bf16);
+  const size_t lds = std::max(2 * S::LDS_ELEMS, EPI == kEpiQkvRope ? 0 : BM * BN) * sizeof(bf16);
   static bool attr_set = false;   // benign race: every thread sets the same value
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
