@@ -38,6 +38,24 @@ def tower_flops(n_tokens, seg_lens, D=1024, I=4096, depth=24, n_ds=3, Dout=2048,
     return f
 
 
+def hbm_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary: FETCH_SIZE +
+    WRITE_SIZE (KiB per dispatch), each scaled by the factor the same counter reads for a plain
+    copy of known size. None when the summary has no line for this kernel."""
+    path = ROOT / "profiles" / "hbm_traffic_config2.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        # | kernel | FETCH KiB | WRITE KiB | fetch scale | write scale | bytes/launch |
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 6 and cells[0] == kernel:
+            try:
+                return int(float(cells[5]))
+            except ValueError:
+                return None
+    return None
+
+
 def cpu_baseline(params, px_one, grid_one, depth=24):
     """The numpy oracle (fp32, the reference's default dtype) on one image of the workload."""
     from oracle import vision_tower as vt
@@ -64,6 +82,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--only", default=None,
+                    help="launch only this kernel class (name prefix, or 'copy') --kernel-reps times; for rocprofv3 runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -87,20 +107,21 @@ def main():
     tower.metadata(grids)
     torch.cuda.synchronize()
 
-    for _ in range(args.warmup):
+    st = torch.cuda.current_stream()
+    steps = 0 if args.only else args.steps
+    for _ in range(0 if args.only else args.warmup):
         tower(px, grids)
     torch.cuda.synchronize()
-    st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(st)
-    for _ in range(args.steps):
+    for _ in range(steps):
         tower(px, grids)
     e1.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+    ms = e0.elapsed_time(e1) / max(steps, 1)
     value = N / (ms / 1e3)
     flops = tower_flops(N, [2304] * 8)
     step_tflops = flops / (ms / 1e3) / 1e12
@@ -128,28 +149,57 @@ def main():
     part = torch.empty(pb.value, dtype=torch.uint8, device=dev)
     pp, pn = part.data_ptr(), pb.value
     seg = [2304] * 8
+    ln_g = torch.ones(D, device=dev)
+    ln_b = torch.zeros(D, device=dev)
+    px_b = torch.empty((N, spec.patch_volume), dtype=torch.bfloat16, device=dev)
     kernels = {
-        # name: (callable, algorithmic FLOPs per launch, launches per step)
+        # name: (callable, "mfma" FLOPs or "hbm" bytes per launch, bound, launches per step)
         "fc1 (gemm, bias+GELU) 18432x4096x1024": (
             lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
-                                     hout.data_ptr(), I, N, I, D, pp, pn), 2.0 * N * D * I, spec.depth),
+                                     hout.data_ptr(), I, N, I, D, pp, pn), 2.0 * N * D * I, "mfma", spec.depth),
         "fc2 (gemm, bias+residual) 18432x1024x4096": (
             lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), I, blk.fc2_w, blk.fc2_b,
-                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, I, pp, pn), 2.0 * N * I * D, spec.depth),
+                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, I, pp, pn), 2.0 * N * I * D, "mfma",
+            spec.depth),
         "proj (gemm, bias+residual) 18432x1024x1024": (
             lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, xk.data_ptr(), D, blk.proj_w, blk.proj_b,
-                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, D, pp, pn), 2.0 * N * D * D, spec.depth),
+                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, D, pp, pn), 2.0 * N * D * D, "mfma",
+            spec.depth),
         "qkv+rotary (gemm) 18432x3072x1024": (
             lambda: lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(),
                                              qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn),
-            2.0 * N * D * 3 * D, spec.depth),
+            2.0 * N * D * 3 * D, "mfma", spec.depth),
         "attention (varlen, 8 x 2304 tokens, 16x64)": (
             lambda: lib.qvl_attention_headmajor(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
                                                 tens["tiles"].data_ptr(), md.n_tiles, N, H, 64, yk.data_ptr(), D),
-            float(sum(4 * L * L * D for L in seg)), spec.depth),
+            float(sum(4 * L * L * D for L in seg)), "mfma", spec.depth),
+        # memory-bound kernels: algorithmic bytes = every operand read once + every output written once
+        "layer_norm (18432x1024 bf16)": (
+            lambda: lib.qvl_layer_norm(s_, BF, xk.data_ptr(), D, ln_g.data_ptr(), ln_b.data_ptr(), yk.data_ptr(), D,
+                                       N, D, 1e-6), 2.0 * N * D * 2 + 2 * D * 4, "hbm", 2 * spec.depth + 4),
+        "pos_embed (18432x1024, 4 bilinear taps)": (
+            lambda: lib.qvl_pos_embed(s_, BF, tower._w.pos_table, tens["tap_idx"].data_ptr(),
+                                      tens["tap_w"].data_ptr(), yk.data_ptr(), N, D),
+            N * D * 2 + N * 4 * 8 + spec.num_position_embeddings * D * 2, "hbm", 1),
+        "cast pixels f32->bf16 (18432x1536)": (
+            lambda: lib.qvl_cast(s_, BF, px.data_ptr(), px_b.data_ptr(), N * spec.patch_volume),
+            N * spec.patch_volume * 6.0, "hbm", 1),
     }
+    if args.only:
+        if args.only == "copy":      # plain copy of known size, the calibration for the HBM byte counters
+            src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(args.kernel_reps):
+                dst.copy_(src)
+        else:
+            fn = next(v[0] for k, v in kernels.items() if k.startswith(args.only))
+            for _ in range(args.kernel_reps):
+                cp.check(fn(), args.only)
+        torch.cuda.synchronize()
+        print(f"bench.py --only {args.only}: {args.kernel_reps} launches", flush=True)
+        return
     kstats = {}
-    for name, (fn, fl, per_step) in kernels.items():
+    for name, (fn, work, bound, per_step) in kernels.items():
         for _ in range(3):
             cp.check(fn(), name)
         k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -159,11 +209,18 @@ def main():
         k1.record(st)
         torch.cuda.synchronize()
         k_ms = k0.elapsed_time(k1) / args.kernel_reps
-        kstats[name] = {"avg_launch_ms": round(k_ms, 4), "tflops": round(fl / (k_ms / 1e3) / 1e12, 1),
-                        "frac_mfma_peak": round(fl / (k_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                        "ms_per_step": round(k_ms * per_step, 3), "flops_per_launch": fl}
-    dom = max(kstats, key=lambda k: kstats[k]["ms_per_step"])
+        if bound == "mfma":
+            kstats[name] = {"bound": "mfma", "avg_launch_ms": round(k_ms, 4), "tflops": round(work / (k_ms / 1e3) / 1e12, 1),
+                            "frac_mfma_peak": round(work / (k_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                            "ms_per_step": round(k_ms * per_step, 3), "flops_per_launch": work}
+        else:
+            gbs = work / (k_ms / 1e3) / 1e9
+            kstats[name] = {"bound": "hbm", "avg_launch_ms": round(k_ms, 4), "gbs": round(gbs, 1),
+                            "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(k_ms * per_step, 3),
+                            "bytes_per_launch": work}
+    dom = max((k for k in kstats if kstats[k]["bound"] == "mfma"), key=lambda k: kstats[k]["ms_per_step"])
     dk = kstats[dom]
+    traffic = hbm_traffic(dom)
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "patches/s", "n_gpus": 1, "steps": args.steps,
@@ -175,7 +232,7 @@ def main():
         "mfma_frac_step": round(step_tflops / PEAK_BF16_TFLOPS, 4),
         "step_tflops": round(step_tflops, 1),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": dk["tflops"], "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": dk["frac_mfma_peak"], "traffic": None,
+                     "unit": "TFLOP/s", "frac": dk["frac_mfma_peak"], "traffic": traffic,
                      "avg_launch_ms": dk["avg_launch_ms"], "flops_per_launch": dk["flops_per_launch"]},
         "kernels": kstats,
         "wall_s_timed": round(wall, 3),
