@@ -68,12 +68,15 @@ int qvl_vision_metadata(const int32_t* h_grid_thw, int64_t n_grids, int32_t merg
                         int32_t num_position_embeddings, int32_t dtype,
                         int32_t* h_cu_seqlens, int32_t* h_pos_hw, int32_t* h_tap_idx, float* h_tap_w);
 
-/* Attention work list for qvl_vision_attention / qvl_encode_vision: one int32 triple
- * (segment start, segment end, first query) per query tile of the kernel's tile height,
- * longest segment first. Replaces the per-segment Python loop of model.py:585-598.
- * With h_tiles == NULL only *n_tiles is written. */
-int qvl_attention_worklist(const int32_t* h_cu_seqlens, int64_t n_segments, int32_t* h_tiles,
-                           int64_t capacity, int64_t* n_tiles);
+/* Attention work list for qvl_vision_attention / qvl_attention_headmajor / qvl_encode_vision:
+ * one int32 quadruple (segment start, segment end, first query, head) per query tile of the
+ * kernel's tile height and per head. Replaces the per-segment Python loop of model.py:585-598.
+ * Layout: (segment, head) groups, longest segment first, are dealt to 8 queues (one per XCD)
+ * by least accumulated work (query tiles x keys); item k is entry k / 8 of queue k % 8, the
+ * XCD that runs workgroup k, so a group's K/V stay in one L2. Short queues are padded with
+ * empty items (start == end). With h_items == NULL only *n_items is written. */
+int qvl_attention_worklist(const int32_t* h_cu_seqlens, int64_t n_segments, int32_t num_heads,
+                           int32_t* h_items, int64_t capacity, int64_t* n_items);
 
 /* Rotary inverse frequencies theta^(-2j/(head_dim/2)), j < head_dim/4, float32
  * (VisionRotaryEmbedding, model.py:540-546 with dim = head_dim/2, model.py:672). */
@@ -131,7 +134,8 @@ int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* d_pos_hw, int64
  * three column blocks of the qkv Dense output), rotated in-kernel with `d_cos_sin`
  * (qvl_rotary_table), then softmax(q k^T / sqrt(head_dim)) v per cu_seqlens segment
  * (block-diagonal, non-causal, fp32 online softmax). Output [n_tokens, num_heads*head_dim]
- * row stride ld_out. `d_tiles` is the qvl_attention_worklist output (device copy).
+ * row stride ld_out. `d_tiles` / `n_tiles` are the qvl_attention_worklist items (device copy)
+ * and their count.
  * Workspace: qvl_vision_attention_workspace_size(). head_dim in {64, 72}. */
 int qvl_vision_attention_workspace_size(int64_t n_tokens, int32_t num_heads, int32_t head_dim,
                                         size_t* bytes);

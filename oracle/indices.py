@@ -192,17 +192,27 @@ def merged_row_closed(grid_thw, merge: int = 2) -> np.ndarray:
     return np.concatenate(out) if out else np.zeros(0, np.int64)
 
 
-def attention_tiles(cu_seqlens, block_m: int):
-    """Work list of (segment start, segment end, q0) q-tiles, longest segment first.
+def attention_tiles(cu_seqlens, block_m: int, num_heads: int = 1, queues: int = 8):
+    """Work list of (segment start, segment end, q0, head) items, dealt to `queues` queues.
 
-    Not a reference quantity: the schedule the HIP attention kernel walks. Every query row of
-    every non-empty segment must appear in exactly one tile.
+    Not a reference quantity: the schedule the HIP attention kernel walks. (segment, head)
+    groups, longest segment first (stable), each go whole to the queue with the least work so far
+    (work = query tiles x keys; ties to the lowest queue); item k is entry k // queues of queue
+    k % queues; short queues are padded with (0, 0, 0, 0). Every query row of every non-empty
+    segment must appear in exactly one item per head.
     """
     cu = np.asarray(cu_seqlens, dtype=np.int64)
     segs = [(int(cu[i]), int(cu[i + 1])) for i in range(len(cu) - 1) if cu[i + 1] > cu[i]]
     segs.sort(key=lambda s: -(s[1] - s[0]))
-    tiles = []
+    qs = [[] for _ in range(queues)]
+    load = [0] * queues
     for s, e in segs:
-        for q0 in range(s, e, block_m):
-            tiles.append((s, e, q0))
-    return np.asarray(tiles, dtype=np.int32).reshape(-1, 3)
+        ntile = -(-(e - s) // block_m)
+        for h in range(num_heads):
+            qi = min(range(queues), key=lambda j: (load[j], j))
+            load[qi] += ntile * (e - s)
+            qs[qi].extend((s, e, q0, h) for q0 in range(s, e, block_m))
+    longest = max((len(q) for q in qs), default=0)
+    items = [qs[k % queues][k // queues] if k // queues < len(qs[k % queues]) else (0, 0, 0, 0)
+             for k in range(longest * queues)]
+    return np.asarray(items, dtype=np.int32).reshape(-1, 4)

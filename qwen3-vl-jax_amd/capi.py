@@ -59,7 +59,7 @@ SIGNATURES = {
     "qvl_version": (C.c_int, []),
     "qvl_grid_counts": (C.c_int, [_pi32, _i64, _i32, C.POINTER(_i64), C.POINTER(_i64)]),
     "qvl_vision_metadata": (C.c_int, [_pi32, _i64, _i32, _i32, _i32, _pi32, _pi32, _pi32, _pf32]),
-    "qvl_attention_worklist": (C.c_int, [_pi32, _i64, _pi32, _i64, C.POINTER(_i64)]),
+    "qvl_attention_worklist": (C.c_int, [_pi32, _i64, _i32, _pi32, _i64, C.POINTER(_i64)]),
     "qvl_rotary_inv_freq": (C.c_int, [_i32, _f32, _pf32]),
     "qvl_pack_dense_weight": (C.c_int, [_p, _i32, _p, _i64, _i64, _p]),
     "qvl_cast": (C.c_int, [_p, _i32, _p, _p, _i64]),

@@ -50,8 +50,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
     const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * kAttnBN * kHD];   // [stage][K | V^T][64][64]
 
-  const int tile = blockIdx.x, head = blockIdx.y;
-  const int seg_s = tiles[3 * tile], seg_e = tiles[3 * tile + 1], q0 = tiles[3 * tile + 2];
+  // Work item: (segment start, segment end, first query, head); empty items pad short queues.
+  const int item = blockIdx.x;
+  const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2], head = tiles[4 * item + 3];
+  if (seg_e <= seg_s) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
@@ -234,8 +236,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_general_kernel(
   __shared__ __attribute__((aligned(16))) bf16 sK[2][kAttnBN * KLD];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][VROWS * VLD];
 
-  const int tile = blockIdx.x, head = blockIdx.y;
-  const int seg_s = tiles[3 * tile], seg_e = tiles[3 * tile + 1], q0 = tiles[3 * tile + 2];
+  // Work item: (segment start, segment end, first query, head); empty items pad short queues.
+  const int item = blockIdx.x;
+  const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2], head = tiles[4 * item + 3];
+  if (seg_e <= seg_s) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const size_t qk_head = (size_t)Np * HDP, v_head = (size_t)VROWS * Np;
@@ -444,10 +448,10 @@ int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int
                       int H, int hd, bf16* out, int64_t ldo, hipStream_t stream) {
   if (n_tiles == 0) return QVL_OK;
   if (hd == 72) {
-    hipLaunchKernelGGL((attn_fwd_general_kernel<80, 3>), dim3((unsigned)n_tiles, (unsigned)H), dim3(256), 0, stream,
+    hipLaunchKernelGGL((attn_fwd_general_kernel<80, 3>), dim3((unsigned)n_tiles), dim3(256), 0, stream,
                        Qb, Kb, Vtb, d_tiles, Np, H, hd, out, ldo);
   } else if (hd == 64) {
-    hipLaunchKernelGGL((attn_fwd_general_kernel<64, 2>), dim3((unsigned)n_tiles, (unsigned)H), dim3(256), 0, stream,
+    hipLaunchKernelGGL((attn_fwd_general_kernel<64, 2>), dim3((unsigned)n_tiles), dim3(256), 0, stream,
                        Qb, Kb, Vtb, d_tiles, Np, H, hd, out, ldo);
   } else {
     return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
@@ -505,7 +509,7 @@ __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles,
                    int Np, int H, bf16* out, int64_t ldo, hipStream_t stream) {
   if (n_tiles == 0) return QVL_OK;
-  hipLaunchKernelGGL(attn_fwd_hd64_kernel, dim3((unsigned)n_tiles, (unsigned)H), dim3(256), 0, stream,
+  hipLaunchKernelGGL(attn_fwd_hd64_kernel, dim3((unsigned)n_tiles), dim3(256), 0, stream,
                      Qb, Kb, Vtb, d_tiles, Np, H, out, ldo);
   return check_launch("attn_fwd_hd64");
 }

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <vector>
 
 #include "qvl_kernels.h"
@@ -33,6 +34,7 @@ int check_launch(const char* what) {
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 constexpr int kAttnTileM = 128;   // query tile height of attn_fwd_hd64_kernel
+constexpr int kAttnQueues = 8;    // attention work queues: one per XCD of an MI355X
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Float32 value of bf16(x) with round-to-nearest-even (host).
@@ -168,8 +170,10 @@ int qvl_vision_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int
   return QVL_OK;
 }
 
-int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t* tiles, int64_t capacity, int64_t* n_tiles) {
-  if (!cu || !n_tiles) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens / n_tiles is NULL");
+int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, int32_t* items, int64_t capacity,
+                           int64_t* n_items) {
+  if (!cu || !n_items) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens / n_items is NULL");
+  if (num_heads <= 0) return set_error(QVL_ERR_INVALID_ARG, "num_heads=%d", num_heads);
   std::vector<std::pair<int32_t, int32_t>> segs;
   for (int64_t i = 0; i < n_seg; ++i) {
     if (cu[i + 1] < cu[i]) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens not monotone at %lld", (long long)i);
@@ -179,17 +183,35 @@ int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t* tiles, int
                    [](const std::pair<int32_t, int32_t>& a, const std::pair<int32_t, int32_t>& b) {
                      return (a.second - a.first) > (b.second - b.first);
                    });
-  int64_t n = 0;
-  for (auto& s : segs) n += (s.second - s.first + kAttnTileM - 1) / kAttnTileM;
-  *n_tiles = n;
-  if (!tiles) return QVL_OK;
-  if (capacity < n) return set_error(QVL_ERR_INVALID_ARG, "worklist capacity %lld < %lld", (long long)capacity, (long long)n);
-  int64_t k = 0;
-  for (auto& s : segs)
-    for (int32_t q0 = s.first; q0 < s.second; q0 += kAttnTileM) {
-      tiles[3 * k] = s.first; tiles[3 * k + 1] = s.second; tiles[3 * k + 2] = q0;
-      ++k;
+  // (segment, head) groups, longest first, each to the queue with the least work so far
+  // (work = query tiles x keys); a group's tiles stay in one queue so its K/V stay in one L2.
+  std::vector<std::vector<std::array<int32_t, 4>>> queue(kAttnQueues);
+  std::vector<int64_t> load(kAttnQueues, 0);
+  for (auto& sg : segs) {
+    const int32_t len = sg.second - sg.first;
+    const int64_t ntile = (len + kAttnTileM - 1) / kAttnTileM;
+    for (int32_t h = 0; h < num_heads; ++h) {
+      int qi = 0;
+      for (int j = 1; j < kAttnQueues; ++j)
+        if (load[j] < load[qi]) qi = j;
+      load[qi] += ntile * len;
+      for (int32_t q0 = sg.first; q0 < sg.second; q0 += kAttnTileM) queue[qi].push_back({sg.first, sg.second, q0, h});
     }
+  }
+  size_t longest = 0;
+  for (auto& q : queue) longest = std::max(longest, q.size());
+  const int64_t n = (int64_t)longest * kAttnQueues;
+  *n_items = n;
+  if (!items) return QVL_OK;
+  if (capacity < n) return set_error(QVL_ERR_INVALID_ARG, "worklist capacity %lld < %lld", (long long)capacity, (long long)n);
+  // Item k goes to the workgroup k, which the dispatcher places on XCD k % 8: queue k % 8,
+  // position k / 8. Short queues are padded with empty items (start == end).
+  for (int64_t k = 0; k < n; ++k) {
+    const auto& q = queue[k % kAttnQueues];
+    const size_t pos = (size_t)(k / kAttnQueues);
+    const std::array<int32_t, 4> it = pos < q.size() ? q[pos] : std::array<int32_t, 4>{0, 0, 0, 0};
+    for (int c = 0; c < 4; ++c) items[4 * k + c] = it[c];
+  }
   return QVL_OK;
 }
 

@@ -153,7 +153,7 @@ class GridMetadata:
 
 
 def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
-                  dtype: int = capi.QVL_DTYPE_BF16) -> GridMetadata:
+                  dtype: int = capi.QVL_DTYPE_BF16, num_heads: int = 16) -> GridMetadata:
     g = np.ascontiguousarray(np.asarray(grid_thw, dtype=np.int32).reshape(-1, 3))
     lib = capi.load()
     nt, ns = C.c_int64(), C.c_int64()
@@ -166,9 +166,9 @@ def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
     capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, num_position_embeddings, dtype, _i32p(cu),
                                        _i32p(pos), _i32p(idx), _f32p(w)), "qvl_vision_metadata")
     nti = C.c_int64()
-    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, None, 0, C.byref(nti)), "qvl_attention_worklist")
-    tiles = np.zeros((max(nti.value, 1), 3), np.int32)
-    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, _i32p(tiles), nti.value, C.byref(nti)),
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, num_heads, None, 0, C.byref(nti)), "qvl_attention_worklist")
+    tiles = np.zeros((max(nti.value, 1), 4), np.int32)
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, num_heads, _i32p(tiles), nti.value, C.byref(nti)),
                "qvl_attention_worklist")
     return GridMetadata(N, cu, pos, idx, w, tiles[: nti.value])
 
@@ -298,10 +298,11 @@ class Qwen3VisionTransformer:
         hit = self._meta_cache.get(key)
         if hit is not None:
             return hit
-        m = grid_metadata(g, self.spec.spatial_merge_size, self.spec.num_position_embeddings, self.qdtype)
+        m = grid_metadata(g, self.spec.spatial_merge_size, self.spec.num_position_embeddings, self.qdtype,
+                          self.spec.num_heads)
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
         tens = {"cu_seqlens": dev(m.cu_seqlens), "pos_hw": dev(m.pos_hw), "tap_idx": dev(m.tap_idx),
-                "tap_w": dev(m.tap_w), "tiles": dev(m.tiles if len(m.tiles) else np.zeros((1, 3), np.int32))}
+                "tap_w": dev(m.tap_w), "tiles": dev(m.tiles if len(m.tiles) else np.zeros((1, 4), np.int32))}
         md = capi.VisionMetadataDev()
         md.n_tokens = m.n_tokens
         md.n_tiles = len(m.tiles)

@@ -60,9 +60,10 @@ def test_metadata_bit_exact_vs_oracle(pkg, grids):
 
 @pytest.mark.parametrize("grids", GRIDS)
 def test_worklist_covers_every_query_once(pkg, grids):
-    m = pkg.grid_metadata(grids)
-    ref = ix.attention_tiles(m.cu_seqlens, 128)
-    assert np.array_equal(m.tiles, ref)
+    for heads in (1, 16):
+        m = pkg.grid_metadata(grids, num_heads=heads)
+        ref = ix.attention_tiles(m.cu_seqlens, 128, heads)
+        assert np.array_equal(m.tiles, ref)
 
 
 def test_inv_freq_matches_oracle(pkg):
@@ -85,16 +86,24 @@ def test_rejects_bad_grids(pkg):
     lib = pkg.capi.load()
     cu = np.array([0, 8, 4], np.int32)
     n = C.c_int64()
-    rc = lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 2, None, 0, C.byref(n))
+    rc = lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 2, 1, None, 0, C.byref(n))
     assert rc == -1 and b"monotone" in lib.qvl_last_error()
+    rc = lib.qvl_attention_worklist(np.array([0, 4], np.int32).ctypes.data_as(C.POINTER(C.c_int32)), 1, 0, None, 0,
+                                    C.byref(n))
+    assert rc == -1 and b"num_heads" in lib.qvl_last_error()
 
 
 def test_empty_segments_are_skipped(pkg):
     lib = pkg.capi.load()
     cu = np.array([0, 0, 130, 130, 131], np.int32)
     n = C.c_int64()
-    assert lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 4, None, 0, C.byref(n)) == 0
-    assert n.value == 3   # 130 -> 2 tiles of 128, 1 -> 1 tile
+    assert lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 4, 1, None, 0, C.byref(n)) == 0
+    assert n.value == 16  # 130 -> 2 tiles of 128 in one queue, 1 -> 1 tile in another; 8 queues of 2 slots
+    items = np.zeros((n.value, 4), np.int32)
+    assert lib.qvl_attention_worklist(cu.ctypes.data_as(C.POINTER(C.c_int32)), 4, 1,
+                                      items.ctypes.data_as(C.POINTER(C.c_int32)), n.value, C.byref(n)) == 0
+    live = items[items[:, 1] > items[:, 0]]
+    assert sorted(map(tuple, live.tolist())) == [(0, 130, 0, 0), (0, 130, 128, 0), (130, 131, 130, 0)]
 
 
 def test_dense_argument_checks(pkg):

@@ -146,7 +146,7 @@ def test_rotary_table_vs_oracle(pkg, lib):
 
 def _attention_case(pkg, lib, grids, H=16, hd=64, seed=0, perturb=None):
     cp = pkg.capi
-    m = pkg.grid_metadata(grids)
+    m = pkg.grid_metadata(grids, num_heads=H)
     N, D = m.n_tokens, H * hd
     rng = np.random.default_rng(seed)
     qkv = vt.bf16_round(rng.standard_normal((N, 3 * D)).astype(np.float32))
@@ -156,7 +156,7 @@ def _attention_case(pkg, lib, grids, H=16, hd=64, seed=0, perturb=None):
     pos = torch.from_numpy(m.pos_hw).to(DEV)
     cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, device=DEV)
     cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
-    tiles = torch.from_numpy(m.tiles if len(m.tiles) else np.zeros((1, 3), np.int32)).to(DEV)
+    tiles = torch.from_numpy(m.tiles if len(m.tiles) else np.zeros((1, 4), np.int32)).to(DEV)
     nb = C.c_size_t()
     cp.check(lib.qvl_vision_attention_workspace_size(N, H, hd, C.byref(nb)))
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)

@@ -85,14 +85,30 @@ def test_rotary_half_table():
         np.testing.assert_allclose(tab, exp, rtol=2e-6, atol=0)
 
 
-def test_attention_tiles_cover_every_query_once():
+@pytest.mark.parametrize("heads", [1, 3, 16])
+def test_attention_tiles_cover_every_query_once(heads):
+    """Schedule invariants: every query row of every segment in exactly one item per head; a
+    (segment, head) group never spans two queues; each queue is longest-segment-first; padding
+    items are empty; queue work is balanced within one group's work (the greedy bound)."""
     cu = ix.cu_seqlens_ref([(1, 32, 32), (1, 24, 40), (1, 16, 16), (1, 48, 48), (1, 2, 2)])
     for bm in (64, 128, 256):
-        tiles = ix.attention_tiles(cu, bm)
-        seen = np.zeros(cu[-1], np.int32)
-        for s, e, q0 in tiles:
-            seen[q0:min(q0 + bm, e)] += 1
-            assert s <= q0 < e
+        items = ix.attention_tiles(cu, bm, heads)
+        assert len(items) % 8 == 0
+        seen = np.zeros((heads, cu[-1]), np.int32)
+        queue_of = {}
+        load = np.zeros(8, np.int64)
+        for k, (s, e, q0, h) in enumerate(items):
+            if e <= s:
+                assert (s, e, q0, h) == (0, 0, 0, 0)
+                continue
+            assert s <= q0 < e and 0 <= h < heads
+            seen[h, q0:min(q0 + bm, e)] += 1
+            assert queue_of.setdefault((s, h), k % 8) == k % 8
+            load[k % 8] += e - s
         assert (seen == 1).all()
-        lens = tiles[:, 1] - tiles[:, 0]
-        assert (np.diff(lens) <= 0).all()
+        for q in range(8):
+            lens = [e - s for (s, e, _, _) in items[q::8] if e > s]
+            assert all(a >= b for a, b in zip(lens, lens[1:]))
+        seg_len = np.diff(cu)
+        biggest = max(-(-L // bm) * L for L in seg_len)
+        assert load.max() - load.min() <= biggest
