@@ -17,6 +17,9 @@
  *     with n_out and k_in zero-padded to multiples of 64; biases and LayerNorm affine
  *     parameters are float32 vectors (holding bf16-representable values in the bf16 mode).
  *   - Token order is the reference's 2x2 merge-block order (sample.py:112-119).
+ *   - dtype: QVL_DTYPE_BF16 (bf16 storage and MFMA, fp32 accumulation / softmax / LayerNorm
+ *     statistics) or QVL_DTYPE_F32 (the reference's default dtype: fp32 storage and arithmetic,
+ *     fp32 MFMA); entries that exist for one of them only say so.
  */
 #ifndef QVL_VISION_H
 #define QVL_VISION_H
@@ -114,7 +117,7 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
                  void* d_workspace, size_t workspace_bytes);
 
 /* LayerNorm over the last axis: fp32 mean / biased variance / rsqrt(var + eps), affine, cast
- * back (model.py:375-388). cols must be a multiple of 8 and <= 8192. */
+ * back (model.py:375-388). cols must be a multiple of 8 and <= 8192. bf16 or fp32. */
 int qvl_layer_norm(void* stream, int32_t dtype, const void* d_x, int64_t ldx, const float* d_gamma,
                    const float* d_beta, void* d_y, int64_t ldy, int64_t rows, int64_t cols, float eps);
 
@@ -137,7 +140,7 @@ int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* d_pos_hw, int64
  * row stride ld_out. `d_tiles` / `n_tiles` are the qvl_attention_worklist items (device copy)
  * and their count.
  * Workspace: qvl_vision_attention_workspace_size(). head_dim in {64, 72}. */
-int qvl_vision_attention_workspace_size(int64_t n_tokens, int32_t num_heads, int32_t head_dim,
+int qvl_vision_attention_workspace_size(int32_t dtype, int64_t n_tokens, int32_t num_heads, int32_t head_dim,
                                         size_t* bytes);
 int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const void* d_k,
                          const void* d_v, int64_t ld_qkv, const void* d_cos_sin,
@@ -149,8 +152,9 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const voi
  * epilogue applies the 2D rotary to q and k with `d_cos_sin` and writes the head-major operands
  * of qvl_attention_headmajor: q (scaled by head_dim^-0.5 * log2(e)) and k as [H][Np][64],
  * v transposed as [H][64][Np], Np = n_tokens rounded up to 64 (rows [n_tokens, Np) zeroed).
- * head_dim must be 64 and D a multiple of 128. The optional workspace (qvl_dense_workspace_size
- * bytes, may be NULL) enables tail split-K as in qvl_dense_ws. */
+ * head_dim must be 64 and D a multiple of 128; bf16 only (the fp32 tower runs qvl_dense and
+ * qvl_vision_attention). The optional workspace (qvl_dense_workspace_size bytes, may be NULL)
+ * enables tail split-K as in qvl_dense_ws. */
 int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
                          const float* d_bias, const void* d_cos_sin, void* d_q, void* d_k, void* d_vt,
                          int64_t n_tokens, int64_t hidden, int32_t num_heads,
@@ -159,7 +163,8 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t l
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
  * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][80] (dims 72..79 zero) and
- * v^T [H][96][Np] (rows 72..95 zero), keys at the same quad-swapped positions. */
+ * v^T [H][96][Np] (rows 72..95 zero), keys at the same quad-swapped positions. fp32: q, k
+ * [H][Np][head_dim], v^T [H][32*ceil(head_dim/32)][Np] (extra rows zero), keys in order. */
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const void* d_k, const void* d_vt,
                             const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,
                             int32_t head_dim, void* d_out, int64_t ld_out);
@@ -181,7 +186,7 @@ typedef struct qvl_vision_config {
   int32_t deepstack_indexes[8];
   float ln_eps;                     /* 1e-6                                */
   float rope_theta;                 /* 10000                               */
-  int32_t dtype;                    /* QVL_DTYPE_BF16                      */
+  int32_t dtype;                    /* QVL_DTYPE_BF16 or QVL_DTYPE_F32     */
 } qvl_vision_config;
 
 typedef struct qvl_block_weights {           /* blocks_{i} (model.py:617-630)          */

@@ -69,7 +69,7 @@ SIGNATURES = {
     "qvl_layer_norm": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _f32]),
     "qvl_pos_embed": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64]),
     "qvl_rotary_table": (C.c_int, [_p, _i32, _p, _i64, _i32, _f32, _p]),
-    "qvl_vision_attention_workspace_size": (C.c_int, [_i64, _i32, _i32, C.POINTER(_sz)]),
+    "qvl_vision_attention_workspace_size": (C.c_int, [_i32, _i64, _i32, _i32, C.POINTER(_sz)]),
     "qvl_vision_attention": (C.c_int, [_p, _i32, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _i32,
                                        _p, _sz]),
     "qvl_dense_qkv_rotary": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _sz]),

@@ -169,9 +169,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
       m_run += sh;
       l_run *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
+      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; negm[r] = -m_run; }
     }
-    if (first || !EDGE) {
+    if (first) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) negm[r] = -m_run;
     }

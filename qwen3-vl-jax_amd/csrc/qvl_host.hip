@@ -233,8 +233,9 @@ int qvl_rotary_inv_freq(int32_t head_dim, float theta, float* inv) {
 // device stages
 // ---------------------------------------------------------------------------------------------
 int qvl_pack_dense_weight(void* stream, int32_t dtype, const float* w, int64_t k_in, int64_t n_out, void* out) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "pack: dtype %d", dtype);
+  if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_UNSUPPORTED, "pack: dtype %d", dtype);
   if (!w || !out || k_in <= 0 || n_out <= 0) return set_error(QVL_ERR_INVALID_ARG, "pack: bad args");
+  if (dtype == QVL_DTYPE_F32) return pack_weight_f32(w, k_in, n_out, (float*)out, (hipStream_t)stream);
   return pack_weight_bf16(w, k_in, n_out, (bf16*)out, (hipStream_t)stream);
 }
 
@@ -248,7 +249,7 @@ int qvl_cast(void* stream, int32_t dtype, const float* x, void* y, int64_t n) {
 static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
                       const float* bias, const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n,
                       int64_t k, void* ws, size_t ws_bytes) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense: dtype %d", dtype);
+  if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_UNSUPPORTED, "dense: dtype %d", dtype);
   if (epi < QVL_EPI_BIAS || epi > QVL_EPI_BIAS_RESIDUAL) return set_error(QVL_ERR_INVALID_ARG, "dense: epilogue %d", epi);
   if (m < 0 || n <= 0 || k <= 0) return set_error(QVL_ERR_INVALID_ARG, "dense: m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
   if (m == 0) return QVL_OK;
@@ -258,6 +259,19 @@ static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, i
     return set_error(QVL_ERR_INVALID_ARG, "dense: NULL operand");
   if (lda < k || ldc < n || (epi == QVL_EPI_BIAS_RESIDUAL && ldr < n))
     return set_error(QVL_ERR_INVALID_ARG, "dense: leading dimension too small");
+  if (dtype == QVL_DTYPE_F32) {
+    // fp32: x [m, lda], packed w [round_up(n, 64), k], y / res [m, ld] fp32, 16-byte rows
+    if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || lda % 4 || ldc % 4 ||
+        (epi == QVL_EPI_BIAS_RESIDUAL && (!aligned16(res) || ldr % 4)))
+      return set_error(QVL_ERR_MISALIGNED, "dense: fp32 operands must be 16-byte aligned (lda, ldc, ldr % 4 == 0)");
+    if (m * lda * 4 >= (int64_t)UINT32_MAX || round_up(n, 64) * k * 4 >= (int64_t)UINT32_MAX)
+      return set_error(QVL_ERR_UNSUPPORTED, "dense: operand larger than 4 GiB");
+    GemmF32Params p{};
+    p.x = (const float*)x; p.lda = lda; p.w = (const float*)w; p.ldw = k; p.n_rows_w = round_up(n, 64);
+    p.bias = bias; p.res = (const float*)res; p.ldr = ldr; p.y = (float*)y; p.ldc = ldc;
+    p.M = (int)m; p.N = (int)n; p.K = (int)k; p.Kp = (int)k;
+    return gemm_f32(p, epi, (hipStream_t)stream);
+  }
   if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || lda % 8 || ldc % 4 ||
       (epi == QVL_EPI_BIAS_RESIDUAL && (((uintptr_t)res & 7) || ldr % 4)) || (ws && !aligned16(ws)))
     return set_error(QVL_ERR_MISALIGNED, "dense: operands must be 16-byte aligned (lda % 8 == 0, ldc % 4 == 0)");
@@ -290,10 +304,15 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epi, const void* x, int64_
 
 int qvl_layer_norm(void* stream, int32_t dtype, const void* x, int64_t ldx, const float* g, const float* b, void* y,
                    int64_t ldy, int64_t rows, int64_t cols, float eps) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "layer_norm: dtype %d", dtype);
+  if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_UNSUPPORTED, "layer_norm: dtype %d", dtype);
   if (rows < 0 || cols <= 0 || cols % 8 || cols > 8192 || ldx < cols || ldy < cols)
     return set_error(QVL_ERR_INVALID_ARG, "layer_norm: rows=%lld cols=%lld", (long long)rows, (long long)cols);
   if (!x || !g || !b || !y) return set_error(QVL_ERR_INVALID_ARG, "layer_norm: NULL operand");
+  if (dtype == QVL_DTYPE_F32) {
+    if (!aligned16(x) || !aligned16(y) || !aligned16(g) || !aligned16(b) || ldx % 4 || ldy % 4)
+      return set_error(QVL_ERR_MISALIGNED, "layer_norm: operands must be 16-byte aligned");
+    return layer_norm_f32((const float*)x, ldx, g, b, (float*)y, ldy, (int)rows, (int)cols, eps, (hipStream_t)stream);
+  }
   if (!aligned16(x) || !aligned16(y) || !aligned16(g) || !aligned16(b) || ldx % 8 || ldy % 8)
     return set_error(QVL_ERR_MISALIGNED, "layer_norm: operands must be 16-byte aligned");
   return layer_norm_bf16((const bf16*)x, ldx, g, b, (bf16*)y, ldy, (int)rows, (int)cols, eps, (hipStream_t)stream);
@@ -301,10 +320,12 @@ int qvl_layer_norm(void* stream, int32_t dtype, const void* x, int64_t ldx, cons
 
 int qvl_pos_embed(void* stream, int32_t dtype, const void* table, const int32_t* idx, const float* w, void* y,
                   int64_t n_tokens, int64_t dim) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "pos_embed: dtype %d", dtype);
+  if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_UNSUPPORTED, "pos_embed: dtype %d", dtype);
   if (n_tokens < 0 || dim <= 0 || dim % 8) return set_error(QVL_ERR_INVALID_ARG, "pos_embed: dim=%lld", (long long)dim);
   if (!table || !idx || !w || !y) return set_error(QVL_ERR_INVALID_ARG, "pos_embed: NULL operand");
   if (!aligned16(table) || !aligned16(y)) return set_error(QVL_ERR_MISALIGNED, "pos_embed: operands must be 16-byte aligned");
+  if (dtype == QVL_DTYPE_F32)
+    return pos_embed_f32((const float*)table, idx, w, (float*)y, (int)n_tokens, (int)dim, (hipStream_t)stream);
   return pos_embed_bf16((const bf16*)table, idx, w, (bf16*)y, (int)n_tokens, (int)dim, (hipStream_t)stream);
 }
 
@@ -320,28 +341,34 @@ int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* pos_hw, int64_t
 
 static int64_t attn_np(int64_t n) { return round_up(std::max<int64_t>(n, 1), 64); }
 
-// Head-major attention operand geometry: Q/K rows of `hdp` dims, V^T of `vrows` rows.
-static int attn_dims(int hd, int* hdp, int* vrows) {
-  if (hd == 64) { *hdp = 64; *vrows = 64; return QVL_OK; }
-  if (hd == 72) { *hdp = 80; *vrows = 96; return QVL_OK; }
-  return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
+// Head-major attention operand geometry: Q/K rows of `hdp` dims, V^T of `vrows` rows. bf16
+// pads head_dim 72 to 80 (Q/K) and 96 (V^T); fp32 keeps Q/K exact and pads V^T to 32-row blocks.
+static int attn_dims(int dtype, int hd, int* hdp, int* vrows) {
+  if (hd != 64 && hd != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
+  if (dtype == QVL_DTYPE_F32) { *hdp = hd; *vrows = (int)round_up(hd, 32); return QVL_OK; }
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
+  *hdp = hd == 64 ? 64 : 80;
+  *vrows = hd == 64 ? 64 : 96;
+  return QVL_OK;
 }
 
-int qvl_vision_attention_workspace_size(int64_t n_tokens, int32_t num_heads, int32_t head_dim, size_t* bytes) {
+static size_t dtype_size(int dtype) { return dtype == QVL_DTYPE_F32 ? 4 : 2; }
+
+int qvl_vision_attention_workspace_size(int32_t dtype, int64_t n_tokens, int32_t num_heads, int32_t head_dim,
+                                        size_t* bytes) {
   if (!bytes || n_tokens < 0 || num_heads <= 0) return set_error(QVL_ERR_INVALID_ARG, "attention ws: bad args");
   int hdp, vrows;
-  int rc = attn_dims(head_dim, &hdp, &vrows);
+  int rc = attn_dims(dtype, head_dim, &hdp, &vrows);
   if (rc) return rc;
-  *bytes = (size_t)num_heads * attn_np(n_tokens) * (2 * hdp + vrows) * sizeof(bf16);
+  *bytes = (size_t)num_heads * attn_np(n_tokens) * (2 * hdp + vrows) * dtype_size(dtype);
   return QVL_OK;
 }
 
 int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void* k, const void* v, int64_t ld,
                          const void* cs, const int32_t* tiles, int64_t n_tiles, void* out, int64_t ld_out,
                          int64_t n_tokens, int32_t H, int32_t hd, void* ws, size_t ws_bytes) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
   size_t need = 0;
-  int rc = qvl_vision_attention_workspace_size(n_tokens, H, hd, &need);
+  int rc = qvl_vision_attention_workspace_size(dtype, n_tokens, H, hd, &need);
   if (rc) return rc;
   if (ws_bytes < need || !ws) return set_error(QVL_ERR_WORKSPACE, "attention: workspace %zu < %zu", ws_bytes, need);
   if (n_tokens == 0) return QVL_OK;
@@ -351,7 +378,18 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void*
   if (((uintptr_t)out & 7) || !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "attention: alignment");
   const int64_t Np = attn_np(n_tokens);
   int hdp, vrows;
-  attn_dims(hd, &hdp, &vrows);
+  attn_dims(dtype, hd, &hdp, &vrows);
+  if (dtype == QVL_DTYPE_F32) {
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || ld % 4 || !aligned16(out))
+      return set_error(QVL_ERR_MISALIGNED, "attention: fp32 operands must be 16-byte aligned");
+    float* Qf = (float*)ws;
+    float* Kf = Qf + (size_t)H * Np * hdp;
+    float* Vf = Kf + (size_t)H * Np * hdp;
+    rc = attention_relayout_f32((const float*)q, (const float*)k, (const float*)v, ld, (const f32x2*)cs, (int)n_tokens,
+                                (int)Np, H, hd, vrows, (1.0f / sqrtf((float)hd)) * kLog2e, Qf, Kf, Vf, (hipStream_t)stream);
+    if (rc) return rc;
+    return attention_f32(Qf, Kf, Vf, tiles, n_tiles, (int)Np, hd, (float*)out, ld_out, (hipStream_t)stream);
+  }
   bf16* Qb = (bf16*)ws;
   bf16* Kb = Qb + (size_t)H * Np * hdp;
   bf16* Vb = Kb + (size_t)H * Np * hdp;
@@ -394,15 +432,19 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
                             const int32_t* tiles, int64_t n_tiles, int64_t n_tokens, int32_t H, int32_t hd, void* out,
                             int64_t ld_out) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
   int hdp, vrows;
-  int rc = attn_dims(hd, &hdp, &vrows);
+  int rc = attn_dims(dtype, hd, &hdp, &vrows);
   if (rc) return rc;
   if (n_tokens < 0 || H <= 0 || n_tiles < 0 || ld_out < (int64_t)H * hd || ld_out % 4)
     return set_error(QVL_ERR_INVALID_ARG, "attention: bad sizes");
   if (n_tokens == 0 || n_tiles == 0) return QVL_OK;
   if (!q || !k || !vt || !tiles || !out) return set_error(QVL_ERR_INVALID_ARG, "attention: NULL operand");
   if ((uintptr_t)out & 7) return set_error(QVL_ERR_MISALIGNED, "attention: out alignment");
+  if (dtype == QVL_DTYPE_F32) {
+    if (!aligned16(out) || ld_out % 4) return set_error(QVL_ERR_MISALIGNED, "attention: fp32 out alignment");
+    return attention_f32((const float*)q, (const float*)k, (const float*)vt, tiles, n_tiles, (int)attn_np(n_tokens), hd,
+                         (float*)out, ld_out, (hipStream_t)stream);
+  }
   if (hd == 64)
     return attention_hd64((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, (int)attn_np(n_tokens), H,
                           (bf16*)out, ld_out, (hipStream_t)stream);
@@ -414,6 +456,8 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const vo
 // whole tower
 // ---------------------------------------------------------------------------------------------
 struct TowerLayout {
+  int dtype;
+  size_t esz;
   int64_t N, Np, D, I_pad, PV, hd, H;
   int hdp, vrows;
   size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, total;
@@ -421,33 +465,39 @@ struct TowerLayout {
 
 static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   if (!c) return set_error(QVL_ERR_INVALID_ARG, "config is NULL");
-  if (c->dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: dtype %d", c->dtype);
+  if (c->dtype != QVL_DTYPE_BF16 && c->dtype != QVL_DTYPE_F32)
+    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: dtype %d", c->dtype);
   if (c->spatial_merge_size != 2) return set_error(QVL_ERR_UNSUPPORTED, "spatial_merge_size=%d", c->spatial_merge_size);
   if (c->num_heads <= 0 || c->hidden_size % c->num_heads) return set_error(QVL_ERR_INVALID_ARG, "hidden/heads");
   const int64_t hd = c->hidden_size / c->num_heads;
   int hdp, vrows;
-  QVL_TRY_RC(attn_dims((int)hd, &hdp, &vrows));
+  QVL_TRY_RC(attn_dims(c->dtype, (int)hd, &hdp, &vrows));
   if (c->hidden_size % 64 || c->patch_volume % 64 || c->out_hidden_size % 64)
     return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden, patch_volume and out_hidden_size must be multiples of 64");
-  if (hd == 64 && c->hidden_size % 128)
+  if (c->dtype == QVL_DTYPE_BF16 && hd == 64 && c->hidden_size % 128)
     return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden %% 128 != 0 with head_dim 64");
   if (c->n_deepstack < 0 || c->n_deepstack > 8) return set_error(QVL_ERR_INVALID_ARG, "n_deepstack=%d", c->n_deepstack);
   if (N % 4) return set_error(QVL_ERR_INVALID_ARG, "n_tokens=%lld not a multiple of 4", (long long)N);
+  L->dtype = c->dtype;
+  L->esz = dtype_size(c->dtype);
   L->N = N; L->Np = attn_np(N); L->D = c->hidden_size; L->I_pad = round_up(c->intermediate_size, 64);
   L->PV = c->patch_volume; L->hd = hd; L->H = c->num_heads; L->hdp = hdp; L->vrows = vrows;
-  // h hosts the bf16 pixels, the MLP hidden, the merger hidden and (head_dim != 64) the qkv output.
+  const bool fused_qkv = c->dtype == QVL_DTYPE_BF16 && hd == 64;
+  // h hosts the bf16 pixels, the MLP hidden, the merger hidden and (unless the qkv GEMM writes
+  // head-major operands itself) the qkv output.
   int64_t hcols = std::max<int64_t>({L->I_pad, L->PV, (int64_t)c->hidden_size});
-  if (hd != 64) hcols = std::max<int64_t>(hcols, 3 * (int64_t)c->hidden_size);
+  if (!fused_qkv) hcols = std::max<int64_t>(hcols, 3 * (int64_t)c->hidden_size);
+  const size_t e = L->esz;
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t r = o; o += round_up((int64_t)bytes, 256); return r; };
-  L->off_x = take((size_t)N * L->D * 2);
-  L->off_xn = take((size_t)N * L->D * 2);
-  L->off_q = take((size_t)L->H * L->Np * hdp * 2);
-  L->off_k = take((size_t)L->H * L->Np * hdp * 2);
-  L->off_vt = take((size_t)L->H * L->Np * vrows * 2);
-  L->off_h = take((size_t)N * hcols * 2);
+  L->off_x = take((size_t)N * L->D * e);
+  L->off_xn = take((size_t)N * L->D * e);
+  L->off_q = take((size_t)L->H * L->Np * hdp * e);
+  L->off_k = take((size_t)L->H * L->Np * hdp * e);
+  L->off_vt = take((size_t)L->H * L->Np * vrows * e);
+  L->off_h = take((size_t)N * hcols * e);
   L->off_cs = take((size_t)N * (hd / 2) * 8);
-  L->part_bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);
+  L->part_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float) : 0;
   L->off_part = take(L->part_bytes);
   L->total = o;
   return QVL_OK;
@@ -466,16 +516,17 @@ int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tok
 // VisionPatchMerger.__call__ (model.py:648-656): main (LN over D then view [N/4, 4D]) or
 // deepstack (view [N/4, 4D] then LN over 4D); fc1 + GELU-tanh; fc2.
 static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLayout& L, const qvl_merger_weights& mw,
-                      bool postshuffle, const bf16* x, bf16* xn, bf16* h, void* out, void* part) {
+                      bool postshuffle, const void* x, void* xn, void* h, void* out, void* part) {
   const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
+  const int dt = L.dtype;
   if (postshuffle)
-    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
+    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
   else
-    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
-  QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4,
-                          D4, part, L.part_bytes));
-  QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out,
-                          c->out_hidden_size, N / 4, c->out_hidden_size, D4, part, L.part_bytes));
+    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
+  QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4,
+                          part, L.part_bytes));
+  QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out, c->out_hidden_size, N / 4,
+                          c->out_hidden_size, D4, part, L.part_bytes));
   return QVL_OK;
 }
 
@@ -491,51 +542,61 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   if (!px || !tokens || (c->n_deepstack > 0 && !deepstack)) return set_error(QVL_ERR_INVALID_ARG, "encode_vision: NULL io");
   if (!W->blocks || (c->n_deepstack > 0 && !W->deepstack)) return set_error(QVL_ERR_INVALID_ARG, "encode_vision: NULL weight arrays");
   hipStream_t st = (hipStream_t)stream;
+  const int dt = L.dtype;
+  const bool f32 = dt == QVL_DTYPE_F32;
   char* base = (char*)ws;
-  bf16* x = (bf16*)(base + L.off_x);
-  bf16* xn = (bf16*)(base + L.off_xn);
-  bf16* Qb = (bf16*)(base + L.off_q);
-  bf16* Kb = (bf16*)(base + L.off_k);
-  bf16* Vb = (bf16*)(base + L.off_vt);
-  bf16* h = (bf16*)(base + L.off_h);
+  char* x = base + L.off_x;
+  char* xn = base + L.off_xn;
+  char* Qb = base + L.off_q;
+  char* Kb = base + L.off_k;
+  char* Vb = base + L.off_vt;
+  char* h = base + L.off_h;
   f32x2* cs = (f32x2*)(base + L.off_cs);
-  void* part = base + L.off_part;
+  void* part = L.part_bytes ? base + L.off_part : nullptr;
   const size_t PB = L.part_bytes;
   const int64_t N = L.N, D = L.D, I = L.I_pad;
+  const size_t e = L.esz;
+  const float qscale = (1.0f / sqrtf((float)L.hd)) * kLog2e;
 
-  // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823)
-  QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
-  QVL_TRY_RC(qvl_rotary_table(st, QVL_DTYPE_BF16, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
-  QVL_TRY_RC(qvl_pos_embed(st, QVL_DTYPE_BF16, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
-  QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
-                          L.PV, part, PB));
+  // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823); in fp32 the
+  // pixels feed the GEMM directly
+  const void* px_in = px;
+  if (!f32) {
+    QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
+    px_in = h;
+  }
+  QVL_TRY_RC(qvl_rotary_table(st, dt, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
+  QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
+  QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV,
+                          part, PB));
 
   int ds_next = 0;
   for (int i = 0; i < c->depth; ++i) {
     const qvl_block_weights& B = W->blocks[i];
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
-    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
-    if (L.hd == 64) {
+    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
+    if (!f32 && L.hd == 64) {
       // qkv Dense with rotary + head-major relayout fused into its epilogue.
-      QVL_TRY_RC(qvl_dense_qkv_rotary(st, QVL_DTYPE_BF16, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H,
-                                      part, PB));
+      QVL_TRY_RC(qvl_dense_qkv_rotary(st, dt, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
     } else {
-      // qkv Dense into h, then rotary + relayout (head_dim 72 pads Q/K to 80 dims, V^T to 96 rows).
-      QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D,
-                              D, part, PB));
-      QVL_TRY_RC(attention_relayout_general(h, h + D, h + 2 * D, 3 * D, cs, (int)N, (int)L.Np, (int)L.H, (int)L.hd,
-                                           L.hdp, L.vrows, (1.0f / sqrtf((float)L.hd)) * kLog2e, Qb, Kb, Vb, st));
+      // qkv Dense into h, then rotary + head-major relayout.
+      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D, D, part,
+                              PB));
+      if (f32)
+        QVL_TRY_RC(attention_relayout_f32((const float*)h, (const float*)h + D, (const float*)h + 2 * D, 3 * D, cs,
+                                          (int)N, (int)L.Np, (int)L.H, (int)L.hd, L.vrows, qscale, (float*)Qb,
+                                          (float*)Kb, (float*)Vb, st));
+      else
+        QVL_TRY_RC(attention_relayout_general((const bf16*)h, (const bf16*)h + D, (const bf16*)h + 2 * D, 3 * D, cs,
+                                              (int)N, (int)L.Np, (int)L.H, (int)L.hd, L.hdp, L.vrows, qscale,
+                                              (bf16*)Qb, (bf16*)Kb, (bf16*)Vb, st));
     }
-    QVL_TRY_RC(qvl_attention_headmajor(st, QVL_DTYPE_BF16, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H,
-                                       (int)L.hd, xn, D));
-    QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D,
-                            part, PB));
+    QVL_TRY_RC(qvl_attention_headmajor(st, dt, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H, (int)L.hd, xn, D));
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, part, PB));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
-    QVL_TRY_RC(qvl_layer_norm(st, QVL_DTYPE_BF16, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
-    QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D,
-                            part, PB));
-    QVL_TRY_RC(qvl_dense_ws(st, QVL_DTYPE_BF16, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I,
-                            part, PB));
+    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D, part, PB));
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I, part, PB));
     // deepstack tap (model.py:841-843)
     for (int j = 0; j < c->n_deepstack; ++j)
       if (c->deepstack_indexes[j] == i) {
@@ -543,6 +604,7 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
         ++ds_next;
       }
   }
+  (void)e;
   QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, tokens, part));
   return QVL_OK;
 }

@@ -1,5 +1,7 @@
 // Launchers of the gfx950 kernels (each .hip file defines its own), shared with the host entries.
 #pragma once
+#include <algorithm>
+
 #include "qvl_common.h"
 
 namespace qvl {
@@ -23,6 +25,16 @@ struct GemmParams {
   float* part;
   int64_t part_elems;
   int full_tiles, split;
+};
+
+// fp32 GEMM (qvl_f32.hip): w packed [n_rows_w][ldw] fp32 (ldw = k padded to 64), Kp = ldw.
+struct GemmF32Params {
+  const float* x; int64_t lda;
+  const float* w; int64_t ldw; int64_t n_rows_w;
+  const float* bias;
+  const float* res; int64_t ldr;   // residual, may alias y
+  float* y; int64_t ldc;
+  int M, N, K, Kp;
 };
 
 // Floats of split-K partial workspace that lets every GEMM of up to 256x256 tiles split its tail
@@ -56,6 +68,17 @@ int pos_embed_bf16(const bf16* table, const int* idx, const float* wts, bf16* y,
 int rotary_table(const int* pos_hw, int n_tok, int head_dim, const float* inv_freq, int round16, f32x2* cs,
                  hipStream_t stream);
 int cast_f32_bf16(const float* x, bf16* y, int64_t n, hipStream_t stream);
+int gemm_f32(const GemmF32Params& p, int epi, hipStream_t stream);
+int layer_norm_f32(const float* x, int64_t ldx, const float* g, const float* b, float* y, int64_t ldy, int rows,
+                   int cols, float eps, hipStream_t stream);
+int pos_embed_f32(const float* table, const int* idx, const float* wts, float* y, int n_tok, int dim,
+                  hipStream_t stream);
+int pack_weight_f32(const float* w, int64_t k_in, int64_t n_out, float* out, hipStream_t stream);
+int attention_relayout_f32(const float* q, const float* k, const float* v, int64_t ld, const f32x2* cs, int N, int Np,
+                           int H, int hd, int vrows, float qscale, float* Qo, float* Ko, float* Vto,
+                           hipStream_t stream);
+int attention_f32(const float* Qb, const float* Kb, const float* Vtb, const int* d_items, int64_t n_items, int Np,
+                  int hd, float* out, int64_t ldo, hipStream_t stream);
 int pack_weight_bf16(const float* w, int64_t k_in, int64_t n_out, bf16* out, hipStream_t stream);
 
 }  // namespace qvl

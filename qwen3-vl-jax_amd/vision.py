@@ -7,7 +7,7 @@ Mirrors /root/reference/model.py:
   Qwen3VLModel.encode_vision    940-944  `apply({"params": params}, pixel_values, grid_thw, method="encode_vision")`
 
 Parameters use the reference's Flax tree (`{"visual": {"patch_embed": {"proj": {"kernel", "bias"}}, ...}}`,
-kernels [in, out]); they are packed once onto the device ([out, in] bf16, zero-padded to 64) when
+kernels [in, out]); they are packed once onto the device ([out, in] in the tower dtype, zero-padded to 64) when
 the tower is bound to them. torch supplies device memory and the stream; every computation is a
 libqvl kernel launched through the C ABI (no torch math on the product path).
 """
@@ -185,13 +185,13 @@ class Qwen3VisionTransformer:
     `tokens, deepstack = tower(pixel_values, grid_thw)`."""
 
     def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0"):
-        if dtype != "bfloat16":
-            raise NotImplementedError("this build runs the tower in bfloat16 only")
+        if dtype not in ("bfloat16", "float32"):
+            raise NotImplementedError(f"dtype {dtype!r}: the tower runs in bfloat16 or float32")
         if spec.spatial_merge_size != 2:
             raise NotImplementedError("spatial_merge_size must be 2")
         self.spec = spec
         self.dtype = dtype
-        self.qdtype = capi.QVL_DTYPE_BF16
+        self.qdtype = capi.QVL_DTYPE_BF16 if dtype == "bfloat16" else capi.QVL_DTYPE_F32
         self.device = device
         self._lib = capi.load()
         self._w = None
@@ -222,25 +222,35 @@ class Qwen3VisionTransformer:
     def _stream(self):
         return _torch().cuda.current_stream().cuda_stream
 
+    def _tdtype(self):
+        """torch dtype of the tower's activations, packed weights and outputs."""
+        torch = _torch()
+        return torch.bfloat16 if self.qdtype == capi.QVL_DTYPE_BF16 else torch.float32
+
+    def _round(self, t):
+        """Values as the tower dtype holds them (bf16 rounding in the bf16 mode), kept in fp32."""
+        torch = _torch()
+        return t.to(torch.bfloat16).to(torch.float32) if self.qdtype == capi.QVL_DTYPE_BF16 else t
+
     def _pack_dense(self, p):
         torch = _torch()
         k = np.ascontiguousarray(np.asarray(p["kernel"], np.float32))
         kin, nout = k.shape
         kp, npad = -(-kin // 64) * 64, -(-nout // 64) * 64
         src = torch.from_numpy(k).to(self.device)
-        out = torch.empty((npad, kp), dtype=torch.bfloat16, device=self.device)
+        out = torch.empty((npad, kp), dtype=self._tdtype(), device=self.device)
         capi.check(self._lib.qvl_pack_dense_weight(self._stream(), self.qdtype, src.data_ptr(), kin, nout,
                                                    out.data_ptr()), "qvl_pack_dense_weight")
         b = np.zeros(npad, np.float32)
         b[:nout] = np.asarray(p["bias"], np.float32)
-        bias = torch.from_numpy(b).to(self.device).to(torch.bfloat16).to(torch.float32)
+        bias = self._round(torch.from_numpy(b).to(self.device))
         self._keep += [out, bias]
         return out, bias
 
     def _vec(self, v):
         torch = _torch()
         t = torch.from_numpy(np.ascontiguousarray(np.asarray(v, np.float32))).to(self.device)
-        t = t.to(torch.bfloat16).to(torch.float32)      # LayerNorm params live in the tower dtype
+        t = self._round(t)                                # LayerNorm params live in the tower dtype
         self._keep.append(t)
         return t
 
@@ -254,7 +264,7 @@ class Qwen3VisionTransformer:
         pw, pb = self._pack_dense(v["patch_embed"]["proj"])
         W.patch_w, W.patch_b = pw.data_ptr(), pb.data_ptr()
         tab = torch.from_numpy(np.ascontiguousarray(v["pos_embed"]["embedding"], np.float32)).to(self.device)
-        tab = tab.to(torch.bfloat16).contiguous()
+        tab = tab.to(self._tdtype()).contiguous()
         self._keep.append(tab)
         W.pos_table = tab.data_ptr()
         blocks = (capi.BlockWeights * s.depth)()
@@ -335,8 +345,8 @@ class Qwen3VisionTransformer:
         if tuple(px.shape) != (N, self.spec.patch_volume):
             raise ValueError(f"pixel_values shape {tuple(px.shape)} != ({N}, {self.spec.patch_volume})")
         s = self.spec
-        tokens = torch.empty((N // 4, s.out_hidden_size), dtype=torch.bfloat16, device=self.device)
-        ds = [torch.empty((N // 4, s.out_hidden_size), dtype=torch.bfloat16, device=self.device)
+        tokens = torch.empty((N // 4, s.out_hidden_size), dtype=self._tdtype(), device=self.device)
+        ds = [torch.empty((N // 4, s.out_hidden_size), dtype=self._tdtype(), device=self.device)
               for _ in s.deepstack_visual_indexes]
         ds_ptrs = (C.c_void_p * max(len(ds), 1))(*[t.data_ptr() for t in ds])
         ws, nbytes = self.workspace(N)
@@ -354,19 +364,19 @@ class Qwen3VisionTransformer:
         N, D, H, hd = m.n_tokens, s.hidden_size, s.num_heads, s.head_dim
         I = -(-s.intermediate_size // 64) * 64
         dev = dict(device=self.device)
-        bf = torch.bfloat16
+        bf = self._tdtype()
         cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, **dev)
         capi.check(self._lib.qvl_rotary_table(self._stream(), self.qdtype, tens["pos_hw"].data_ptr(), N, hd, 10000.0,
                                               cs.data_ptr()), "qvl_rotary_table")
         nb = C.c_size_t()
-        capi.check(self._lib.qvl_vision_attention_workspace_size(N, H, hd, C.byref(nb)), "attention ws")
+        capi.check(self._lib.qvl_vision_attention_workspace_size(self.qdtype, N, H, hd, C.byref(nb)), "attention ws")
         return dict(m=m, tens=tens, md=md, N=N, D=D, H=H, hd=hd, I=I, cs=cs, aws_bytes=nb.value,
                     aws=torch.empty(max(nb.value, 256), dtype=torch.uint8, **dev),
                     xn=torch.empty((N, D), dtype=bf, **dev), qkv=torch.empty((N, 3 * D), dtype=bf, **dev),
                     o=torch.empty((N, D), dtype=bf, **dev), h=torch.empty((N, I), dtype=bf, **dev))
 
     def block_staged(self, i: int, x, ctx) -> None:
-        """VisionBlock i (model.py:627-630) applied in place to the bf16 residual stream x [N, D],
+        """VisionBlock i (model.py:627-630) applied in place to the residual stream x [N, D],
         one C-ABI stage entry per reference op (qkv Dense, rotary + varlen attention, proj Dense +
         residual, LayerNorms, fc1 + GELU, fc2 + residual)."""
         lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
@@ -376,7 +386,8 @@ class Qwen3VisionTransformer:
         ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
         ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS, xn.data_ptr(), D, B.qkv_w, B.qkv_b, None, 0, qkv.data_ptr(),
                          3 * D, N, 3 * D, D), "qkv")
-        ck(lib.qvl_vision_attention(st, dt, qkv.data_ptr(), qkv.data_ptr() + 2 * D, qkv.data_ptr() + 4 * D, 3 * D,
+        esz = qkv.element_size()
+        ck(lib.qvl_vision_attention(st, dt, qkv.data_ptr(), qkv.data_ptr() + esz * D, qkv.data_ptr() + 2 * esz * D, 3 * D,
                                     ctx["cs"].data_ptr(), ctx["tens"]["tiles"].data_ptr(), ctx["md"].n_tiles,
                                     o.data_ptr(), D, N, H, hd, ctx["aws"].data_ptr(), ctx["aws_bytes"]), "attention")
         ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D,
@@ -397,23 +408,24 @@ class Qwen3VisionTransformer:
         D4 = 4 * D
         mw = self._w.merger if which < 0 else self._ds_arr[which]
         dev = dict(device=self.device)
-        xm = torch.empty((N // 4, D4), dtype=torch.bfloat16, **dev)
+        xm = torch.empty((N // 4, D4), dtype=self._tdtype(), **dev)
         if which >= 0:
             ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D4, mw.norm_w, mw.norm_b, xm.data_ptr(), D4, N // 4, D4,
                                   1e-6), "merger ln")
         else:
             ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, mw.norm_w, mw.norm_b, xm.data_ptr(), D, N, D, 1e-6),
                "merger ln")
-        hm = torch.empty((N // 4, D4), dtype=torch.bfloat16, **dev)
+        hm = torch.empty((N // 4, D4), dtype=self._tdtype(), **dev)
         ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_GELU, xm.data_ptr(), D4, mw.fc1_w, mw.fc1_b, None, 0, hm.data_ptr(),
                          D4, N // 4, D4, D4), "merger fc1")
-        out = torch.empty((N // 4, s.out_hidden_size), dtype=torch.bfloat16, **dev)
+        out = torch.empty((N // 4, s.out_hidden_size), dtype=self._tdtype(), **dev)
         ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS, hm.data_ptr(), D4, mw.fc2_w, mw.fc2_b, None, 0, out.data_ptr(),
                          s.out_hidden_size, N // 4, s.out_hidden_size, D4), "merger fc2")
         return out
 
     def embed_staged(self, pixel_values, ctx):
-        """Patch embed + learned pos-embed (model.py:802-806) via qvl_cast / qvl_pos_embed / qvl_dense."""
+        """Patch embed + learned pos-embed (model.py:802-806) via qvl_cast (bf16) / qvl_pos_embed /
+        qvl_dense."""
         torch = _torch()
         lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
         N, D = ctx["N"], ctx["D"]
@@ -422,12 +434,15 @@ class Qwen3VisionTransformer:
             np.ascontiguousarray(np.asarray(pixel_values, np.float32)))
         px = px.to(device=self.device, dtype=torch.float32).contiguous()
         W = self._w
-        x16 = torch.empty((N, s.patch_volume), dtype=torch.bfloat16, device=self.device)
-        ck(lib.qvl_cast(st, dt, px.data_ptr(), x16.data_ptr(), px.numel()), "qvl_cast")
-        pos = torch.empty((N, D), dtype=torch.bfloat16, device=self.device)
+        if self.qdtype == capi.QVL_DTYPE_BF16:
+            x16 = torch.empty((N, s.patch_volume), dtype=torch.bfloat16, device=self.device)
+            ck(lib.qvl_cast(st, dt, px.data_ptr(), x16.data_ptr(), px.numel()), "qvl_cast")
+        else:
+            x16 = px
+        pos = torch.empty((N, D), dtype=self._tdtype(), device=self.device)
         ck(lib.qvl_pos_embed(st, dt, W.pos_table, ctx["tens"]["tap_idx"].data_ptr(), ctx["tens"]["tap_w"].data_ptr(),
                              pos.data_ptr(), N, D), "qvl_pos_embed")
-        x = torch.empty((N, D), dtype=torch.bfloat16, device=self.device)
+        x = torch.empty((N, D), dtype=self._tdtype(), device=self.device)
         ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, x16.data_ptr(), s.patch_volume, W.patch_w, W.patch_b,
                          pos.data_ptr(), D, x.data_ptr(), D, N, D, s.patch_volume), "qvl_dense(patch)")
         return x

@@ -117,8 +117,14 @@ def test_dense_argument_checks(pkg):
     # residual epilogue without residual
     assert lib.qvl_dense(None, cp.QVL_DTYPE_BF16, 2, fake, 64, fake, fake, None, 64, fake, 64, 8, 64, 64) == -1
     # unsupported dtype
-    assert lib.qvl_dense(None, cp.QVL_DTYPE_F32, 0, fake, 64, fake, fake, None, 0, fake, 64, 8, 64, 64) == -2
+    assert lib.qvl_dense(None, 7, 0, fake, 64, fake, fake, None, 0, fake, 64, 8, 64, 64) == -2
+    # fp32: rows must be 16-byte aligned (lda % 4)
+    assert lib.qvl_dense(None, cp.QVL_DTYPE_F32, 0, fake, 66, fake, fake, None, 0, fake, 64, 8, 64, 64) == -3
     assert lib.qvl_layer_norm(None, cp.QVL_DTYPE_BF16, fake, 100, fake, fake, fake, 100, 4, 100, 1e-6) == -1
+    assert lib.qvl_layer_norm(None, cp.QVL_DTYPE_F32, fake + 4, 64, fake, fake, fake, 64, 4, 64, 1e-6) == -3
+    # the fp32 tower runs qvl_dense + qvl_vision_attention; the fused qkv+rotary entry is bf16 only
+    assert lib.qvl_dense_qkv_rotary(None, cp.QVL_DTYPE_F32, fake, 1024, fake, fake, fake, fake, fake, fake, 64, 1024,
+                                    16, None, 0) == -2
 
 
 def test_workspace_sizes(pkg):
@@ -133,5 +139,17 @@ def test_workspace_sizes(pkg):
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == 0
     assert 200e6 < nb.value < 600e6
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18430, C.byref(nb)) == -1   # not a multiple of 4
+    bf16_bytes = nb.value
+    cfg.dtype = pkg.capi.QVL_DTYPE_F32        # fp32 activations, no split-K partials
+    assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == 0
+    assert 1.5 * bf16_bytes < nb.value < 2.5 * bf16_bytes
+    cfg.dtype = 5
+    assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == -2
+    cfg.dtype = pkg.capi.QVL_DTYPE_BF16
     cfg.spatial_merge_size = 3
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == -2
+    for dt, hd, want in ((pkg.capi.QVL_DTYPE_BF16, 72, 16 * 64 * (80 + 80 + 96) * 2),
+                         (pkg.capi.QVL_DTYPE_F32, 72, 16 * 64 * (72 + 72 + 96) * 4),
+                         (pkg.capi.QVL_DTYPE_F32, 64, 16 * 64 * (64 + 64 + 64) * 4)):
+        assert lib.qvl_vision_attention_workspace_size(dt, 10, 16, hd, C.byref(nb)) == 0
+        assert nb.value == want

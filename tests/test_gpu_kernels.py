@@ -158,7 +158,7 @@ def _attention_case(pkg, lib, grids, H=16, hd=64, seed=0, perturb=None):
     cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
     tiles = torch.from_numpy(m.tiles if len(m.tiles) else np.zeros((1, 4), np.int32)).to(DEV)
     nb = C.c_size_t()
-    cp.check(lib.qvl_vision_attention_workspace_size(N, H, hd, C.byref(nb)))
+    cp.check(lib.qvl_vision_attention_workspace_size(cp.QVL_DTYPE_BF16, N, H, hd, C.byref(nb)))
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
     out = torch.full((N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
     cp.check(lib.qvl_vision_attention(stream(), cp.QVL_DTYPE_BF16, qkv_t.data_ptr(), qkv_t.data_ptr() + 2 * D,
