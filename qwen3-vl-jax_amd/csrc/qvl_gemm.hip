@@ -109,90 +109,31 @@ __device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n,
   }
 }
 
-// Rotary epilogue of the qkv GEMM for one pair of quads: features n..n+3 (dims d..d+3 < 32 of a
-// head) and n+32..n+35 of token m. q/k: x*cos + rotate_half(x)*sin, q also scaled; written to
-// [H][Np][64]. v: written transposed to [H][64][Np] at key position vt_pos(m). Tokens in
-// [M, Np) get zeros (the attention kernel's padding).
+__device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int n, int d, const float (&lo_acc)[4],
+                                            const float (&hi_acc)[4], float (&o1)[4], float (&o2)[4]);
+
+// Rotary epilogue of the qkv GEMM for one pair of quads (the split-K reduction's path): features
+// n..n+3 (dims d..d+3 < 32 of a head) and n+32..n+35 of token m, stored straight to q/k
+// [H][Np][64] and v^T [H][64][Np] at key position vt_pos(m). Tokens in [M, Np) get zeros.
 __device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n, const float (&lo_acc)[4],
                                               const float (&hi_acc)[4]) {
   if (m >= p.Np || n >= p.N) return;
-  const bool live = m < p.M;
   const int which = n / p.D;                 // 0 = q, 1 = k, 2 = v
   const int head = (n % p.D) / 64, d = n % 64;
-  float lo[4], hi[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    lo[e] = live ? epi_value<kEpiBias>(lo_acc[e], p.bias[n + e]) : 0.f;
-    hi[e] = live ? epi_value<kEpiBias>(hi_acc[e], p.bias[n + e + 32]) : 0.f;
-  }
+  float o1[4], o2[4];
+  rope_values(p, which, m, n, d, lo_acc, hi_acc, o1, o2);
   if (which == 2) {
     bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vt[(int64_t)(d + e) * p.Np] = (bf16)lo[e];
-      vt[(int64_t)(d + e + 32) * p.Np] = (bf16)hi[e];
+      vt[(int64_t)(d + e) * p.Np] = (bf16)o1[e];
+      vt[(int64_t)(d + e + 32) * p.Np] = (bf16)o2[e];
     }
     return;
   }
-  float o1[4], o2[4];
-  if (live) {
-    const f32x2* csr = p.cs + (int64_t)m * 32 + d;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const f32x2 t = csr[e];
-      // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582)
-      o1[e] = round_bf16(round_bf16(lo[e] * t.x) - round_bf16(hi[e] * t.y));   // dims < 32
-      o2[e] = round_bf16(round_bf16(hi[e] * t.x) + round_bf16(lo[e] * t.y));   // dims + 32
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { o1[e] = 0.f; o2[e] = 0.f; }
-  }
-  const float sc = which == 0 ? p.qscale : 1.0f;
   bf16* dst = (which == 0 ? p.q : p.k) + ((int64_t)head * p.Np + m) * 64;
-  const u32x2 v1 = {pack_bf16x2(o1[0] * sc, o1[1] * sc), pack_bf16x2(o1[2] * sc, o1[3] * sc)};
-  const u32x2 v2 = {pack_bf16x2(o2[0] * sc, o2[1] * sc), pack_bf16x2(o2[2] * sc, o2[3] * sc)};
-  *reinterpret_cast<u32x2*>(dst + d) = v1;
-  *reinterpret_cast<u32x2*>(dst + d + 32) = v2;
-}
-
-// Epilogue of one wave's accumulators. Block (a, b), register r: feature
-// n = n0 + wn*TN + 32a + 8*(r/4) + 4*hh + r%4, token m = m0 + wm*TM + 32b + l32.
-template <int BM, int BN, int WM, int WN, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
-                                              f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
-                                              int m0, int n0, int wm, int wn, int lane) {
-  using S = GemmShape<BM, BN, WM, WN>;
-  const int l32 = lane & 31, hh = lane >> 5;
-  if constexpr (EPI == kEpiQkvRope) {
-    static_assert(S::TN % 64 == 0, "the rotary epilogue needs whole 64-feature heads per wave");
-    // The wave's TN features are whole heads: blocks (2h, 2h+1) hold dims [0,32) / [32,64).
-#pragma unroll
-    for (int b = 0; b < S::MB; ++b) {
-      const int m = m0 + wm * S::TM + b * 32 + l32;
-#pragma unroll
-      for (int h2 = 0; h2 < S::NB / 2; ++h2)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float lo[4], hi[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
-          epi_rope_pair(p, m, n0 + wn * S::TN + h2 * 64 + 8 * g + 4 * hh, lo, hi);
-        }
-    }
-  } else {
-#pragma unroll
-    for (int a = 0; a < S::NB; ++a)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int b = 0; b < S::MB; ++b) {
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
-          epi_store_quad<EPI>(p, m0 + wm * S::TM + b * 32 + l32, n0 + wn * S::TN + a * 32 + 8 * g + 4 * hh, v);
-        }
-  }
+  *reinterpret_cast<u32x2*>(dst + d) = u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
+  *reinterpret_cast<u32x2*>(dst + d + 32) = u32x2{pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3])};
 }
 
 // LDS-staged epilogue: each wave writes bf16(acc) of its sub-tile into the (free) LDS as a
@@ -230,6 +171,103 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
     const u32x4 raw = *reinterpret_cast<const u32x4*>(smem + r * BN + ((c ^ (r % CH)) << 3));
     const int m = m0 + r, n = n0 + c * 8;
     if (m < p.M && n < p.N) epi_store_oct<EPI>(p, m, n, raw, vec16);
+  }
+}
+
+// Rotary qkv values of 4 consecutive dims d..d+3 (< 32) and d+32..d+35 of one head, for token m:
+// bias, the reference's bf16 cast points, rotary (q, k) and the softmax pre-scale (q). Tokens
+// at or past M give zeros (the attention kernel's padding).
+__device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int n, int d, const float (&lo_acc)[4],
+                                            const float (&hi_acc)[4], float (&o1)[4], float (&o2)[4]) {
+  const bool live = m < p.M;
+  float lo[4], hi[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lo[e] = live ? epi_value<kEpiBias>(lo_acc[e], p.bias[n + e]) : 0.f;
+    hi[e] = live ? epi_value<kEpiBias>(hi_acc[e], p.bias[n + e + 32]) : 0.f;
+  }
+  if (which == 2 || !live) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o1[e] = lo[e]; o2[e] = hi[e]; }
+    return;
+  }
+  const f32x2* csr = p.cs + (int64_t)m * 32 + d;
+  const float sc = which == 0 ? p.qscale : 1.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const f32x2 t = csr[e];
+    // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582)
+    o1[e] = round_bf16(round_bf16(round_bf16(lo[e] * t.x) - round_bf16(hi[e] * t.y)) * sc);   // dims < 32
+    o2[e] = round_bf16(round_bf16(round_bf16(hi[e] * t.x) + round_bf16(lo[e] * t.y)) * sc);   // dims + 32
+  }
+}
+
+// LDS-staged rotary epilogue of the qkv GEMM. A wave's TN features are whole heads of one of q,
+// k, v; it writes its TM x TN block of final bf16 values into its own LDS region (row-major,
+// 16-byte chunks XOR-swizzled by row), then streams it out: q/k rows of a head are 128 contiguous
+// bytes of [H][Np][64] (16 bytes per lane), and v goes out transposed to [H][64][Np] as 16-byte
+// runs of 8 key positions (gathered from the block with the vt_pos quad swap), instead of
+// 8-byte pieces of 32 rows (q, k) and 2-byte scattered stores (v).
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
+                                                       f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
+                                                       int m0, int n0, int wm, int wn, int lane, int wave, bf16* smem) {
+  using S = GemmShape<BM, BN, WM, WN>;
+  constexpr int TM = S::TM, TN = S::TN, CPR = TN / 8, HPW = TN / 64;
+  static_assert(TN % 64 == 0 && TM % 16 == 0, "the rotary epilogue needs whole heads and 16-token groups");
+  constexpr int RSH = TN == 64 ? 1 : 0;          // rows per 256-byte bank row: 2 (TN 64) or 1 (TN 128)
+  bf16* reg = smem + wave * TM * TN;
+  auto off = [](int row, int chunk) { return row * TN + ((chunk ^ ((row >> RSH) & (CPR - 1))) << 3); };
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int nw = n0 + wn * TN;                   // first feature of the wave's block
+  if (nw >= p.N) return;
+  const int which = nw / p.D;                    // 0 = q, 1 = k, 2 = v
+  const int head0 = (nw % p.D) / 64;
+  const int base = m0 + wm * TM;                 // first token of the wave's block
+#pragma unroll
+  for (int b = 0; b < S::MB; ++b)
+#pragma unroll
+    for (int h2 = 0; h2 < HPW; ++h2)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int t = b * 32 + l32, d = 8 * g + 4 * hh;
+        float lo[4], hi[4], o1[4], o2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
+        rope_values(p, which, base + t, nw + h2 * 64 + d, d, lo, hi, o1, o2);
+        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + g) + 4 * hh) =
+            u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
+        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + 4 + g) + 4 * hh) =
+            u32x2{pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3])};
+      }
+  // (a wave reads back only its own region; its LDS operations complete in order)
+  if (which < 2) {
+    bf16* dst = which == 0 ? p.q : p.k;
+    constexpr int RPI = 64 / CPR;                 // rows per instruction
+#pragma unroll 4
+    for (int i = 0; i < TM / RPI; ++i) {
+      const int t = i * RPI + lane / CPR, c = lane % CPR;
+      const int m = base + t;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(reg + off(t, c));
+      if (m < p.Np) *reinterpret_cast<u32x4*>(dst + ((int64_t)(head0 + c / 8) * p.Np + m) * 64 + (c % 8) * 8) = v;
+    }
+  } else {
+    constexpr int PCH = TM / 8;                   // 8-position chunks per V^T row
+#pragma unroll 2
+    for (int i = 0; i < HPW * 64 * PCH / 64; ++i) {
+      const int item = i * 64 + lane;
+      const int r = item / PCH, pc = item % PCH;  // r: head-in-wave * 64 + dim
+      const int h2 = r / 64, d = r % 64;
+      const int P = base + pc * 8;                // 8 consecutive V^T positions
+      bf16 vals[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = vt_pos(P + e) - base;       // the token stored at position P + e
+        vals[e] = reg[off(t, h2 * 8 + d / 8) + (d & 7)];
+      }
+      if (P < p.Np)
+        *reinterpret_cast<u32x4*>(p.vt + ((int64_t)(head0 + h2) * 64 + d) * p.Np + P) = __builtin_bit_cast(u32x4, vals);
+    }
   }
 }
 
@@ -359,8 +397,12 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         }
     return;
   }
-  if constexpr (EPI == kEpiQkvRope) gemm_epilogue<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane);
-  else gemm_epilogue_lds<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane, tid, smem);
+  if constexpr (EPI == kEpiQkvRope) {
+    __syncthreads();                    // every wave is done with the last stage
+    gemm_epilogue_rope_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, wave, smem);
+  } else {
+    gemm_epilogue_lds<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane, tid, smem);
+  }
 }
 
 // Sums the split-K partials of the tail tiles and applies the epilogue, one thread per 4-feature
@@ -441,7 +483,7 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 template <int BM, int BN, int WM, int WN, int EPI>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
-  const size_t lds = std::max(2 * S::LDS_ELEMS, EPI == kEpiQkvRope ? 0 : BM * BN) * sizeof(bf16);
+  const size_t lds = std::max(2 * S::LDS_ELEMS, BM * BN) * sizeof(bf16);
   static bool attr_set = false;   // benign race: every thread sets the same value
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
