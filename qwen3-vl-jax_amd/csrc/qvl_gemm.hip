@@ -176,29 +176,39 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
 
 // Rotary qkv values of 4 consecutive dims d..d+3 (< 32) and d+32..d+35 of one head, for token m:
 // bias, the reference's bf16 cast points, rotary (q, k) and the softmax pre-scale (q). Tokens
-// at or past M give zeros (the attention kernel's padding).
+// at or past M give zeros (the attention kernel's padding). All operands are vector loads:
+// bias[n..n+3], bias[n+32..n+35] and the token's (cos, sin)[d..d+3].
 __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int n, int d, const float (&lo_acc)[4],
                                             const float (&hi_acc)[4], float (&o1)[4], float (&o2)[4]) {
   const bool live = m < p.M;
+  if (!live) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o1[e] = 0.f; o2[e] = 0.f; }
+    return;
+  }
+  const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
+  const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
   float lo[4], hi[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    lo[e] = live ? epi_value<kEpiBias>(lo_acc[e], p.bias[n + e]) : 0.f;
-    hi[e] = live ? epi_value<kEpiBias>(hi_acc[e], p.bias[n + e + 32]) : 0.f;
+    lo[e] = epi_value<kEpiBias>(lo_acc[e], blo[e]);
+    hi[e] = epi_value<kEpiBias>(hi_acc[e], bhi[e]);
   }
-  if (which == 2 || !live) {
+  if (which == 2) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) { o1[e] = lo[e]; o2[e] = hi[e]; }
     return;
   }
-  const f32x2* csr = p.cs + (int64_t)m * 32 + d;
+  const f32x4* csr = reinterpret_cast<const f32x4*>(p.cs + (int64_t)m * 32 + d);
+  const f32x4 c01 = csr[0], c23 = csr[1];       // (cos, sin) of dims d, d+1 | d+2, d+3
+  const float cs_c[4] = {c01[0], c01[2], c23[0], c23[2]};
+  const float cs_s[4] = {c01[1], c01[3], c23[1], c23[3]};
   const float sc = which == 0 ? p.qscale : 1.0f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const f32x2 t = csr[e];
     // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582)
-    o1[e] = round_bf16(round_bf16(round_bf16(lo[e] * t.x) - round_bf16(hi[e] * t.y)) * sc);   // dims < 32
-    o2[e] = round_bf16(round_bf16(round_bf16(hi[e] * t.x) + round_bf16(lo[e] * t.y)) * sc);   // dims + 32
+    o1[e] = round_bf16(round_bf16(round_bf16(lo[e] * cs_c[e]) - round_bf16(hi[e] * cs_s[e])) * sc);   // dims < 32
+    o2[e] = round_bf16(round_bf16(round_bf16(hi[e] * cs_c[e]) + round_bf16(lo[e] * cs_s[e])) * sc);   // dims + 32
   }
 }
 

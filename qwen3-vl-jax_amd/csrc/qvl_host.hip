@@ -415,7 +415,8 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda
   if (n_tokens < 0 || lda < hidden || lda % 8) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: n_tokens / lda");
   if (n_tokens == 0) return QVL_OK;
   if (!x || !w || !bias || !cs || !q || !k || !vt) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
-  if (!aligned16(x) || !aligned16(w) || !aligned16(q) || !aligned16(k) || !aligned16(vt) || ((uintptr_t)cs & 7))
+  if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(q) || !aligned16(k) || !aligned16(vt) ||
+      !aligned16(cs))
     return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: alignment");
   if (n_tokens * lda * 2 >= (int64_t)UINT32_MAX) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: operand > 4 GiB");
   GemmParams p{};
