@@ -94,8 +94,11 @@ __device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n,
       v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
       v[4] += bf16_lo(r.z); v[5] += bf16_hi(r.z); v[6] += bf16_lo(r.w); v[7] += bf16_hi(r.w);
     }
-    *reinterpret_cast<u32x4*>(dst) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                           pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    // Streaming (nt) store: every CU writes its whole tile at once at the end of a round, and
+    // the output is not re-read by this kernel; measured ~1.5% faster per tower forward.
+    __builtin_nontemporal_store(u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                      pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])},
+                                reinterpret_cast<u32x4*>(dst));
     return;
   }
 #pragma unroll
