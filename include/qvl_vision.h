@@ -219,7 +219,7 @@ typedef struct qvl_vision_metadata_dev {
   const int32_t* pos_hw;    /* [n_tokens, 2]  */
   const int32_t* tap_idx;   /* [4, n_tokens]  */
   const float* tap_w;       /* [4, n_tokens]  */
-  const int32_t* tiles;     /* [n_tiles, 3]   */
+  const int32_t* tiles;     /* [n_tiles, 4]   */
 } qvl_vision_metadata_dev;
 
 int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tokens, size_t* bytes);
@@ -231,6 +231,46 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* cfg, const qvl_visi
                       const qvl_vision_metadata_dev* meta, const float* d_pixel_values,
                       void* d_tokens, void* const* d_deepstack, void* d_workspace,
                       size_t workspace_bytes);
+
+/* ------------------------------------------------------------------------------------------ */
+/* The steps either side of the tower: patchify before it, decoder-side injection after it.    */
+/* ------------------------------------------------------------------------------------------ */
+
+/* On-device patchify: replaces the array part of `preprocess_image` (sample.py:86-121), i.e.
+ * everything after PIL's convert("RGB") / resize. `d_frames` is uint8 [n_frames][height][width]
+ * [channels] (HWC per frame, channels 3 or 4; a 4th channel is dropped like sample.py:74-75).
+ * Writes pixel_values [gt*gh*gw, 3*Tp*P*P] (row stride ld_out elements) in dtype: value =
+ * ((u8 / 255) - 0.5) / 0.5 computed in float32 exactly as sample.py:86-87 (bf16 output is that
+ * value rounded to nearest even, i.e. `pixel_values.astype(bf16)` of model.py:556), frames padded
+ * to a multiple of temporal_patch_size by repeating the last one (sample.py:93-98), rows in
+ * merge-block order and columns (c, tp, ph, pw) (sample.py:112-119); gt = ceil(n_frames / Tp),
+ * gh = height / P, gw = width / P. Errors like sample.py:104-110: height/width not divisible by
+ * P, or gh/gw not divisible by merge_size -> QVL_ERR_INVALID_ARG. */
+int qvl_patchify(void* stream, int32_t dtype, const uint8_t* d_frames, int64_t n_frames, int64_t height,
+                 int64_t width, int32_t channels, int32_t patch_size, int32_t temporal_patch_size,
+                 int32_t merge_size, void* d_out, int64_t ld_out);
+
+/* Vision-token positions (model.py:927-931 `visual_mask` / `jnp.where(..., size=n, fill_value=-1)`,
+ * also model.py:880-882): for each of `batch` rows of `d_tokens` [batch][seq_len] (int32), the
+ * first n_rows indices s with tokens[s] == match, increasing, then -1; d_count[b] = the number of
+ * matches (may exceed n_rows). A boolean mask works with tokens = mask as int32 and match = 1. */
+int qvl_vision_positions(void* stream, const int32_t* d_tokens, int64_t batch, int64_t seq_len, int32_t match,
+                         int64_t n_rows, int32_t* d_pos, int32_t* d_count);
+
+#define QVL_SCATTER_SET 0   /* `_inject`: hidden[pos] = rows            (model.py:932-935) */
+#define QVL_SCATTER_ADD 1   /* `_apply_deepstack`: hidden[pos] += rows  (model.py:880-886) */
+
+/* hidden [batch][seq_len][dim] (hidden_dtype) at row d_pos[b][j] gets rows[b][j] (rows_dtype,
+ * cast to hidden_dtype first, `feat.astype(h.dtype)`), for j < n_rows with pos >= 0; ADD rounds
+ * hidden + row to hidden_dtype. `rows_batch_stride` (elements) is 0 to use one set of rows for
+ * every batch row (VisionEmbeddings.with_batch_dim, model.py:47-63). `d_pos` / `d_count` come from
+ * qvl_vision_positions. Where a row has fewer matches than n_rows, the reference's unfilled
+ * updates all land on row 0 (a re-write of its old value after SET, a +0 after ADD); they are
+ * applied in update order, as XLA's CPU scatter does. */
+int qvl_scatter_vision_rows(void* stream, int32_t mode, int32_t hidden_dtype, void* d_hidden, int64_t batch,
+                            int64_t seq_len, int64_t dim, int32_t rows_dtype, const void* d_rows,
+                            int64_t rows_batch_stride, int64_t n_rows, const int32_t* d_pos,
+                            const int32_t* d_count);
 
 #ifdef __cplusplus
 }

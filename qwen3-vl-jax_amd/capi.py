@@ -15,6 +15,8 @@ QVL_DTYPE_BF16 = 1
 QVL_EPI_BIAS = 0
 QVL_EPI_BIAS_GELU = 1
 QVL_EPI_BIAS_RESIDUAL = 2
+QVL_SCATTER_SET = 0
+QVL_SCATTER_ADD = 1
 
 _p = C.c_void_p
 _i64 = C.c_int64
@@ -77,6 +79,9 @@ SIGNATURES = {
     "qvl_encode_vision_workspace_size": (C.c_int, [C.POINTER(VisionConfig), _i64, C.POINTER(_sz)]),
     "qvl_encode_vision": (C.c_int, [_p, C.POINTER(VisionConfig), C.POINTER(VisionWeights),
                                     C.POINTER(VisionMetadataDev), _p, _p, C.POINTER(_p), _p, _sz]),
+    "qvl_patchify": (C.c_int, [_p, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _i64]),
+    "qvl_vision_positions": (C.c_int, [_p, _p, _i64, _i64, _i32, _i64, _p, _p]),
+    "qvl_scatter_vision_rows": (C.c_int, [_p, _i32, _i32, _p, _i64, _i64, _i64, _i32, _p, _i64, _i64, _p, _p]),
 }
 
 

@@ -1,0 +1,225 @@
+// The steps either side of encode_vision: on-device patchify of uint8 frames (the array
+// preprocess_image builds after PIL's convert/resize, sample.py:86-121) and the decoder-side
+// injection of vision rows into the hidden states plus the deepstack adds (model.py:874-886,
+// 927-938). All are HBM-bound byte / row movement; each kernel reads its inputs once and writes
+// every output element once, with 8- or 16-byte row-contiguous stores.
+#include <type_traits>
+
+#include "qvl_kernels.h"
+
+namespace qvl {
+
+// ---------------------------------------------------------------------------------------------
+// Patchify (sample.py:86-121): value = ((u8 / 255) - 0.5) / 0.5 in fp32 (numpy's float32 ops,
+// sample.py:86-87), frames padded to a multiple of Tp by repeating the last one (sample.py:93-98),
+// rows in merge-block order (t, hb, wb, mi, mj) and columns (c, tp, ph, pw) (sample.py:112-119).
+// One workgroup per 2-D merge block (m*m rows); VEC consecutive columns (one pw run) per step.
+// ---------------------------------------------------------------------------------------------
+template <int VEC, typename OutT>
+__global__ __launch_bounds__(256) void patchify_kernel(const uint8_t* __restrict__ frames, int F, int H, int W,
+                                                       int cin, int P, int Tp, int m, int GH, int GW,
+                                                       OutT* __restrict__ out, int64_t ldo) {
+  __shared__ float lut[256];
+  // The 256 possible values, each by the reference's two float32 operations (IEEE division).
+  lut[threadIdx.x] = ((float)threadIdx.x / 255.0f - 0.5f) / 0.5f;
+  __syncthreads();
+
+  const int K = 3 * Tp * P * P;
+  const int KV = K / VEC, rows = m * m;
+  const int64_t g = blockIdx.x;                       // merge block: (t * GH + hb) * GW + wb
+  const int wb = (int)(g % GW);
+  const int64_t tg = g / GW;
+  const int hb = (int)(tg % GH), t = (int)(tg / GH);
+  for (int q = threadIdx.x; q < rows * KV; q += 256) {
+    const int r = q / KV, k = (q % KV) * VEC;
+    const int mi = r / m, mj = r % m;
+    const int pw = k % P, ph = (k / P) % P, tp = (k / (P * P)) % Tp, c = k / (P * P * Tp);
+    const int f = min(t * Tp + tp, F - 1);
+    const int y = (hb * m + mi) * P + ph, x = (wb * m + mj) * P + pw;
+    const uint8_t* src = frames + (((int64_t)f * H + y) * W + x) * cin + c;
+    OutT* dst = out + (g * rows + r) * ldo + k;
+    if constexpr (VEC == 4) {
+      const float v0 = lut[src[0]], v1 = lut[src[cin]], v2 = lut[src[2 * cin]], v3 = lut[src[3 * cin]];
+      if constexpr (std::is_same<OutT, float>::value) {
+        *reinterpret_cast<f32x4*>(dst) = f32x4{v0, v1, v2, v3};
+      } else {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+      }
+    } else {
+      *dst = (OutT)lut[src[0]];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Vision-token positions (model.py:927-931 / 880-882): for each batch row, the first n_rows
+// token indices s with tokens[s] == match, in increasing order, then -1 fill; count = number of
+// matches (may exceed n_rows). One 1024-thread workgroup per batch row: ballot + per-wave
+// popcount prefix over 1024-token chunks.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void vision_positions_kernel(const int32_t* __restrict__ tokens, int64_t S,
+                                                                int32_t match, int64_t n_rows,
+                                                                int32_t* __restrict__ pos, int32_t* __restrict__ count) {
+  __shared__ int wave_hits[16];
+  const int b = blockIdx.x;
+  const int32_t* tk = tokens + (int64_t)b * S;
+  int32_t* pb = pos + (int64_t)b * n_rows;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int64_t base = 0;
+  for (int64_t s0 = 0; s0 < S; s0 += 1024) {
+    const int64_t s = s0 + threadIdx.x;
+    const bool hit = s < S && tk[s] == match;
+    const uint64_t bal = __ballot(hit);
+    if (lane == 0) wave_hits[wv] = __popcll(bal);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int h = wave_hits[i];
+      before += i < wv ? h : 0;
+      total += h;
+    }
+    const int64_t rank = base + before + __popcll(bal & ((1ull << lane) - 1ull));
+    if (hit && rank < n_rows) pb[rank] = (int32_t)s;
+    base += total;
+    __syncthreads();
+  }
+  for (int64_t r = base + threadIdx.x; r < n_rows; r += 1024) pb[r] = -1;
+  if (threadIdx.x == 0) count[b] = (int32_t)base;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Row scatter (model.py:880-886 `_add`, 932-935 `_inject`): hidden[b, pos[b, j], :] =
+// cast(rows[b, j, :]) (SET) or hidden + cast(rows) rounded to the hidden dtype (ADD), for
+// pos >= 0. The reference scatters all n_rows updates, sending the unfilled ones (count <
+// n_rows) to row 0 with "keep" / "+0" updates; applied in update order (XLA's CPU scatter)
+// those leave hidden[b, 0] as it was before a SET, and add +0 to it after an ADD. Workgroup
+// (j, b) moves one row; workgroup (n_rows, b) applies the trailing "+0" to row 0 when no
+// filled entry targets it.
+// ---------------------------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float ld_f(const T* p) { return (float)*p; }
+template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+
+template <int MODE, typename HT, typename RT>
+__global__ __launch_bounds__(256) void scatter_rows_kernel(HT* __restrict__ hidden, int64_t S, int64_t D,
+                                                           const RT* __restrict__ rows, int64_t rows_bstride,
+                                                           int64_t n_rows, const int32_t* __restrict__ pos,
+                                                           const int32_t* __restrict__ count) {
+  const int64_t j = blockIdx.x;
+  const int b = blockIdx.y;
+  const int64_t cnt = count[b];
+  const bool unfilled = cnt < n_rows;
+  HT* hb = hidden + (int64_t)b * S * D;
+  if (j == n_rows) {
+    // trailing "+0" updates of the unfilled entries on row 0 (only if no filled entry is row 0)
+    if (MODE == QVL_SCATTER_ADD && unfilled && pos[(int64_t)b * n_rows] != 0)
+      for (int64_t d = threadIdx.x; d < D; d += 256) hb[d] = from_f<HT>(ld_f(hb + d) + 0.0f);
+    return;
+  }
+  const int p = pos[(int64_t)b * n_rows + j];
+  if (p < 0) return;
+  if (MODE == QVL_SCATTER_SET && p == 0 && unfilled) return;   // overwritten by the old row 0 afterwards
+  HT* h = hb + (int64_t)p * D;
+  const RT* r = rows + (int64_t)b * rows_bstride + j * D;
+  for (int64_t d = threadIdx.x; d < D; d += 256) {
+    const HT u = from_f<HT>(ld_f(r + d));                   // feat.astype(h.dtype)
+    if (MODE == QVL_SCATTER_SET) {
+      h[d] = u;
+    } else {
+      float v = ld_f(h + d) + (float)u;                     // h + u in the hidden dtype
+      v = (float)from_f<HT>(v);
+      if (p == 0 && unfilled) v = (float)from_f<HT>(v + 0.0f);
+      h[d] = from_f<HT>(v);
+    }
+  }
+}
+
+}  // namespace qvl
+
+using namespace qvl;
+
+extern "C" {
+
+int qvl_patchify(void* stream, int32_t dtype, const uint8_t* frames, int64_t n_frames, int64_t height, int64_t width,
+                 int32_t channels, int32_t patch_size, int32_t temporal_patch_size, int32_t merge_size, void* out,
+                 int64_t ld_out) {
+  if (dtype != QVL_DTYPE_F32 && dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "patchify: dtype %d", dtype);
+  if (n_frames <= 0 || height <= 0 || width <= 0 || (channels != 3 && channels != 4) || patch_size <= 0 ||
+      temporal_patch_size <= 0 || merge_size <= 0)
+    return set_error(QVL_ERR_INVALID_ARG, "patchify: bad sizes");
+  if (height % patch_size || width % patch_size)
+    return set_error(QVL_ERR_INVALID_ARG, "patchify: dimensions must be divisible by patch_size");
+  const int64_t gh = height / patch_size, gw = width / patch_size;
+  if (gh % merge_size || gw % merge_size)
+    return set_error(QVL_ERR_INVALID_ARG, "patchify: grid must be divisible by spatial_merge_size");
+  const int64_t K = 3LL * temporal_patch_size * patch_size * patch_size;
+  if (ld_out < K) return set_error(QVL_ERR_INVALID_ARG, "patchify: ld_out %lld < %lld", (long long)ld_out, (long long)K);
+  if (!frames || !out) return set_error(QVL_ERR_INVALID_ARG, "patchify: NULL pointer");
+  if (K * merge_size * merge_size > (1LL << 30) || height * width * channels * n_frames > (1LL << 40))
+    return set_error(QVL_ERR_UNSUPPORTED, "patchify: sizes");
+  const int64_t gt = (n_frames + temporal_patch_size - 1) / temporal_patch_size;
+  const int64_t blocks = gt * (gh / merge_size) * (gw / merge_size);
+  if (blocks == 0) return QVL_OK;
+  if (blocks > 0x7fffffffLL) return set_error(QVL_ERR_UNSUPPORTED, "patchify: too many merge blocks");
+  const bool vec = patch_size % 4 == 0 && ld_out % 4 == 0 &&
+                   ((uintptr_t)out % (dtype == QVL_DTYPE_F32 ? 16 : 8)) == 0;
+  hipStream_t st = (hipStream_t)stream;
+  const int F = (int)n_frames, H = (int)height, W = (int)width, P = patch_size, Tp = temporal_patch_size,
+            m = merge_size, GH = (int)(gh / merge_size), GW = (int)(gw / merge_size);
+  const dim3 grid((unsigned)blocks);
+  if (dtype == QVL_DTYPE_F32) {
+    if (vec) hipLaunchKernelGGL((patchify_kernel<4, float>), grid, dim3(256), 0, st, frames, F, H, W, channels, P, Tp, m, GH, GW, (float*)out, ld_out);
+    else hipLaunchKernelGGL((patchify_kernel<1, float>), grid, dim3(256), 0, st, frames, F, H, W, channels, P, Tp, m, GH, GW, (float*)out, ld_out);
+  } else {
+    if (vec) hipLaunchKernelGGL((patchify_kernel<4, bf16>), grid, dim3(256), 0, st, frames, F, H, W, channels, P, Tp, m, GH, GW, (bf16*)out, ld_out);
+    else hipLaunchKernelGGL((patchify_kernel<1, bf16>), grid, dim3(256), 0, st, frames, F, H, W, channels, P, Tp, m, GH, GW, (bf16*)out, ld_out);
+  }
+  return check_launch("patchify");
+}
+
+int qvl_vision_positions(void* stream, const int32_t* tokens, int64_t batch, int64_t seq_len, int32_t match,
+                         int64_t n_rows, int32_t* pos, int32_t* count) {
+  if (batch < 0 || seq_len < 0 || n_rows < 0) return set_error(QVL_ERR_INVALID_ARG, "vision_positions: bad sizes");
+  if (seq_len > 0x7fffffffLL || batch > 0x7fffffffLL) return set_error(QVL_ERR_UNSUPPORTED, "vision_positions: sizes");
+  if (batch == 0) return QVL_OK;
+  if ((!tokens && seq_len > 0) || (!pos && n_rows > 0) || !count)
+    return set_error(QVL_ERR_INVALID_ARG, "vision_positions: NULL pointer");
+  hipLaunchKernelGGL(vision_positions_kernel, dim3((unsigned)batch), dim3(1024), 0, (hipStream_t)stream, tokens, seq_len,
+                     match, n_rows, pos, count);
+  return check_launch("vision_positions");
+}
+
+int qvl_scatter_vision_rows(void* stream, int32_t mode, int32_t hidden_dtype, void* hidden, int64_t batch,
+                            int64_t seq_len, int64_t dim, int32_t rows_dtype, const void* rows,
+                            int64_t rows_batch_stride, int64_t n_rows, const int32_t* pos, const int32_t* count) {
+  if (mode != QVL_SCATTER_SET && mode != QVL_SCATTER_ADD) return set_error(QVL_ERR_INVALID_ARG, "scatter_vision_rows: mode %d", mode);
+  const bool hok = hidden_dtype == QVL_DTYPE_F32 || hidden_dtype == QVL_DTYPE_BF16;
+  const bool rok = rows_dtype == QVL_DTYPE_F32 || rows_dtype == QVL_DTYPE_BF16;
+  if (!hok || !rok) return set_error(QVL_ERR_UNSUPPORTED, "scatter_vision_rows: dtypes %d/%d", hidden_dtype, rows_dtype);
+  if (batch < 0 || seq_len < 0 || dim < 0 || n_rows < 0 || rows_batch_stride < 0)
+    return set_error(QVL_ERR_INVALID_ARG, "scatter_vision_rows: bad sizes");
+  if (batch == 0 || n_rows == 0 || dim == 0) return QVL_OK;
+  if (batch > 65535 || n_rows >= 0x7fffffffLL) return set_error(QVL_ERR_UNSUPPORTED, "scatter_vision_rows: sizes");
+  if (!hidden || !rows || !pos || !count) return set_error(QVL_ERR_INVALID_ARG, "scatter_vision_rows: NULL pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)(n_rows + 1), (unsigned)batch);
+#define QVL_SCATTER(M, HT, RT)                                                                               \
+  hipLaunchKernelGGL((scatter_rows_kernel<M, HT, RT>), grid, dim3(256), 0, st, (HT*)hidden, seq_len, dim,      \
+                     (const RT*)rows, rows_batch_stride, n_rows, pos, count)
+  const bool hb = hidden_dtype == QVL_DTYPE_BF16, rb = rows_dtype == QVL_DTYPE_BF16;
+  if (mode == QVL_SCATTER_SET) {
+    if (hb && rb) QVL_SCATTER(QVL_SCATTER_SET, bf16, bf16);
+    else if (hb) QVL_SCATTER(QVL_SCATTER_SET, bf16, float);
+    else if (rb) QVL_SCATTER(QVL_SCATTER_SET, float, bf16);
+    else QVL_SCATTER(QVL_SCATTER_SET, float, float);
+  } else {
+    if (hb && rb) QVL_SCATTER(QVL_SCATTER_ADD, bf16, bf16);
+    else if (hb) QVL_SCATTER(QVL_SCATTER_ADD, bf16, float);
+    else if (rb) QVL_SCATTER(QVL_SCATTER_ADD, float, bf16);
+    else QVL_SCATTER(QVL_SCATTER_ADD, float, float);
+  }
+#undef QVL_SCATTER
+  return check_launch("scatter_vision_rows");
+}
+
+}  // extern "C"

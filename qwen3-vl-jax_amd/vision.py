@@ -196,6 +196,7 @@ class Qwen3VisionTransformer:
         self._lib = capi.load()
         self._w = None
         self._keep = []
+        self._state: Dict[str, object] = {}
         self._meta_cache: Dict[tuple, tuple] = {}
         self._ws = None
         cfg = capi.VisionConfig()
@@ -233,6 +234,7 @@ class Qwen3VisionTransformer:
         return t.to(torch.bfloat16).to(torch.float32) if self.qdtype == capi.QVL_DTYPE_BF16 else t
 
     def _pack_dense(self, p):
+        """Flax Dense {kernel [in, out], bias [out]} -> (packed [n_pad, k_pad] weight, bias [n_pad])."""
         torch = _torch()
         k = np.ascontiguousarray(np.asarray(p["kernel"], np.float32))
         kin, nout = k.shape
@@ -243,60 +245,126 @@ class Qwen3VisionTransformer:
                                                    out.data_ptr()), "qvl_pack_dense_weight")
         b = np.zeros(npad, np.float32)
         b[:nout] = np.asarray(p["bias"], np.float32)
-        bias = self._round(torch.from_numpy(b).to(self.device))
-        self._keep += [out, bias]
-        return out, bias
+        return out, self._round(torch.from_numpy(b).to(self.device))
 
     def _vec(self, v):
         torch = _torch()
         t = torch.from_numpy(np.ascontiguousarray(np.asarray(v, np.float32))).to(self.device)
-        t = self._round(t)                                # LayerNorm params live in the tower dtype
-        self._keep.append(t)
-        return t
+        return self._round(t)                             # LayerNorm params live in the tower dtype
 
     def bind(self, params: Dict) -> "Qwen3VisionTransformer":
         """Pack a Flax-tree param dict onto the device (load-time, model.py:1105-1160 layout)."""
         torch = _torch()
         v = params.get("visual", params)
         s = self.spec
-        self._keep = []
-        W = capi.VisionWeights()
-        pw, pb = self._pack_dense(v["patch_embed"]["proj"])
-        W.patch_w, W.patch_b = pw.data_ptr(), pb.data_ptr()
-        tab = torch.from_numpy(np.ascontiguousarray(v["pos_embed"]["embedding"], np.float32)).to(self.device)
-        tab = tab.to(self._tdtype()).contiguous()
-        self._keep.append(tab)
-        W.pos_table = tab.data_ptr()
-        blocks = (capi.BlockWeights * s.depth)()
+        st: Dict[str, object] = {}
+
+        def dense(name, p):
+            st[name + ".w"], st[name + ".b"] = self._pack_dense(p)
+
+        dense("patch_embed", v["patch_embed"]["proj"])
+        st["pos_table"] = torch.from_numpy(np.ascontiguousarray(v["pos_embed"]["embedding"], np.float32)).to(
+            self.device).to(self._tdtype()).contiguous()
         for i in range(s.depth):
             b = v[f"blocks_{i}"]
-            bw = blocks[i]
-            bw.norm1_w, bw.norm1_b = self._vec(b["norm1"]["weight"]).data_ptr(), self._vec(b["norm1"]["bias"]).data_ptr()
-            bw.norm2_w, bw.norm2_b = self._vec(b["norm2"]["weight"]).data_ptr(), self._vec(b["norm2"]["bias"]).data_ptr()
+            for n in ("norm1", "norm2"):
+                st[f"blocks.{i}.{n}.w"], st[f"blocks.{i}.{n}.b"] = self._vec(b[n]["weight"]), self._vec(b[n]["bias"])
             for name, key in (("qkv", ("attn", "qkv")), ("proj", ("attn", "proj")),
                               ("fc1", ("mlp", "linear_fc1")), ("fc2", ("mlp", "linear_fc2"))):
-                w, bias = self._pack_dense(b[key[0]][key[1]])
-                setattr(bw, name + "_w", w.data_ptr())
-                setattr(bw, name + "_b", bias.data_ptr())
+                dense(f"blocks.{i}.{name}", b[key[0]][key[1]])
+        mergers = [("merger", v["merger"])] + [(f"deepstack.{j}", v[f"deepstack_mergers_{j}"])
+                                               for j in range(len(s.deepstack_visual_indexes))]
+        for name, m in mergers:
+            st[name + ".norm.w"], st[name + ".norm.b"] = self._vec(m["norm"]["weight"]), self._vec(m["norm"]["bias"])
+            dense(name + ".fc1", m["linear_fc1"])
+            dense(name + ".fc2", m["linear_fc2"])
+        torch.cuda.current_stream().synchronize()
+        return self._bind_state(st)
+
+    def packed_state(self) -> Dict[str, object]:
+        """The bound device buffers by name (packed weights, biases, LayerNorm params, pos table)."""
+        if self._w is None:
+            raise RuntimeError("tower is not bound")
+        return dict(self._state)
+
+    def expected_packed_shapes(self) -> Dict[str, Tuple[Tuple[int, ...], str]]:
+        """name -> (shape, "w" for tower-dtype buffers | "f" for fp32 vectors) of a bound tower."""
+        s = self.spec
+        r64 = lambda x: -(-x // 64) * 64
+        D, I, PV, Do = s.hidden_size, s.intermediate_size, s.patch_volume, s.out_hidden_size
+        M4 = D * s.spatial_merge_size ** 2
+        out = {}
+
+        def dense(name, kin, nout):
+            out[name + ".w"] = ((r64(nout), r64(kin)), "w")
+            out[name + ".b"] = ((r64(nout),), "f")
+
+        dense("patch_embed", PV, D)
+        out["pos_table"] = ((s.num_position_embeddings, D), "w")
+        for i in range(s.depth):
+            for n in ("norm1", "norm2"):
+                out[f"blocks.{i}.{n}.w"], out[f"blocks.{i}.{n}.b"] = ((D,), "f"), ((D,), "f")
+            dense(f"blocks.{i}.qkv", D, 3 * D)
+            dense(f"blocks.{i}.proj", D, D)
+            dense(f"blocks.{i}.fc1", D, I)
+            dense(f"blocks.{i}.fc2", I, D)
+        for j, name in enumerate(["merger"] + [f"deepstack.{k}" for k in range(len(s.deepstack_visual_indexes))]):
+            nd = D if j == 0 else M4
+            out[name + ".norm.w"], out[name + ".norm.b"] = ((nd,), "f"), ((nd,), "f")
+            dense(name + ".fc1", M4, M4)
+            dense(name + ".fc2", M4, Do)
+        return out
+
+    def bind_packed(self, state: Dict[str, object]) -> "Qwen3VisionTransformer":
+        """Bind already-packed device buffers (e.g. `load_packed`), checking every name, shape and
+        dtype against this tower's spec and dtype; no packing kernels run."""
+        torch = _torch()
+        exp = self.expected_packed_shapes()
+        missing = sorted(set(exp) - set(state))
+        extra = sorted(set(state) - set(exp))
+        if missing or extra:
+            raise ValueError(f"packed state mismatch: missing {missing[:4]}, unexpected {extra[:4]}")
+        st = {}
+        for name, (shape, kind) in exp.items():
+            t = state[name]
+            want = self._tdtype() if kind == "w" else torch.float32
+            if tuple(t.shape) != shape or t.dtype != want:
+                raise ValueError(f"{name}: {tuple(t.shape)} {t.dtype}, expected {shape} {want}")
+            st[name] = t.to(self.device).contiguous()
+        return self._bind_state(st)
+
+    def _bind_state(self, st: Dict[str, object]) -> "Qwen3VisionTransformer":
+        s = self.spec
+        p = lambda name: st[name].data_ptr()
+        W = capi.VisionWeights()
+        W.patch_w, W.patch_b, W.pos_table = p("patch_embed.w"), p("patch_embed.b"), p("pos_table")
+        blocks = (capi.BlockWeights * s.depth)()
+        for i in range(s.depth):
+            bw = blocks[i]
+            bw.norm1_w, bw.norm1_b = p(f"blocks.{i}.norm1.w"), p(f"blocks.{i}.norm1.b")
+            bw.norm2_w, bw.norm2_b = p(f"blocks.{i}.norm2.w"), p(f"blocks.{i}.norm2.b")
+            for name in ("qkv", "proj", "fc1", "fc2"):
+                setattr(bw, name + "_w", p(f"blocks.{i}.{name}.w"))
+                setattr(bw, name + "_b", p(f"blocks.{i}.{name}.b"))
         W.blocks = blocks
 
-        def merger(m):
+        def merger(name):
             mw = capi.MergerWeights()
-            mw.norm_w, mw.norm_b = self._vec(m["norm"]["weight"]).data_ptr(), self._vec(m["norm"]["bias"]).data_ptr()
-            w1, b1 = self._pack_dense(m["linear_fc1"])
-            w2, b2 = self._pack_dense(m["linear_fc2"])
-            mw.fc1_w, mw.fc1_b, mw.fc2_w, mw.fc2_b = w1.data_ptr(), b1.data_ptr(), w2.data_ptr(), b2.data_ptr()
+            mw.norm_w, mw.norm_b = p(name + ".norm.w"), p(name + ".norm.b")
+            mw.fc1_w, mw.fc1_b, mw.fc2_w, mw.fc2_b = p(name + ".fc1.w"), p(name + ".fc1.b"), p(name + ".fc2.w"), p(
+                name + ".fc2.b")
             return mw
 
-        W.merger = merger(v["merger"])
+        W.merger = merger("merger")
         nds = len(s.deepstack_visual_indexes)
         ds = (capi.MergerWeights * max(nds, 1))()
         for j in range(nds):
-            ds[j] = merger(v[f"deepstack_mergers_{j}"])
+            ds[j] = merger(f"deepstack.{j}")
         W.deepstack = ds
+        self._state = st
+        self._keep = list(st.values())
         self._blocks_arr, self._ds_arr = blocks, ds
         self._w = W
-        torch.cuda.current_stream().synchronize()
         return self
 
     # -- per-grid metadata ----------------------------------------------------------------------

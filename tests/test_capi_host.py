@@ -153,3 +153,30 @@ def test_workspace_sizes(pkg):
                          (pkg.capi.QVL_DTYPE_F32, 64, 16 * 64 * (64 + 64 + 64) * 4)):
         assert lib.qvl_vision_attention_workspace_size(dt, 10, 16, hd, C.byref(nb)) == 0
         assert nb.value == want
+
+
+def test_io_entry_argument_checks(pkg):
+    """patchify / positions / scatter reject bad arguments before any launch."""
+    lib = pkg.capi.load()
+    cp = pkg.capi
+    fake = 1 << 20   # never dereferenced: validation fails first
+    BF, F32 = cp.QVL_DTYPE_BF16, cp.QVL_DTYPE_F32
+    # height not divisible by patch, grid not divisible by merge, bad channels / dtype / ld_out
+    assert lib.qvl_patchify(None, F32, fake, 1, 40, 64, 3, 16, 2, 2, fake, 1536) == -1
+    assert b"divisible" in lib.qvl_last_error()
+    assert lib.qvl_patchify(None, F32, fake, 1, 48, 64, 3, 16, 2, 2, fake, 1536) == -1
+    assert lib.qvl_patchify(None, F32, fake, 1, 32, 32, 2, 16, 2, 2, fake, 1536) == -1
+    assert lib.qvl_patchify(None, 9, fake, 1, 32, 32, 3, 16, 2, 2, fake, 1536) == -2
+    assert lib.qvl_patchify(None, BF, fake, 1, 32, 32, 3, 16, 2, 2, fake, 1535) == -1
+    assert lib.qvl_patchify(None, BF, fake, 0, 32, 32, 3, 16, 2, 2, fake, 1536) == -1
+    assert lib.qvl_patchify(None, BF, None, 1, 32, 32, 3, 16, 2, 2, fake, 1536) == -1
+    # positions: empty batch is a no-op; negative sizes / NULL rejected
+    assert lib.qvl_vision_positions(None, fake, 0, 10, 5, 4, fake, fake) == 0
+    assert lib.qvl_vision_positions(None, fake, 1, -1, 5, 4, fake, fake) == -1
+    assert lib.qvl_vision_positions(None, fake, 1, 10, 5, 4, fake, None) == -1
+    # scatter: bad mode, dtype, sizes; empty work is a no-op
+    assert lib.qvl_scatter_vision_rows(None, 2, BF, fake, 1, 8, 4, BF, fake, 0, 2, fake, fake) == -1
+    assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_SET, 3, fake, 1, 8, 4, BF, fake, 0, 2, fake, fake) == -2
+    assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_ADD, BF, fake, 1, 8, 4, F32, fake, -1, 2, fake, fake) == -1
+    assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_ADD, BF, fake, 1, 8, 4, F32, fake, 0, 0, fake, fake) == 0
+    assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_SET, BF, fake, 1, 8, 4, F32, None, 0, 2, fake, fake) == -1
