@@ -187,6 +187,10 @@ typedef struct qvl_vision_config {
   float ln_eps;                     /* 1e-6                                */
   float rope_theta;                 /* 10000                               */
   int32_t dtype;                    /* QVL_DTYPE_BF16 or QVL_DTYPE_F32     */
+  int32_t use_window;               /* 1: window attention on the blocks not in fullatt_mask
+                                       (model.py:808-850; fullatt_block_indexes != all)   */
+  uint64_t fullatt_mask;            /* window mode: bit i = block i attends over the full
+                                       cu_seqlens (depth <= 64)                          */
 } qvl_vision_config;
 
 typedef struct qvl_block_weights {           /* blocks_{i} (model.py:617-630)          */
@@ -212,6 +216,25 @@ typedef struct qvl_vision_weights {
   const qvl_merger_weights* deepstack;       /* HOST array [n_deepstack]                       */
 } qvl_vision_weights;
 
+/* Window-attention metadata (model.py:769-799 `_get_window_index`, host side, bit-exact):
+ * window_index [n_tokens/merge^2]: the merge group at each position of the window order (windows
+ * of vit = window_size/merge/patch_size groups square, row-major per frame, groups row-major inside
+ * a window, grids padded to whole windows and the padding skipped); cu_window: window boundaries
+ * in tokens with consecutive duplicates removed, *n_cu_window entries (pass cu_window = NULL to
+ * query the count). cu_full [n_grids + 1]: the full-attention cu_seqlens the reference uses in the
+ * window path (model.py:828-830: cumsum of t*h*w*merge^2 per image), each clamped to n_tokens as
+ * its q[start:end] slicing clamps it. Any output may be NULL. */
+int qvl_window_metadata(const int32_t* h_grid_thw, int64_t n_grids, int32_t merge, int32_t patch_size,
+                        int32_t window_size, int32_t* h_window_index, int32_t* h_cu_window, int64_t capacity,
+                        int64_t* n_cu_window, int32_t* h_cu_full);
+
+/* dst[r, :width] = src[idx[r / group] * group + r % group, :width], converted to dst_dtype (bf16
+ * rounds to nearest even); n_rows (output rows) a multiple of group. The window path's merge-group
+ * shuffle (model.py:809-812, group = merge^2) and unshuffle (845-848, group = 1). */
+int qvl_gather_rows(void* stream, int32_t src_dtype, const void* d_src, int64_t ld_src, int32_t dst_dtype,
+                    void* d_dst, int64_t ld_dst, const int32_t* d_idx, int64_t n_rows, int32_t group,
+                    int64_t width);
+
 /* Device metadata of one grid (qvl_vision_metadata / qvl_attention_worklist, copied to the GPU). */
 typedef struct qvl_vision_metadata_dev {
   int64_t n_tokens;
@@ -220,6 +243,12 @@ typedef struct qvl_vision_metadata_dev {
   const int32_t* tap_idx;   /* [4, n_tokens]  */
   const float* tap_w;       /* [4, n_tokens]  */
   const int32_t* tiles;     /* [n_tiles, 4]   */
+  /* window mode only (else 0 / NULL): `tiles` are the worklist of cu_full, these of cu_window,
+   * and pos_hw / tap_idx / tap_w are in window order (row r = token window_order[r]). */
+  int64_t n_window_tiles;
+  const int32_t* window_tiles;    /* [n_window_tiles, 4]                                     */
+  const int32_t* window_index;    /* [n_tokens/4] merge group at each window-order position  */
+  const int32_t* window_reverse;  /* [n_tokens/4] argsort(window_index)                      */
 } qvl_vision_metadata_dev;
 
 int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tokens, size_t* bytes);

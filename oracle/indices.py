@@ -7,6 +7,8 @@ Everything here is host-side numpy, exactly as the reference builds it before th
 * `rotary_half_ref`     model.py:540-546, 694-698 (inv_freq table, gather, [h-freqs, w-freqs])
 * `pos_embed_taps_ref`  model.py:700-767  (4 bilinear taps per raster patch, then the
                         `jnp.repeat(.., t, axis=0)` frame expansion and the merge-block reshape)
+* `window_index_ref`    model.py:769-799  (window order of merge groups, cu_window) and
+  `cu_full_window_ref`  model.py:828-830  (the window path's full-attention cu_seqlens)
 
 The `*_closed` functions are the same quantities written as closed forms of the token index; the
 tests check each `*_ref` against its closed form on every small grid, so a slip in either
@@ -190,6 +192,64 @@ def merged_row_closed(grid_thw, merge: int = 2) -> np.ndarray:
         out.append(G)
         off += int(t * h * w)
     return np.concatenate(out) if out else np.zeros(0, np.int64)
+
+
+def window_index_ref(grid_thw, merge: int, patch: int, window_size: int):
+    """`_get_window_index` (model.py:769-799): pad each frame's merge-group grid to whole windows
+    with -100, reshape/transpose into windows, drop the padding. Returns (window_index, cu_window)."""
+    vw = window_size // merge // patch
+    idxs, cu, wid = [], [0], 0
+    for t, h, w in _grid(grid_thw):
+        gh, gw = h // merge, w // merge
+        index = np.arange(t * gh * gw).reshape(t, gh, gw)
+        ph, pw = (vw - gh % vw) % vw, (vw - gw % vw) % vw
+        nh, nw = (gh + ph) // vw, (gw + pw) // vw
+        pad = np.pad(index, ((0, 0), (0, ph), (0, pw)), constant_values=-100)
+        pad = pad.reshape(t, nh, vw, nw, vw).transpose(0, 1, 3, 2, 4).reshape(t, nh * nw, vw, vw)
+        seqlens = (pad != -100).sum(axis=(2, 3)).reshape(-1)
+        flat = pad.reshape(-1)
+        idxs.append(flat[flat != -100] + wid)
+        cu.extend(list(np.cumsum(seqlens) * merge * merge + cu[-1]))
+        wid += int(t * gh * gw)
+    cu = np.asarray(cu, np.int64)
+    keep = np.concatenate([[True], cu[1:] != cu[:-1]])
+    widx = np.concatenate(idxs) if idxs else np.zeros(0, np.int64)
+    return widx.astype(np.int64), cu[keep]
+
+
+def window_index_closed(grid_thw, merge: int, patch: int, window_size: int):
+    """Window id and window-order position of every merge group, from its (frame, row, col):
+    window = (frame, row // vw, col // vw) numbered frame-major then row-major over the padded
+    window grid; inside a window, groups are row-major. Returns (window_index, cu_window)."""
+    vw = window_size // merge // patch
+    keyed, sizes, wid, win_off = [], [], 0, 0
+    for t, h, w in _grid(grid_thw):
+        gh, gw = h // merge, w // merge
+        nh, nw = -(-gh // vw), -(-gw // vw)
+        for f in range(t):
+            for r in range(gh):
+                for c in range(gw):
+                    win = win_off + (f * nh + r // vw) * nw + c // vw
+                    keyed.append((win, (r % vw) * vw + c % vw, wid + (f * gh + r) * gw + c))
+        for f in range(t):
+            for a in range(nh):
+                for b in range(nw):
+                    sizes.append(min(vw, gh - a * vw) * min(vw, gw - b * vw))
+        win_off += t * nh * nw
+        wid += t * gh * gw
+    keyed.sort()
+    cu = np.concatenate([[0], np.cumsum(sizes) * merge * merge])
+    keep = np.concatenate([[True], cu[1:] != cu[:-1]])
+    return np.asarray([k[2] for k in keyed], np.int64), cu[keep]
+
+
+def cu_full_window_ref(grid_thw, merge: int) -> np.ndarray:
+    """model.py:828-830: [0, cumsum(t*h*w*merge^2)] — in tokens times merge^2 — with each bound
+    clamped to n_tokens as the reference's q[start:end] slicing clamps it."""
+    g = _grid(grid_thw)
+    n = int((g[:, 0] * g[:, 1] * g[:, 2]).sum())
+    cu = np.concatenate([[0], np.cumsum(g[:, 0] * g[:, 1] * g[:, 2] * merge * merge)])
+    return np.minimum(cu, n)
 
 
 def attention_tiles(cu_seqlens, block_m: int, num_heads: int = 1, queues: int = 8):

@@ -154,6 +154,13 @@ class VisionSpec:
     in_channels: int = 3
     num_position_embeddings: int = 2304
     deepstack_visual_indexes: Tuple[int, ...] = (5, 11, 17)
+    window_size: int = 32
+    fullatt_block_indexes: Optional[Tuple[int, ...]] = None      # None: every block (qwen3_vl)
+
+    @property
+    def use_window(self) -> bool:
+        fa = self.fullatt_block_indexes
+        return fa is not None and len(set(fa)) < self.depth
 
     @property
     def head_dim(self) -> int:
@@ -290,17 +297,34 @@ def encode_vision(params: Dict, pixel_values, grid_thw, spec: VisionSpec, precis
     embed = x.copy() if keep_layers else None
     cos, sin = rotary_cos_sin(grid, spec, p)
     cu = ix.cu_seqlens_ref(grid)
+    window = spec.use_window
+    if window:
+        # model.py:808-830: shuffle x and the rotary table by merge groups into window order;
+        # window blocks use cu_window, full blocks the window path's cu_seqlens
+        mm = spec.spatial_merge_size ** 2
+        widx, cu_win = ix.window_index_ref(grid, spec.spatial_merge_size, spec.patch_size, spec.window_size)
+        n = x.shape[0]
+        x = x.reshape(n // mm, mm, -1)[widx].reshape(n, -1)
+        cos = cos.reshape(n // mm, mm, -1)[widx].reshape(n, -1)
+        sin = sin.reshape(n // mm, mm, -1)[widx].reshape(n, -1)
+        cu = ix.cu_full_window_ref(grid, spec.spatial_merge_size)
+        fullatt = set(spec.fullatt_block_indexes)
     ds = set(spec.deepstack_visual_indexes)
     feats, layers = [], []
     nblk = spec.depth if depth is None else depth
     for i in range(nblk):
-        x = vision_block(x, prm[f"blocks_{i}"], cos, sin, cu, spec, p)
+        cu_i = cu if (not window or i in fullatt) else cu_win
+        x = vision_block(x, prm[f"blocks_{i}"], cos, sin, cu_i, spec, p)
         if keep_layers:
             layers.append(x.copy())
         if i in ds:
             j = len(feats)
             feats.append(patch_merger(x, prm[f"deepstack_mergers_{j}"], spec, True, p))
     tokens = patch_merger(x, prm["merger"], spec, False, p)
+    if window:
+        rev = np.argsort(widx, kind="stable")          # model.py:845-848
+        tokens = tokens[rev]
+        feats = [f[rev] for f in feats]
     return OracleOutput(tokens=tokens, deepstack=tuple(feats), layers=layers, embed=embed)
 
 

@@ -31,7 +31,8 @@ class VisionConfig(C.Structure):
     _fields_ = [("hidden_size", _i32), ("out_hidden_size", _i32), ("depth", _i32), ("num_heads", _i32),
                 ("intermediate_size", _i32), ("patch_volume", _i32), ("spatial_merge_size", _i32),
                 ("num_position_embeddings", _i32), ("n_deepstack", _i32), ("deepstack_indexes", _i32 * 8),
-                ("ln_eps", _f32), ("rope_theta", _f32), ("dtype", _i32)]
+                ("ln_eps", _f32), ("rope_theta", _f32), ("dtype", _i32), ("use_window", _i32),
+                ("fullatt_mask", C.c_uint64)]
 
 
 class BlockWeights(C.Structure):
@@ -51,7 +52,8 @@ class VisionWeights(C.Structure):
 
 class VisionMetadataDev(C.Structure):
     _fields_ = [("n_tokens", _i64), ("n_tiles", _i64), ("pos_hw", _p), ("tap_idx", _p), ("tap_w", _p),
-                ("tiles", _p)]
+                ("tiles", _p), ("n_window_tiles", _i64), ("window_tiles", _p), ("window_index", _p),
+                ("window_reverse", _p)]
 
 
 # name -> (restype, argtypes); every function in include/qvl_vision.h
@@ -79,6 +81,8 @@ SIGNATURES = {
     "qvl_encode_vision_workspace_size": (C.c_int, [C.POINTER(VisionConfig), _i64, C.POINTER(_sz)]),
     "qvl_encode_vision": (C.c_int, [_p, C.POINTER(VisionConfig), C.POINTER(VisionWeights),
                                     C.POINTER(VisionMetadataDev), _p, _p, C.POINTER(_p), _p, _sz]),
+    "qvl_window_metadata": (C.c_int, [_pi32, _i64, _i32, _i32, _i32, _pi32, _pi32, _i64, C.POINTER(_i64), _pi32]),
+    "qvl_gather_rows": (C.c_int, [_p, _i32, _p, _i64, _i32, _p, _i64, _p, _i64, _i32, _i64]),
     "qvl_patchify": (C.c_int, [_p, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _i64]),
     "qvl_vision_positions": (C.c_int, [_p, _p, _i64, _i64, _i32, _i64, _p, _p]),
     "qvl_scatter_vision_rows": (C.c_int, [_p, _i32, _i32, _p, _i64, _i64, _i64, _i32, _p, _i64, _i64, _p, _p]),

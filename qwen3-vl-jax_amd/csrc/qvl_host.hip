@@ -170,6 +170,60 @@ int qvl_vision_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int
   return QVL_OK;
 }
 
+// model.py:769-799 (_get_window_index) and 828-830 (the full-attention cu_seqlens of the window
+// branch, which scales token counts by merge_unit: its boundaries are clamped to n_tokens here as
+// the reference's q[start:end] slicing clamps them).
+int qvl_window_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int32_t patch_size, int32_t window_size,
+                        int32_t* window_index, int32_t* cu_window, int64_t capacity, int64_t* n_cu_window,
+                        int32_t* cu_full) {
+  int64_t N = 0, S = 0;
+  int rc = qvl_grid_counts(grid, n_grids, merge, &N, &S);
+  if (rc) return rc;
+  if (!n_cu_window) return set_error(QVL_ERR_INVALID_ARG, "window metadata: n_cu_window is NULL");
+  if (patch_size <= 0) return set_error(QVL_ERR_INVALID_ARG, "patch_size=%d", patch_size);
+  const int vw = window_size / merge / patch_size;   // vit_merger_window_size
+  if (vw <= 0) return set_error(QVL_ERR_INVALID_ARG, "window_size=%d gives an empty window", window_size);
+  const int64_t mm = (int64_t)merge * merge;
+  std::vector<int32_t> cu(1, 0);
+  int64_t wid = 0, k = 0;
+  for (int64_t i = 0; i < n_grids; ++i) {
+    const int64_t t = grid[3 * i], gh = grid[3 * i + 1] / merge, gw = grid[3 * i + 2] / merge;
+    const int64_t nh = (gh + vw - 1) / vw, nw = (gw + vw - 1) / vw;
+    for (int64_t f = 0; f < t; ++f)
+      for (int64_t a = 0; a < nh; ++a)
+        for (int64_t b = 0; b < nw; ++b) {
+          int64_t len = 0;
+          for (int64_t ih = 0; ih < vw; ++ih)
+            for (int64_t iw = 0; iw < vw; ++iw) {
+              const int64_t r = a * vw + ih, c = b * vw + iw;
+              if (r >= gh || c >= gw) continue;              // the -100 padding
+              if (window_index) window_index[k] = (int32_t)(wid + (f * gh + r) * gw + c);
+              ++k;
+              ++len;
+            }
+          const int32_t next = (int32_t)(cu.back() + len * mm);
+          if (next != cu.back()) cu.push_back(next);          // consecutive duplicates dropped
+        }
+    wid += t * gh * gw;
+  }
+  *n_cu_window = (int64_t)cu.size();
+  if (cu_window) {
+    if (capacity < (int64_t)cu.size())
+      return set_error(QVL_ERR_INVALID_ARG, "window metadata: cu_window capacity %lld < %lld", (long long)capacity,
+                       (long long)cu.size());
+    memcpy(cu_window, cu.data(), cu.size() * sizeof(int32_t));
+  }
+  if (cu_full) {
+    int64_t acc = 0;
+    cu_full[0] = 0;
+    for (int64_t i = 0; i < n_grids; ++i) {
+      acc += (int64_t)grid[3 * i] * grid[3 * i + 1] * grid[3 * i + 2] * mm;
+      cu_full[i + 1] = (int32_t)std::min<int64_t>(acc, N);
+    }
+  }
+  return QVL_OK;
+}
+
 int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, int32_t* items, int64_t capacity,
                            int64_t* n_items) {
   if (!cu || !n_items) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens / n_items is NULL");
@@ -558,11 +612,26 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   const int64_t N = L.N, D = L.D, I = L.I_pad;
   const size_t e = L.esz;
   const float qscale = (1.0f / sqrtf((float)L.hd)) * kLog2e;
+  const bool win = c->use_window != 0;
+  const int64_t Dout = c->out_hidden_size;
+  if (win) {
+    if (c->depth > 64) return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: window mode with depth > 64");
+    if (!meta->window_index || !meta->window_reverse || (meta->n_window_tiles > 0 && !meta->window_tiles))
+      return set_error(QVL_ERR_INVALID_ARG, "encode_vision: window metadata missing");
+    // merger outputs are staged in the (then idle) q buffer before the unshuffle
+    if ((N / 4) * Dout > L.H * L.Np * L.hdp)
+      return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: window mode with out_hidden_size > 4 * hidden");
+  }
 
   // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823); in fp32 the
-  // pixels feed the GEMM directly
+  // pixels feed the GEMM directly. Window mode: the pixel rows are taken in window order (the
+  // reference shuffles x after the row-wise patch embed and pos-embed add, model.py:809-812; the
+  // metadata's taps and rotary ids arrive in window order).
   const void* px_in = px;
-  if (!f32) {
+  if (win) {
+    QVL_TRY_RC(qvl_gather_rows(st, QVL_DTYPE_F32, px, L.PV, dt, h, L.PV, meta->window_index, N, 4, L.PV));
+    px_in = h;
+  } else if (!f32) {
     QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
     px_in = h;
   }
@@ -592,7 +661,10 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
                                               (int)N, (int)L.Np, (int)L.H, (int)L.hd, L.hdp, L.vrows, qscale,
                                               (bf16*)Qb, (bf16*)Kb, (bf16*)Vb, st));
     }
-    QVL_TRY_RC(qvl_attention_headmajor(st, dt, Qb, Kb, Vb, meta->tiles, meta->n_tiles, N, (int)L.H, (int)L.hd, xn, D));
+    // window mode: blocks outside fullatt_block_indexes attend within windows (model.py:838-839)
+    const bool full = !win || ((c->fullatt_mask >> i) & 1ull);
+    QVL_TRY_RC(qvl_attention_headmajor(st, dt, Qb, Kb, Vb, full ? meta->tiles : meta->window_tiles,
+                                       full ? meta->n_tiles : meta->n_window_tiles, N, (int)L.H, (int)L.hd, xn, D));
     QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, part, PB));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
     QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
@@ -601,12 +673,16 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     // deepstack tap (model.py:841-843)
     for (int j = 0; j < c->n_deepstack; ++j)
       if (c->deepstack_indexes[j] == i) {
-        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, deepstack[ds_next], part));
+        void* out = win ? (void*)Qb : deepstack[ds_next];
+        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, out, part));
+        if (win)   // unshuffle (model.py:845-848)
+          QVL_TRY_RC(qvl_gather_rows(st, dt, Qb, Dout, dt, deepstack[ds_next], Dout, meta->window_reverse, N / 4, 1, Dout));
         ++ds_next;
       }
   }
   (void)e;
-  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, tokens, part));
+  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, win ? (void*)Qb : tokens, part));
+  if (win) QVL_TRY_RC(qvl_gather_rows(st, dt, Qb, Dout, dt, tokens, Dout, meta->window_reverse, N / 4, 1, Dout));
   return QVL_OK;
 }
 

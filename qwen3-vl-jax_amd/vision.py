@@ -42,13 +42,21 @@ class VisionBackboneSpec:
     spatial_merge_size: int = 2
     window_size: int = 32
     in_channels: int = 3
-    fullatt_block_indexes: Sequence[int] = ()
+    # None = every block (what spec_from_config fixes for qwen3_vl, model.py:1033-1034); a list
+    # that misses blocks selects the window-attention path for them (model.py:808-850).
+    fullatt_block_indexes: Optional[Sequence[int]] = None
     num_position_embeddings: Optional[int] = 2304
     deepstack_visual_indexes: Sequence[int] = ()
 
     @property
     def head_dim(self) -> int:
         return self.hidden_size // self.num_heads
+
+    @property
+    def use_window(self) -> bool:
+        """model.py:809-810: window attention when the full-attention set is smaller than the depth."""
+        fa = self.fullatt_block_indexes
+        return fa is not None and len(set(fa)) < self.depth
 
     @property
     def patch_volume(self) -> int:
@@ -150,6 +158,42 @@ class GridMetadata:
     tap_idx: np.ndarray
     tap_w: np.ndarray
     tiles: np.ndarray
+    # window mode only (model.py:769-799, 808-830): pos_hw / tap_* above are then in window order
+    # and `tiles` is the worklist of cu_full
+    window_index: Optional[np.ndarray] = None
+    window_reverse: Optional[np.ndarray] = None
+    cu_window: Optional[np.ndarray] = None
+    cu_full: Optional[np.ndarray] = None
+    window_tiles: Optional[np.ndarray] = None
+
+
+def _worklist(lib, cu: np.ndarray, num_heads: int) -> np.ndarray:
+    cu = np.ascontiguousarray(cu, np.int32)
+    n = C.c_int64()
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), len(cu) - 1, num_heads, None, 0, C.byref(n)),
+               "qvl_attention_worklist")
+    tiles = np.zeros((max(n.value, 1), 4), np.int32)
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), len(cu) - 1, num_heads, _i32p(tiles), n.value, C.byref(n)),
+               "qvl_attention_worklist")
+    return tiles[: n.value]
+
+
+def window_metadata(grid_thw, merge: int = 2, patch_size: int = 16, window_size: int = 32):
+    """(window_index [N/merge^2], cu_window, cu_full) of `_get_window_index` and the window path's
+    full-attention cu_seqlens (model.py:769-799, 828-830), from qvl_window_metadata."""
+    g = np.ascontiguousarray(np.asarray(grid_thw, dtype=np.int32).reshape(-1, 3))
+    lib = capi.load()
+    nt = C.c_int64()
+    capi.check(lib.qvl_grid_counts(_i32p(g), g.shape[0], merge, C.byref(nt), None), "qvl_grid_counts")
+    ncu = C.c_int64()
+    capi.check(lib.qvl_window_metadata(_i32p(g), g.shape[0], merge, patch_size, window_size, None, None, 0,
+                                       C.byref(ncu), None), "qvl_window_metadata")
+    widx = np.zeros(max(nt.value // (merge * merge), 1), np.int32)
+    cuw = np.zeros(ncu.value, np.int32)
+    cuf = np.zeros(g.shape[0] + 1, np.int32)
+    capi.check(lib.qvl_window_metadata(_i32p(g), g.shape[0], merge, patch_size, window_size, _i32p(widx), _i32p(cuw),
+                                       ncu.value, C.byref(ncu), _i32p(cuf)), "qvl_window_metadata")
+    return widx[: nt.value // (merge * merge)], cuw, cuf
 
 
 def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
@@ -165,12 +209,22 @@ def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
     w = np.zeros((4, N), np.float32)
     capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, num_position_embeddings, dtype, _i32p(cu),
                                        _i32p(pos), _i32p(idx), _f32p(w)), "qvl_vision_metadata")
-    nti = C.c_int64()
-    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, num_heads, None, 0, C.byref(nti)), "qvl_attention_worklist")
-    tiles = np.zeros((max(nti.value, 1), 4), np.int32)
-    capi.check(lib.qvl_attention_worklist(_i32p(cu), S, num_heads, _i32p(tiles), nti.value, C.byref(nti)),
-               "qvl_attention_worklist")
-    return GridMetadata(N, cu, pos, idx, w, tiles[: nti.value])
+    return GridMetadata(N, cu, pos, idx, w, _worklist(lib, cu, num_heads))
+
+
+def window_grid_metadata(m: GridMetadata, grid_thw, merge: int, patch_size: int, window_size: int,
+                         num_heads: int) -> GridMetadata:
+    """`m` re-expressed for the window path: per-token metadata in window order (the reference
+    shuffles x and the rotary ids by merge groups, model.py:809-812), the worklists of cu_full and
+    cu_window, and the unshuffle index argsort(window_index) (model.py:845-848)."""
+    lib = capi.load()
+    widx, cuw, cuf = window_metadata(grid_thw, merge, patch_size, window_size)
+    mm = merge * merge
+    perm = (widx.astype(np.int64)[:, None] * mm + np.arange(mm)[None, :]).reshape(-1)
+    rev = np.argsort(widx, kind="stable").astype(np.int32)
+    return GridMetadata(m.n_tokens, m.cu_seqlens, np.ascontiguousarray(m.pos_hw[perm]),
+                        np.ascontiguousarray(m.tap_idx[:, perm]), np.ascontiguousarray(m.tap_w[:, perm]),
+                        _worklist(lib, cuf, num_heads), widx, rev, cuw, cuf, _worklist(lib, cuw, num_heads))
 
 
 # ---------------------------------------------------------------------------------------------
@@ -217,6 +271,11 @@ class Qwen3VisionTransformer:
         cfg.ln_eps = 1e-6
         cfg.rope_theta = 10000.0
         cfg.dtype = self.qdtype
+        if spec.use_window:
+            if spec.depth > 64:
+                raise NotImplementedError("window attention with depth > 64")
+            cfg.use_window = 1
+            cfg.fullatt_mask = sum(1 << i for i in set(spec.fullatt_block_indexes) if 0 <= i < spec.depth)
         self._cfg = cfg
 
     # -- weights --------------------------------------------------------------------------------
@@ -376,16 +435,27 @@ class Qwen3VisionTransformer:
         hit = self._meta_cache.get(key)
         if hit is not None:
             return hit
-        m = grid_metadata(g, self.spec.spatial_merge_size, self.spec.num_position_embeddings, self.qdtype,
-                          self.spec.num_heads)
+        s = self.spec
+        m = grid_metadata(g, s.spatial_merge_size, s.num_position_embeddings, self.qdtype, s.num_heads)
+        if s.use_window:
+            m = window_grid_metadata(m, g, s.spatial_merge_size, s.patch_size, s.window_size, s.num_heads)
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
+        nz = lambda a: a if a is not None and len(a) else np.zeros((1, 4), np.int32)
         tens = {"cu_seqlens": dev(m.cu_seqlens), "pos_hw": dev(m.pos_hw), "tap_idx": dev(m.tap_idx),
-                "tap_w": dev(m.tap_w), "tiles": dev(m.tiles if len(m.tiles) else np.zeros((1, 4), np.int32))}
+                "tap_w": dev(m.tap_w), "tiles": dev(nz(m.tiles))}
         md = capi.VisionMetadataDev()
         md.n_tokens = m.n_tokens
         md.n_tiles = len(m.tiles)
         md.pos_hw, md.tap_idx, md.tap_w, md.tiles = (tens["pos_hw"].data_ptr(), tens["tap_idx"].data_ptr(),
                                                      tens["tap_w"].data_ptr(), tens["tiles"].data_ptr())
+        if s.use_window:
+            tens["window_tiles"] = dev(nz(m.window_tiles))
+            tens["window_index"] = dev(m.window_index if len(m.window_index) else np.zeros(1, np.int32))
+            tens["window_reverse"] = dev(m.window_reverse if len(m.window_reverse) else np.zeros(1, np.int32))
+            md.n_window_tiles = len(m.window_tiles)
+            md.window_tiles = tens["window_tiles"].data_ptr()
+            md.window_index = tens["window_index"].data_ptr()
+            md.window_reverse = tens["window_reverse"].data_ptr()
         entry = (m, tens, md)
         self._meta_cache[key] = entry
         return entry
@@ -427,6 +497,8 @@ class Qwen3VisionTransformer:
     # -- staged forward: one C-ABI stage entry per reference op, with per-layer taps -------------
     def _staged_ctx(self, grid_thw):
         torch = _torch()
+        if self.spec.use_window:
+            raise NotImplementedError("the staged path runs full attention only; window specs run through __call__")
         m, tens, md = self.metadata(grid_thw)
         s = self.spec
         N, D, H, hd = m.n_tokens, s.hidden_size, s.num_heads, s.head_dim

@@ -180,3 +180,27 @@ def test_io_entry_argument_checks(pkg):
     assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_ADD, BF, fake, 1, 8, 4, F32, fake, -1, 2, fake, fake) == -1
     assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_ADD, BF, fake, 1, 8, 4, F32, fake, 0, 0, fake, fake) == 0
     assert lib.qvl_scatter_vision_rows(None, cp.QVL_SCATTER_SET, BF, fake, 1, 8, 4, F32, None, 0, 2, fake, fake) == -1
+
+
+def test_window_entry_argument_checks(pkg):
+    lib = pkg.capi.load()
+    cp = pkg.capi
+    g = np.array([[1, 8, 12]], np.int32)
+    n = C.c_int64()
+    gp = g.ctypes.data_as(C.POINTER(C.c_int32))
+    # window smaller than one merge group, odd grid, missing count pointer
+    assert lib.qvl_window_metadata(gp, 1, 2, 16, 16, None, None, 0, C.byref(n), None) == -1
+    bad = np.array([[1, 7, 12]], np.int32)
+    assert lib.qvl_window_metadata(bad.ctypes.data_as(C.POINTER(C.c_int32)), 1, 2, 16, 64, None, None, 0,
+                                   C.byref(n), None) == -1
+    assert lib.qvl_window_metadata(gp, 1, 2, 16, 64, None, None, 0, None, None) == -1
+    # capacity too small
+    assert lib.qvl_window_metadata(gp, 1, 2, 16, 64, None, None, 0, C.byref(n), None) == 0
+    cu = np.zeros(n.value, np.int32)
+    assert lib.qvl_window_metadata(gp, 1, 2, 16, 64, None, cu.ctypes.data_as(C.POINTER(C.c_int32)), n.value - 1,
+                                   C.byref(n), None) == -1
+    fake = 1 << 20
+    assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 8, 5, fake, 8, fake, 8, 4, 8) == -2
+    assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 8, cp.QVL_DTYPE_F32, fake, 8, fake, 6, 4, 8) == -1
+    assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 4, cp.QVL_DTYPE_F32, fake, 8, fake, 8, 4, 8) == -1
+    assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 8, cp.QVL_DTYPE_F32, fake, 8, fake, 0, 4, 8) == 0

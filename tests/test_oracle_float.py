@@ -125,3 +125,80 @@ def test_patchify_layout():
     for n in range(px.shape[0]):
         blk = dup[:, :, 2 * r[n]:2 * r[n] + 2, 2 * c[n]:2 * c[n] + 2]       # (Tp, C, P, P)
         np.testing.assert_array_equal(px[n], blk.transpose(1, 0, 2, 3).reshape(-1))
+
+
+# ---------------------------------------------------------------------------------------------
+# window-attention path (model.py:808-850): permutation formulation vs a dense mask in token order
+# ---------------------------------------------------------------------------------------------
+def _masked_window_tower(params, px, grid, spec):
+    """The window path without any shuffle: every block attends through an explicit token x token
+    mask in the original order (same window / same full-attention range of the window order)."""
+    p = P64
+    prm = params["visual"]
+    x = vt.dense(px, prm["patch_embed"]["proj"]["kernel"], prm["patch_embed"]["proj"]["bias"], p)
+    x = x + vt.pos_embed(prm["pos_embed"]["embedding"], grid, spec, p)
+    cos, sin = vt.rotary_cos_sin(grid, spec, p)
+    n, D, H, hd = x.shape[0], spec.hidden_size, spec.num_heads, spec.head_dim
+    widx, cuw = ix.window_index_closed(grid, spec.spatial_merge_size, spec.patch_size, spec.window_size)
+    wpos = np.empty(n, np.int64)                           # window-order position of each token
+    for r, g in enumerate(widx):
+        wpos[4 * g:4 * g + 4] = 4 * r + np.arange(4)
+    win = np.searchsorted(cuw, wpos, side="right")
+    full = np.searchsorted(ix.cu_full_window_ref(grid, 2), wpos, side="right")
+    masks = {True: full[:, None] == full[None, :], False: win[:, None] == win[None, :]}
+    feats = []
+    for i in range(spec.depth):
+        b = prm[f"blocks_{i}"]
+        h = vt.layer_norm(x, b["norm1"]["weight"], b["norm1"]["bias"], 1e-6, p)
+        qkv = vt.dense(h, b["attn"]["qkv"]["kernel"], b["attn"]["qkv"]["bias"], p)
+        q = vt.apply_rotary(qkv[:, :D].reshape(n, H, hd), cos, sin, p)
+        k = vt.apply_rotary(qkv[:, D:2 * D].reshape(n, H, hd), cos, sin, p)
+        v = qkv[:, 2 * D:].reshape(n, H, hd)
+        m = masks[i in set(spec.fullatt_block_indexes)]
+        o = np.zeros((n, H, hd))
+        for hh in range(H):
+            sc = (q[:, hh] @ k[:, hh].T) * hd ** -0.5
+            sc = np.where(m, sc, -np.inf)
+            sc = np.exp(sc - sc.max(axis=1, keepdims=True))
+            o[:, hh] = (sc / sc.sum(axis=1, keepdims=True)) @ v[:, hh]
+        x = x + vt.dense(o.reshape(n, D), b["attn"]["proj"]["kernel"], b["attn"]["proj"]["bias"], p)
+        h = vt.layer_norm(x, b["norm2"]["weight"], b["norm2"]["bias"], 1e-6, p)
+        x = x + vt.vision_mlp(h, b["mlp"], p)
+        if i in set(spec.deepstack_visual_indexes):
+            feats.append(vt.patch_merger(x, prm[f"deepstack_mergers_{len(feats)}"], spec, True, p))
+    return vt.patch_merger(x, prm["merger"], spec, False, p), feats
+
+
+WSPEC = vt.VisionSpec(hidden_size=32, out_hidden_size=24, depth=4, num_heads=2, intermediate_size=48,
+                      patch_size=4, temporal_patch_size=2, spatial_merge_size=2, in_channels=3,
+                      num_position_embeddings=64, deepstack_visual_indexes=(0, 2), window_size=16,
+                      fullatt_block_indexes=(1, 3))
+
+
+@pytest.mark.parametrize("grids", [[(1, 8, 12)], [(1, 8, 12), (2, 4, 4)], [(2, 6, 10)], [(1, 12, 4), (1, 4, 8)]])
+def test_window_path_vs_dense_mask(grids):
+    params = vt.init_params(WSPEC, seed=6, bias_std=0.1, ln_noise=0.1)
+    n = sum(t * h * w for t, h, w in grids)
+    px = np.random.default_rng(1).standard_normal((n, WSPEC.patch_volume))
+    out = vt.encode_vision(params, px, grids, WSPEC, "fp64")
+    tok, feats = _masked_window_tower(params, px, np.asarray(grids), WSPEC)
+    np.testing.assert_allclose(out.tokens, tok, rtol=1e-10, atol=1e-10)
+    for a, b in zip(out.deepstack, feats):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-10)
+    # and the windows really restrict attention: the full-attention-only tower differs
+    import dataclasses
+    full = vt.encode_vision(params, px, grids, dataclasses.replace(WSPEC, fullatt_block_indexes=None), "fp64")
+    assert rel_l2(full.tokens, out.tokens) > 1e-3
+
+
+def test_window_covering_whole_frames_equals_full_path():
+    """One window per frame (window_size >= frame) and no full blocks: window order is the identity
+    and cu_window the per-frame cu_seqlens, so the window path equals the standard path."""
+    import dataclasses
+    spec = dataclasses.replace(WSPEC, window_size=64, fullatt_block_indexes=())
+    params = vt.init_params(spec, seed=2)
+    grids = [(1, 8, 8), (2, 4, 8)]
+    px = np.random.default_rng(3).standard_normal((sum(t * h * w for t, h, w in grids), spec.patch_volume))
+    a = vt.encode_vision(params, px, grids, spec, "fp64")
+    b = vt.encode_vision(params, px, grids, dataclasses.replace(spec, fullatt_block_indexes=None), "fp64")
+    np.testing.assert_allclose(a.tokens, b.tokens, rtol=1e-12, atol=1e-12)

@@ -112,3 +112,49 @@ def test_attention_tiles_cover_every_query_once(heads):
         seg_len = np.diff(cu)
         biggest = max(-(-L // bm) * L for L in seg_len)
         assert load.max() - load.min() <= biggest
+
+
+# ---------------------------------------------------------------------------------------------
+# window attention metadata (model.py:769-799, 828-830)
+# ---------------------------------------------------------------------------------------------
+WINDOW_GRIDS = [[(1, 8, 12)], [(1, 8, 12), (2, 4, 4)], [(3, 10, 6)], [(1, 2, 2)], [(2, 14, 18), (1, 6, 4)],
+                [(1, 16, 16)], [(4, 6, 10)]]
+
+
+@pytest.mark.parametrize("grids", WINDOW_GRIDS)
+@pytest.mark.parametrize("merge,patch,window", [(2, 14, 112), (2, 16, 64), (2, 16, 32), (2, 14, 56)])
+def test_window_index_ref_vs_closed_and_transformers(grids, merge, patch, window):
+    torch = pytest.importorskip("torch")
+    a, ca = ix.window_index_ref(grids, merge, patch, window)
+    b, cb = ix.window_index_closed(grids, merge, patch, window)
+    assert np.array_equal(a, b) and np.array_equal(ca, cb)
+    assert sorted(a.tolist()) == list(range(len(a)))                  # a permutation of merge groups
+    try:
+        from transformers.vision_utils import get_vision_window_index
+    except ImportError:
+        pytest.skip("transformers.vision_utils not available")
+    hi, hc = get_vision_window_index(torch.tensor(grids), spatial_merge_size=merge, window_size=window,
+                                     patch_size=patch)
+    assert np.array_equal(a, hi.numpy()) and np.array_equal(ca, np.asarray(hc))
+
+
+@pytest.mark.parametrize("grids", WINDOW_GRIDS)
+def test_cu_full_window_matches_slice_semantics(grids):
+    """The reference's q[start:end] over [0, N) with the unclamped merge^2-scaled bounds."""
+    g = np.asarray(grids)
+    n = int((g[:, 0] * g[:, 1] * g[:, 2]).sum())
+    raw = np.concatenate([[0], np.cumsum(g[:, 0] * g[:, 1] * g[:, 2] * 4)])
+    cu = ix.cu_full_window_ref(grids, 2)
+    tokens = list(range(n))
+    for i in range(len(raw) - 1):
+        assert tokens[raw[i]:raw[i + 1]] == tokens[cu[i]:cu[i + 1]]
+    assert cu[-1] == n
+
+
+@pytest.mark.parametrize("grids", WINDOW_GRIDS)
+@pytest.mark.parametrize("patch,window", [(14, 112), (16, 64)])
+def test_window_metadata_host_bit_exact(pkg, grids, patch, window):
+    widx, cuw, cuf = pkg.vision.window_metadata(grids, 2, patch, window)
+    a, ca = ix.window_index_ref(grids, 2, patch, window)
+    assert np.array_equal(widx, a) and np.array_equal(cuw, ca)
+    assert np.array_equal(cuf, ix.cu_full_window_ref(grids, 2))
