@@ -152,6 +152,18 @@ def main():
     ln_g = torch.ones(D, device=dev)
     ln_b = torch.zeros(D, device=dev)
     px_b = torch.empty((N, spec.patch_volume), dtype=torch.bfloat16, device=dev)
+    frames_u8 = torch.randint(0, 256, (8, 768, 768, 3), dtype=torch.uint8, device=dev)
+    px_p = torch.empty((N, spec.patch_volume), dtype=torch.float32, device=dev)
+    V, Dtxt = N // 4, spec.out_hidden_size
+    S_txt = V + 512
+    tok_txt = torch.zeros((1, S_txt), dtype=torch.int32, device=dev)
+    tok_txt[0, 256:256 + V] = 1
+    hid = torch.randn((1, S_txt, Dtxt), device=dev).to(torch.bfloat16)
+    vrows = torch.randn((V, Dtxt), device=dev).to(torch.bfloat16)
+    vpos = torch.empty((1, V), dtype=torch.int32, device=dev)
+    vcnt = torch.empty((1,), dtype=torch.int32, device=dev)
+    cp.check(lib.qvl_vision_positions(s_, tok_txt.data_ptr(), 1, S_txt, 1, V, vpos.data_ptr(), vcnt.data_ptr()),
+             "positions")
     kernels = {
         # name: (callable, "mfma" FLOPs or "hbm" bytes per launch, bound, launches per step)
         "fc1 (gemm, bias+GELU) 18432x4096x1024": (
@@ -184,6 +196,20 @@ def main():
         "cast pixels f32->bf16 (18432x1536)": (
             lambda: lib.qvl_cast(s_, BF, px.data_ptr(), px_b.data_ptr(), N * spec.patch_volume),
             N * spec.patch_volume * 6.0, "hbm", 1),
+        # the steps either side of the tower (not in the step time): on-device patchify of the 8
+        # uint8 frames, and the decoder-side injection / deepstack add of the 4608 vision rows
+        "patchify (8 x 768x768x3 uint8 -> 18432x1536 f32)": (
+            lambda: lib.qvl_patchify(s_, cp.QVL_DTYPE_F32, frames_u8.data_ptr(), 8, 768, 768, 3, 16, 2, 2,
+                                     px_p.data_ptr(), spec.patch_volume),
+            8 * 768 * 768 * 3 + N * spec.patch_volume * 4.0, "hbm", 0),
+        "inject vision rows (4608 x 2048 bf16 into 5120 x 2048)": (
+            lambda: lib.qvl_scatter_vision_rows(s_, cp.QVL_SCATTER_SET, BF, hid.data_ptr(), 1, S_txt, Dtxt, BF,
+                                                vrows.data_ptr(), 0, V, vpos.data_ptr(), vcnt.data_ptr()),
+            2.0 * V * Dtxt * 2, "hbm", 0),
+        "deepstack add (4608 x 2048 bf16)": (
+            lambda: lib.qvl_scatter_vision_rows(s_, cp.QVL_SCATTER_ADD, BF, hid.data_ptr(), 1, S_txt, Dtxt, BF,
+                                                vrows.data_ptr(), 0, V, vpos.data_ptr(), vcnt.data_ptr()),
+            3.0 * V * Dtxt * 2, "hbm", 0),
     }
     if args.only:
         if args.only == "copy":      # plain copy of known size, the calibration for the HBM byte counters
@@ -198,8 +224,34 @@ def main():
         torch.cuda.synchronize()
         print(f"bench.py --only {args.only}: {args.kernel_reps} launches", flush=True)
         return
-    kstats = {}
+    # The per-block kernels are timed inside a replay of one block's launch sequence (the order
+    # the tower runs them): the GPU's clock under a sustained single-kernel loop drops well below
+    # its level in the tower (power), so an isolated loop would misstate each kernel's share of
+    # the step. Each kernel launches GROUP times back to back between one pair of HIP events on
+    # the launch stream, which spreads the events' own cost (a few us) over the group. The rest
+    # run in back-to-back loops of their own.
+    GROUP = 4
+    name_of = {k.split(" ")[0]: k for k in kernels}
+    block_seq = [name_of[k] for k in ("layer_norm", "qkv+rotary", "attention", "proj", "layer_norm", "fc1", "fc2")]
+    times = {k: [] for k in kernels}
+    for _ in range(2):
+        for name in block_seq:
+            cp.check(kernels[name][0](), name)
+    evs = []
+    for _ in range(args.kernel_reps):
+        for name in block_seq:
+            a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a_.record(st)
+            for _ in range(GROUP):
+                kernels[name][0]()
+            b_.record(st)
+            evs.append((name, a_, b_))
+    torch.cuda.synchronize()
+    for name, a_, b_ in evs:
+        times[name].append(a_.elapsed_time(b_) / GROUP)
     for name, (fn, work, bound, per_step) in kernels.items():
+        if name in block_seq:
+            continue
         for _ in range(3):
             cp.check(fn(), name)
         k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -208,7 +260,10 @@ def main():
             fn()
         k1.record(st)
         torch.cuda.synchronize()
-        k_ms = k0.elapsed_time(k1) / args.kernel_reps
+        times[name] = [k0.elapsed_time(k1) / args.kernel_reps]
+    kstats = {}
+    for name, (fn, work, bound, per_step) in kernels.items():
+        k_ms = sum(times[name]) / len(times[name])
         if bound == "mfma":
             kstats[name] = {"bound": "mfma", "avg_launch_ms": round(k_ms, 4), "tflops": round(work / (k_ms / 1e3) / 1e12, 1),
                             "frac_mfma_peak": round(work / (k_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
