@@ -462,14 +462,21 @@ int gemm_device_cus() {
 }
 
 // Work plan for BM x BN tiles, one workgroup per CU (every tile shape takes 96-136 KB of LDS).
-// Cost model, in microseconds: a tile costs BM*BN*K MACs at a per-CU rate `tile_rate`; whole
-// rounds of tiles run as is; the last partial round either runs as is or, with a partials
-// workspace, is split along K so its units fill one round (1/split of a tile) plus the split-K
-// reduction, priced at its fp32 partial traffic (written once, read once) over HBM.
+// Cost model, in microseconds: a tile costs BM*BN*K MACs at a per-CU rate `tile_rate` measured
+// with every CU busy; whole rounds of tiles run as is; the last partial round either runs as is
+// or, with a partials workspace, is split along K so its units fill one round (1/split of a tile)
+// plus the split-K reduction, priced at its fp32 partial traffic (written once, read once; the
+// partials mostly stay in L2 / MALL). The chip is power-limited: with a fraction f of the CUs
+// busy the clock rises until it caps, so a round with f below kRoundFloor takes kRoundFloor of
+// a full round's time, not f of it (measured: 128 tiles of 288x256x4096 on 256 CUs run at 2.6x
+// the per-CU rate of a full round).
 struct GemmPlan { int full, split, tail; double cost_us; };
 
-constexpr double kHbmBytesPerUs = 4.0e6;     // sustained fp32 partial traffic, bytes per us
+constexpr double kPartialBytesPerUs = 16.0e6;
 constexpr double kReduceLaunchUs = 4.0;
+constexpr double kRoundFloor = 0.65;
+
+static double round_fraction(int units, int cus) { return std::max((double)units / cus, kRoundFloor); }
 
 template <int BM, int BN>
 static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_cu, int split_mode) {
@@ -477,14 +484,14 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
   const int tiles = ((rows + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   const int KT = p.K / kBK;
   const double tile_us = (double)BM * BN * p.K / macs_per_us_per_cu;
-  const int rounds = (tiles + cus - 1) / cus;
-  GemmPlan g{tiles, 1, 0, rounds * tile_us};
   const int tail = tiles % cus;
+  GemmPlan g{tiles, 1, 0, (tiles / cus) * tile_us + (tail ? round_fraction(tail, cus) * tile_us : 0.0)};
   if (tail == 0 || !p.part || split_mode < 0) return g;
   const int split = std::min(std::min(8, KT), cus / tail);
   if (split < 2 || (int64_t)tail * split * BM * BN > p.part_elems) return g;
   const double part_bytes = 2.0 * tail * split * BM * BN * sizeof(float);
-  const double cost = (tiles / cus) * tile_us + tile_us / split + part_bytes / kHbmBytesPerUs + kReduceLaunchUs;
+  const double cost = (tiles / cus) * tile_us + round_fraction(tail * split, cus) * tile_us / split +
+                      part_bytes / kPartialBytesPerUs + kReduceLaunchUs;
   if (cost >= g.cost_us && split_mode == 0) return g;
   g.full = tiles - tail;
   g.tail = tail;
