@@ -9,6 +9,10 @@ namespace qvl {
 // ---------------------------------------------------------------------------------------------
 // LayerNorm (model.py:375-388): one wave per row, row held in registers (CH 16-byte chunks per
 // lane), exact two-pass mean / biased variance in fp32, rsqrt(var + eps), affine, bf16 out.
+// Each wave walks rows row0, row0 + stride, ... (a grid of ~4 workgroups per CU) with gamma /
+// beta held in registers and the next row's loads issued before the current row's reductions:
+// 12.7 us for 18432 x 1024 against 15.1 us for one short-lived wave per row (a plain copy of
+// the same bytes takes 11.5 us).
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -23,57 +27,83 @@ __global__ __launch_bounds__(256) void layernorm_bf16_kernel(const bf16* __restr
                                                              bf16* __restrict__ y, int64_t ldy, int rows,
                                                              int cols, float eps) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int stride = gridDim.x * 4;
   const int nch = cols >> 3;
-  const bf16* xr = x + (int64_t)row * ldx;
-  float v[CH][8];
-  float s = 0.f;
+  // gamma / beta: held in registers for rows up to 2048 features, re-read (L1 / L2 hits) above.
+  constexpr bool kHold = CH <= 4;
+  f32x4 g[kHold ? CH : 1][2], b[kHold ? CH : 1][2];
+  if constexpr (kHold) {
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(xr + c * 8);
-      v[i][0] = bf16_lo(w.x); v[i][1] = bf16_hi(w.x); v[i][2] = bf16_lo(w.y); v[i][3] = bf16_hi(w.y);
-      v[i][4] = bf16_lo(w.z); v[i][5] = bf16_hi(w.z); v[i][6] = bf16_lo(w.w); v[i][7] = bf16_hi(w.w);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+    for (int i = 0; i < CH; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+        g[i][0] = *reinterpret_cast<const f32x4*>(gamma + c * 8);
+        g[i][1] = *reinterpret_cast<const f32x4*>(gamma + c * 8 + 4);
+        b[i][0] = *reinterpret_cast<const f32x4*>(beta + c * 8);
+        b[i][1] = *reinterpret_cast<const f32x4*>(beta + c * 8 + 4);
+      }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += v[i][e];
   }
   const float inv_n = 1.0f / (float)cols;
-  const float mean = wave_sum(s) * inv_n;
-  float q = 0.f;
+  auto load_row = [&](int r, u32x4* dst) {
+    const bf16* xr = x + (int64_t)r * ldx;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
+    for (int i = 0; i < CH; ++i) {
+      const int c = lane + 64 * i;
+      dst[i] = (c < nch) ? *reinterpret_cast<const u32x4*>(xr + c * 8) : u32x4{0u, 0u, 0u, 0u};
     }
-  }
-  const float var = wave_sum(q) * inv_n;
-  const float rstd = rsqrtf(var + eps);
-  bf16* yr = y + (int64_t)row * ldy;
+  };
+  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  u32x4 nxt[CH];
+  if (row < rows) load_row(row, nxt);
+  for (; row < rows; row += stride) {
+    float v[CH][8];
+    float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + c * 8);
-      const f32x4 g1 = *reinterpret_cast<const f32x4*>(gamma + c * 8 + 4);
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + c * 8);
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(beta + c * 8 + 4);
-      float o[8];
+    for (int i = 0; i < CH; ++i) {
+      const u32x4 w = nxt[i];
+      v[i][0] = bf16_lo(w.x); v[i][1] = bf16_hi(w.x); v[i][2] = bf16_lo(w.y); v[i][3] = bf16_hi(w.y);
+      v[i][4] = bf16_lo(w.z); v[i][5] = bf16_hi(w.z); v[i][6] = bf16_lo(w.w); v[i][7] = bf16_hi(w.w);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = (v[i][e] - mean) * rstd * g0[e] + b0[e];
-        o[4 + e] = (v[i][4 + e] - mean) * rstd * g1[e] + b1[e];
+      for (int e = 0; e < 8; ++e) s += v[i][e];      // chunks past the row end hold zeros
+    }
+    if (row + stride < rows) load_row(row + stride, nxt);
+    const float mean = wave_sum(s) * inv_n;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
       }
-      u32x4 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
-                 pack_bf16x2(o[6], o[7])};
-      *reinterpret_cast<u32x4*>(yr + c * 8) = w;
+    }
+    const float var = wave_sum(q) * inv_n;
+    const float rstd = rsqrtf(var + eps);
+    bf16* yr = y + (int64_t)row * ldy;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+        f32x4 g0, g1, b0, b1;
+        if constexpr (kHold) {
+          g0 = g[i][0]; g1 = g[i][1]; b0 = b[i][0]; b1 = b[i][1];
+        } else {
+          g0 = *reinterpret_cast<const f32x4*>(gamma + c * 8);
+          g1 = *reinterpret_cast<const f32x4*>(gamma + c * 8 + 4);
+          b0 = *reinterpret_cast<const f32x4*>(beta + c * 8);
+          b1 = *reinterpret_cast<const f32x4*>(beta + c * 8 + 4);
+        }
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = (v[i][e] - mean) * rstd * g0[e] + b0[e];
+          o[4 + e] = (v[i][4 + e] - mean) * rstd * g1[e] + b1[e];
+        }
+        u32x4 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                   pack_bf16x2(o[6], o[7])};
+        *reinterpret_cast<u32x4*>(yr + c * 8) = w;
+      }
     }
   }
 }
@@ -81,8 +111,9 @@ __global__ __launch_bounds__(256) void layernorm_bf16_kernel(const bf16* __restr
 template <int CH>
 static int launch_ln(const bf16* x, int64_t ldx, const float* g, const float* b, bf16* y, int64_t ldy,
                      int rows, int cols, float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(layernorm_bf16_kernel<CH>, dim3((rows + 3) / 4), dim3(256), 0, stream, x, ldx, g, b, y,
-                     ldy, rows, cols, eps);
+  const int grid = std::min((rows + 3) / 4, 4 * gemm_device_cus());
+  hipLaunchKernelGGL(layernorm_bf16_kernel<CH>, dim3(grid), dim3(256), 0, stream, x, ldx, g, b, y, ldy, rows, cols,
+                     eps);
   return check_launch("layernorm_bf16");
 }
 
