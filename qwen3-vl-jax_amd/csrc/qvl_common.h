@@ -50,12 +50,12 @@ __device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; 
 
 __device__ __forceinline__ float gelu_tanh(float x) {
   // jax.nn.gelu(approximate=True): 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3).
-  // Identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)); exp via the hardware exp2 on -2u*log2(e).
-  // Saturates correctly: exp2 -> inf gives 0, exp2 -> 0 gives x.
-  const float k0 = 0.7978845608028654f;   // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  float u = k0 * (x + k1 * x * x * x);
-  float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);   // exp(-2u)
+  // Identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), and -2u log2(e) = x (c0 + c1 x^2) with
+  // c0 = -2 log2(e) sqrt(2/pi), c1 = 0.044715 c0; exp via the hardware exp2. Saturates
+  // correctly: exp2 -> inf gives (-)0, exp2 -> 0 gives x.
+  const float c0 = -2.3022082f;                 // -2 * log2(e) * sqrt(2/pi)
+  const float c1 = -0.10294324f;                // 0.044715 * c0
+  const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(c1, x * x, c0));
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 

@@ -73,19 +73,29 @@ __device__ __forceinline__ void epi_store_quad(const GemmParams& p, int m, int n
   *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldc + n) = o;
 }
 
+// Rounds a and b to bf16 (kept as floats) with one packed conversion.
+__device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = bf16_lo(w);
+  b = bf16_hi(w);
+}
+
 // Same on 8 consecutive features n..n+7 whose products arrive already rounded to bf16 (packed
-// pairs, from the LDS-staged tile): 16-byte loads/stores when the rows are 16-byte aligned.
+// pairs, from the LDS-staged tile), with the bias of those features preloaded (b0 | b1, zeros
+// past N): 16-byte loads/stores when the rows are 16-byte aligned. The products are exact bf16
+// values, so only the sum with the bias is rounded (pairwise, one conversion per two values).
 template <int EPI>
-__device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n, u32x4 raw, bool vec16) {
-  const f32x4 b0 = *reinterpret_cast<const f32x4*>(p.bias + n);
-  const bool full = n + 8 <= p.N;
-  const f32x4 b1 = full ? *reinterpret_cast<const f32x4*>(p.bias + n + 4) : f32x4{};
-  float v[8] = {bf16_lo(raw.x), bf16_hi(raw.x), bf16_lo(raw.y), bf16_hi(raw.y),
-                bf16_lo(raw.z), bf16_hi(raw.z), bf16_lo(raw.w), bf16_hi(raw.w)};
+__device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n, u32x4 raw, const f32x4& b0,
+                                              const f32x4& b1, bool full, bool vec16) {
+  float v[8] = {bf16_lo(raw.x) + b0[0], bf16_hi(raw.x) + b0[1], bf16_lo(raw.y) + b0[2], bf16_hi(raw.y) + b0[3],
+                bf16_lo(raw.z) + b1[0], bf16_hi(raw.z) + b1[1], bf16_lo(raw.w) + b1[2], bf16_hi(raw.w) + b1[3]};
+  if constexpr (EPI != kEpiBias) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    v[e] = epi_value<EPI>(v[e], b0[e]);
-    v[e + 4] = epi_value<EPI>(v[e + 4], b1[e]);
+    for (int e = 0; e < 8; e += 2) round_bf16_pair(v[e], v[e + 1]);
+  }
+  if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]);
   }
   bf16* dst = p.y + (int64_t)m * p.ldc + n;
   if (vec16 && full) {
@@ -165,15 +175,22 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
       }
   __syncthreads();
   const bool vec16 = ((p.ldc | (EPI == kEpiBiasResidual ? p.ldr : 0)) & 7) == 0;
-  constexpr int ITERS = BM * CH / S::THREADS;
-  static_assert(BM * CH % S::THREADS == 0, "epilogue walk");
+  // A thread keeps one 8-feature column group for the whole walk (THREADS is a multiple of the
+  // groups per row), so its bias is loaded once.
+  static_assert(S::THREADS % CH == 0 && BM % (S::THREADS / CH) == 0, "epilogue walk");
+  constexpr int RSTEP = S::THREADS / CH;
+  const int c = tid % CH, n = n0 + c * 8;
+  if (n >= p.N) return;
+  const bool full = n + 8 <= p.N;
+  const f32x4 b0 = *reinterpret_cast<const f32x4*>(p.bias + n);
+  const f32x4 b1 = full ? *reinterpret_cast<const f32x4*>(p.bias + n + 4) : f32x4{};
 #pragma unroll 4
-  for (int i = 0; i < ITERS; ++i) {
-    const int q = i * S::THREADS + tid;
-    const int r = q / CH, c = q % CH;
+  for (int i = 0; i < BM / RSTEP; ++i) {
+    const int r = i * RSTEP + tid / CH;
+    const int m = m0 + r;
+    if (m >= p.M) break;               // rows only grow with i
     const u32x4 raw = *reinterpret_cast<const u32x4*>(smem + r * BN + ((c ^ (r % CH)) << 3));
-    const int m = m0 + r, n = n0 + c * 8;
-    if (m < p.M && n < p.N) epi_store_oct<EPI>(p, m, n, raw, vec16);
+    epi_store_oct<EPI>(p, m, n, raw, b0, b1, full, vec16);
   }
 }
 
