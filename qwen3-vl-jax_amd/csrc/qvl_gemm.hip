@@ -122,8 +122,9 @@ __device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n,
   }
 }
 
-__device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int n, int d, const float (&lo_acc)[4],
-                                            const float (&hi_acc)[4], float (&o1)[4], float (&o2)[4]);
+__device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int d, const f32x4& blo,
+                                            const f32x4& bhi, const float (&lo_acc)[4], const float (&hi_acc)[4],
+                                            u32x2& o1, u32x2& o2);
 
 // Rotary epilogue of the qkv GEMM for one pair of quads (the split-K reduction's path): features
 // n..n+3 (dims d..d+3 < 32 of a head) and n+32..n+35 of token m, stored straight to q/k
@@ -133,20 +134,23 @@ __device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n,
   if (m >= p.Np || n >= p.N) return;
   const int which = n / p.D;                 // 0 = q, 1 = k, 2 = v
   const int head = (n % p.D) / 64, d = n % 64;
-  float o1[4], o2[4];
-  rope_values(p, which, m, n, d, lo_acc, hi_acc, o1, o2);
+  const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
+  const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
+  u32x2 o1, o2;
+  rope_values(p, which, m, d, blo, bhi, lo_acc, hi_acc, o1, o2);
   if (which == 2) {
     bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
+    const uint32_t w[4] = {o1.x, o1.y, o2.x, o2.y};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vt[(int64_t)(d + e) * p.Np] = (bf16)o1[e];
-      vt[(int64_t)(d + e + 32) * p.Np] = (bf16)o2[e];
+      vt[(int64_t)(d + e) * p.Np] = __builtin_bit_cast(bf16, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+      vt[(int64_t)(d + e + 32) * p.Np] = __builtin_bit_cast(bf16, (uint16_t)(w[2 + (e >> 1)] >> (16 * (e & 1))));
     }
     return;
   }
   bf16* dst = (which == 0 ? p.q : p.k) + ((int64_t)head * p.Np + m) * 64;
-  *reinterpret_cast<u32x2*>(dst + d) = u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
-  *reinterpret_cast<u32x2*>(dst + d + 32) = u32x2{pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3])};
+  *reinterpret_cast<u32x2*>(dst + d) = o1;
+  *reinterpret_cast<u32x2*>(dst + d + 32) = o2;
 }
 
 // LDS-staged epilogue: each wave writes bf16(acc) of its sub-tile into the (free) LDS as a
@@ -194,42 +198,57 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
   }
 }
 
-// Rotary qkv values of 4 consecutive dims d..d+3 (< 32) and d+32..d+35 of one head, for token m:
-// bias, the reference's bf16 cast points, rotary (q, k) and the softmax pre-scale (q). Tokens
-// at or past M give zeros (the attention kernel's padding). All operands are vector loads:
-// bias[n..n+3], bias[n+32..n+35] and the token's (cos, sin)[d..d+3].
-__device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int n, int d, const float (&lo_acc)[4],
-                                            const float (&hi_acc)[4], float (&o1)[4], float (&o2)[4]) {
-  const bool live = m < p.M;
-  if (!live) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { o1[e] = 0.f; o2[e] = 0.f; }
+// Rotary qkv values of 4 consecutive dims d..d+3 (< 32) and d+32..d+35 of one head, for token m,
+// as packed bf16 pairs: bias (blo = bias[n..n+3], bhi = bias[n+32..n+35]), the reference's bf16
+// cast points, rotary (q, k) and the softmax pre-scale (q). Tokens at or past M give zeros (the
+// attention kernel's padding). Every rounding is the reference's; pairs of them share one
+// packed conversion.
+__device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int d, const f32x4& blo,
+                                            const f32x4& bhi, const float (&lo_acc)[4], const float (&hi_acc)[4],
+                                            u32x2& o1, u32x2& o2) {
+  if (m >= p.M) {
+    o1 = u32x2{0u, 0u};
+    o2 = u32x2{0u, 0u};
     return;
   }
-  const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
-  const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
-  float lo[4], hi[4];
+  float lo[4] = {lo_acc[0], lo_acc[1], lo_acc[2], lo_acc[3]};
+  float hi[4] = {hi_acc[0], hi_acc[1], hi_acc[2], hi_acc[3]};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    lo[e] = epi_value<kEpiBias>(lo_acc[e], blo[e]);
-    hi[e] = epi_value<kEpiBias>(hi_acc[e], bhi[e]);
-  }
+  for (int e = 0; e < 4; e += 2) { round_bf16_pair(lo[e], lo[e + 1]); round_bf16_pair(hi[e], hi[e + 1]); }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { lo[e] += blo[e]; hi[e] += bhi[e]; }
   if (which == 2) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { o1[e] = lo[e]; o2[e] = hi[e]; }
+    o1 = u32x2{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3])};
+    o2 = u32x2{pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3])};
     return;
   }
+#pragma unroll
+  for (int e = 0; e < 4; e += 2) { round_bf16_pair(lo[e], lo[e + 1]); round_bf16_pair(hi[e], hi[e + 1]); }
   const f32x4* csr = reinterpret_cast<const f32x4*>(p.cs + (int64_t)m * 32 + d);
   const f32x4 c01 = csr[0], c23 = csr[1];       // (cos, sin) of dims d, d+1 | d+2, d+3
   const float cs_c[4] = {c01[0], c01[2], c23[0], c23[2]};
   const float cs_s[4] = {c01[1], c01[3], c23[1], c23[3]};
-  const float sc = which == 0 ? p.qscale : 1.0f;
+  // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582):
+  // dims < 32: lo*cos - hi*sin; dims + 32: hi*cos + lo*sin.
+  float lc[4], hs[4], hc[4], ls[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582)
-    o1[e] = round_bf16(round_bf16(round_bf16(lo[e] * cs_c[e]) - round_bf16(hi[e] * cs_s[e])) * sc);   // dims < 32
-    o2[e] = round_bf16(round_bf16(round_bf16(hi[e] * cs_c[e]) + round_bf16(lo[e] * cs_s[e])) * sc);   // dims + 32
+  for (int e = 0; e < 4; ++e) { lc[e] = lo[e] * cs_c[e]; hs[e] = hi[e] * cs_s[e]; hc[e] = hi[e] * cs_c[e]; ls[e] = lo[e] * cs_s[e]; }
+#pragma unroll
+  for (int e = 0; e < 4; e += 2) {
+    round_bf16_pair(lc[e], lc[e + 1]); round_bf16_pair(hs[e], hs[e + 1]);
+    round_bf16_pair(hc[e], hc[e + 1]); round_bf16_pair(ls[e], ls[e + 1]);
   }
+  float r1[4], r2[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { r1[e] = lc[e] - hs[e]; r2[e] = hc[e] + ls[e]; }
+  if (which == 0) {                             // q: round the sum, then the pre-scale
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) { round_bf16_pair(r1[e], r1[e + 1]); round_bf16_pair(r2[e], r2[e + 1]); }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { r1[e] *= p.qscale; r2[e] *= p.qscale; }
+  }
+  o1 = u32x2{pack_bf16x2(r1[0], r1[1]), pack_bf16x2(r1[2], r1[3])};
+  o2 = u32x2{pack_bf16x2(r2[0], r2[1]), pack_bf16x2(r2[2], r2[3])};
 }
 
 // LDS-staged rotary epilogue of the qkv GEMM. A wave's TN features are whole heads of one of q,
@@ -255,21 +274,24 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
   const int head0 = (nw % p.D) / 64;
   const int base = m0 + wm * TM;                 // first token of the wave's block
 #pragma unroll
-  for (int b = 0; b < S::MB; ++b)
+  for (int h2 = 0; h2 < HPW; ++h2)
 #pragma unroll
-    for (int h2 = 0; h2 < HPW; ++h2)
+    for (int g = 0; g < 4; ++g) {
+      const int d = 8 * g + 4 * hh, n = nw + h2 * 64 + d;
+      const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);      // once per (head, dims)
+      const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int t = b * 32 + l32, d = 8 * g + 4 * hh;
-        float lo[4], hi[4], o1[4], o2[4];
+      for (int b = 0; b < S::MB; ++b) {
+        const int t = b * 32 + l32;
+        float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
-        rope_values(p, which, base + t, nw + h2 * 64 + d, d, lo, hi, o1, o2);
-        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + g) + 4 * hh) =
-            u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
-        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + 4 + g) + 4 * hh) =
-            u32x2{pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3])};
+        u32x2 o1, o2;
+        rope_values(p, which, base + t, d, blo, bhi, lo, hi, o1, o2);
+        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + g) + 4 * hh) = o1;
+        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + 4 + g) + 4 * hh) = o2;
       }
+    }
   // (a wave reads back only its own region; its LDS operations complete in order)
   if (which < 2) {
     bf16* dst = which == 0 ? p.q : p.k;
