@@ -566,13 +566,16 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 //   288x256 on 12 waves (three per SIMD, 96x64 each): 64 row tiles cover 18432 tokens, so the
 //     N = 1024 / 3072 / 4096 GEMMs fill exactly 1 / 3 / 4 rounds of 256 CUs;
 //   256x256 on 8 waves (two per SIMD, 64x128 each): the least LDS traffic per MFMA;
-//   256x128 on 8 waves (64x64 each): half the work per tile, for balancing small grids.
-constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.36e6;   // MACs/us/CU
+//   256x128 on 8 waves (64x64 each): half the work per tile, for balancing small grids;
+//   288x128 on 12 waves (96x32 each): fills the CUs where 288x256 tiles would cover only half
+//     of them (the merger's 4608 x 2048 output is exactly 256 such tiles).
+constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.36e6,
+                 kRate288x128 = 1.36e6;   // MACs/us/CU
 
-// Test hook: QVL_GEMM_PLAN = "<tile>[:split|:nosplit]" with tile 288x256 | 256x256 | 256x128
-// pins the tile shape (and forces or forbids the tail split) so every variant can be checked
-// against the others; unset, the cost model decides.
-struct ForcedPlan { int tile = 0, split_mode = 0; };   // tile: 0 auto, 1/2/3 as listed
+// Test hook: QVL_GEMM_PLAN = "<tile>[:split|:nosplit]" with tile 288x256 | 256x256 | 256x128 |
+// 288x128 pins the tile shape (and forces or forbids the tail split) so every variant can be
+// checked against the others; unset, the cost model decides.
+struct ForcedPlan { int tile = 0, split_mode = 0; };   // tile: 0 auto, 1/2/3/4 as listed
 
 static ForcedPlan forced_plan() {
   ForcedPlan f;
@@ -581,6 +584,7 @@ static ForcedPlan forced_plan() {
   if (!strncmp(e, "288x256", 7)) f.tile = 1;
   else if (!strncmp(e, "256x256", 7)) f.tile = 2;
   else if (!strncmp(e, "256x128", 7)) f.tile = 3;
+  else if (!strncmp(e, "288x128", 7)) f.tile = 4;
   if (strstr(e, ":nosplit")) f.split_mode = -1;
   else if (strstr(e, ":split")) f.split_mode = 1;
   return f;
@@ -593,17 +597,23 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const GemmPlan a = plan_gemm<288, 256>(p, cus, kRate288x256, f.split_mode);
   const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
+  const GemmPlan d = plan_gemm<288, 128>(p, cus, kRate288x128, f.split_mode);
   int pick = f.tile;
-  if (EPI == kEpiQkvRope && pick == 3) pick = 2;     // 64-feature heads need TN % 64 == 0
+  if (EPI == kEpiQkvRope && pick >= 3) pick = 2;     // 64-feature heads need TN % 64 == 0
   if (pick == 0) {
-    pick = (a.cost_us <= b.cost_us && a.cost_us <= c.cost_us) ? 1 : (EPI == kEpiQkvRope || b.cost_us <= c.cost_us) ? 2 : 3;
+    const double cost[4] = {a.cost_us, b.cost_us, EPI == kEpiQkvRope ? 1e30 : c.cost_us,
+                            EPI == kEpiQkvRope ? 1e30 : d.cost_us};
+    pick = 1;
+    for (int i = 1; i < 4; ++i)
+      if (cost[i] < cost[pick - 1]) pick = i + 1;
   }
   if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI>(p, a, stream);
   if constexpr (EPI == kEpiQkvRope) {
     return launch_gemm<256, 256, 4, 2, EPI>(p, b, stream);
   } else {
     if (pick == 2) return launch_gemm<256, 256, 4, 2, EPI>(p, b, stream);
-    return launch_gemm<256, 128, 4, 2, EPI>(p, c, stream);
+    if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI>(p, c, stream);
+    return launch_gemm<288, 128, 3, 4, EPI>(p, d, stream);
   }
 }
 

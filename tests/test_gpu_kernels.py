@@ -229,7 +229,8 @@ def test_attention_hd72_ragged(pkg, lib, grids):
         assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (i, s, e)
 
 
-PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x256:split", "256x256:split", "256x128:split"]
+PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x128:nosplit", "288x256:split", "256x256:split",
+         "256x128:split", "288x128:split"]
 
 
 def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
@@ -244,7 +245,7 @@ def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
 @pytest.mark.parametrize("m,n,k", [(18432, 1024, 1024), (4600, 2048, 4096), (2304, 4096, 1024), (300, 192, 128),
                                    (18000, 1152, 4352)])
 def test_dense_tile_plans_agree(pkg, lib, monkeypatch, epi, m, n, k):
-    """Every tile shape (288x256 / 256x256 / 256x128) gives bit-identical results without the
+    """Every tile shape (288x256 / 256x256 / 256x128 / 288x128) gives bit-identical results without the
     tail split (same K order per output); with the split (fp32 partials summed by the reduce
     kernel) within rel-L2 2e-3 of them; all within rel-L2 4e-3 of torch fp32 on the same bf16
     operands. Shapes include M not a multiple of any tile height and N not a multiple of 256."""
