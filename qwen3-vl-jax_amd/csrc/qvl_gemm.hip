@@ -323,6 +323,19 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
   }
 }
 
+// Tile t -> (row tile, column tile). Tiles are ordered in panels of group_n column tiles, row tile
+// by row tile within a panel, so the tiles that one XCD runs in one round (a contiguous range, see
+// xcd_remap) form a block of about (cus/8)/group_n row tiles by group_n column tiles, and the
+// operand bytes that XCD's L2 fetches per round are ~rows*|x tile| + cols*|w tile| instead of the
+// whole weight matrix (row-major order puts all column tiles of 2 row tiles in one round).
+__device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, int group_n, int& tm, int& tn) {
+  const int panel = tile / (tiles_m * group_n);
+  const int width = min(group_n, tiles_n - panel * group_n);
+  const int r = tile - panel * tiles_m * group_n;
+  tm = r / width;
+  tn = panel * group_n + r % width;
+}
+
 template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
   using S = GemmShape<BM, BN, WM, WN>;
@@ -342,7 +355,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
     kt0 = s * KT / p.split;
     kt1 = (s + 1) * KT / p.split;
   }
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  int tm, tn;
+  tile_coords(tile, (max(p.M, p.Np) + BM - 1) / BM, tiles_n, p.group_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int tid = threadIdx.x;
@@ -471,7 +485,9 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
   const int nn = (EPI == kEpiQkvRope) ? (q / 8) * 64 + (q % 8) * 4 : q * 4;
   const int tiles_n = (p.N + BN - 1) / BN;
   const int tile = p.full_tiles + t;
-  const int m = (tile / tiles_n) * BM + mm, n = (tile % tiles_n) * BN + nn;
+  int tm, tn;
+  tile_coords(tile, (max(p.M, p.Np) + BM - 1) / BM, tiles_n, p.group_n, tm, tn);
+  const int m = tm * BM + mm, n = tn * BN + nn;
   float lo[4] = {0.f, 0.f, 0.f, 0.f}, hi[4] = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < p.split; ++s) {
     const float* src = p.part + ((size_t)(t * p.split + s) * BM + mm) * BN + nn;
@@ -539,6 +555,14 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
   return g;
 }
 
+// Column tiles per panel of the tile order (QVL_GEMM_GROUP overrides, for the tests and sweeps).
+static int gemm_group_n(int tiles_n) {
+  int g = 4;
+  const char* e = getenv("QVL_GEMM_GROUP");
+  if (e && *e) g = atoi(e);
+  return std::max(1, std::min(g, tiles_n));
+}
+
 template <int BM, int BN, int WM, int WN, int EPI>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
@@ -552,6 +576,7 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   }
   p.full_tiles = g.full;
   p.split = g.split;
+  p.group_n = gemm_group_n((p.N + BN - 1) / BN);
   const int grid = g.full + g.tail * g.split;
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI>), dim3(grid), dim3(S::THREADS), lds, stream, p);
   int rc = check_launch("gemm_bf16");

@@ -25,6 +25,7 @@ struct GemmParams {
   float* part;
   int64_t part_elems;
   int full_tiles, split;
+  int group_n;                   // tile order: panels of group_n column tiles (set by the launcher)
 };
 
 // fp32 GEMM (qvl_f32.hip): w packed [n_rows_w][ldw] fp32 (ldw = k padded to 64), Kp = ldw.
