@@ -51,6 +51,54 @@ __global__ __launch_bounds__(256) void patchify_kernel(const uint8_t* __restrict
   }
 }
 
+// The reference's configuration (patch 16, temporal patch 2, merge 2), with the index arithmetic
+// in shifts: thread (mi, mj, ph, j) of a merge block reads the 4 pixels x CIN channels of one
+// patch row quarter (x = 4j..4j+3) once per temporal slot (once when both slots repeat the same
+// frame) and writes the 3 channel runs of 4 columns; a wave writes 1 KB contiguous per (c, tp).
+template <int CIN, typename OutT>
+__global__ __launch_bounds__(256) void patchify_p16_kernel(const uint8_t* __restrict__ frames, int F, int H, int W,
+                                                           int GH, int GW, OutT* __restrict__ out, int64_t ldo) {
+  constexpr int P = 16, TP = 2, M = 2;
+  __shared__ float lut[256];
+  lut[threadIdx.x] = ((float)threadIdx.x / 255.0f - 0.5f) / 0.5f;
+  __syncthreads();
+  const int64_t g = blockIdx.x;                       // merge block: (t * GH + hb) * GW + wb
+  const int wb = (int)(g % GW);
+  const int64_t tg = g / GW;
+  const int hb = (int)(tg % GH), t = (int)(tg / GH);
+  const int r = threadIdx.x >> 6, ph = (threadIdx.x >> 2) & 15, j = threadIdx.x & 3;
+  const int mi = r >> 1, mj = r & 1;
+  const int y = (hb * M + mi) * P + ph, x = (wb * M + mj) * P + 4 * j;
+  OutT* dst = out + (g * (M * M) + r) * ldo + ph * P + 4 * j;
+  uint8_t px[4 * CIN];
+  int loaded = -1;
+#pragma unroll
+  for (int tp = 0; tp < TP; ++tp) {
+    const int f = min(t * TP + tp, F - 1);
+    if (f != loaded) {
+      const uint8_t* src = frames + (((int64_t)f * H + y) * W + x) * CIN;
+      if constexpr (CIN == 4) {
+        *reinterpret_cast<u32x4*>(px) = *reinterpret_cast<const u32x4*>(src);
+      } else {
+        const uint32_t* s4 = reinterpret_cast<const uint32_t*>(src);
+        uint32_t w3[3] = {s4[0], s4[1], s4[2]};
+        __builtin_memcpy(px, w3, 12);
+      }
+      loaded = f;
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float v0 = lut[px[c]], v1 = lut[px[CIN + c]], v2 = lut[px[2 * CIN + c]], v3 = lut[px[3 * CIN + c]];
+      OutT* d = dst + (c * TP + tp) * P * P;
+      if constexpr (std::is_same<OutT, float>::value) {
+        *reinterpret_cast<f32x4*>(d) = f32x4{v0, v1, v2, v3};
+      } else {
+        *reinterpret_cast<u32x2*>(d) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Vision-token positions (model.py:927-931 / 880-882): for each batch row, the first n_rows
 // token indices s with tokens[s] == match, in increasing order, then -1 fill; count = number of
@@ -195,6 +243,17 @@ int qvl_patchify(void* stream, int32_t dtype, const uint8_t* frames, int64_t n_f
   const int F = (int)n_frames, H = (int)height, W = (int)width, P = patch_size, Tp = temporal_patch_size,
             m = merge_size, GH = (int)(gh / merge_size), GW = (int)(gw / merge_size);
   const dim3 grid((unsigned)blocks);
+  const bool p16 = vec && P == 16 && Tp == 2 && m == 2 && (uintptr_t)frames % 4 == 0;
+  if (p16) {
+    if (dtype == QVL_DTYPE_F32) {
+      if (channels == 3) hipLaunchKernelGGL((patchify_p16_kernel<3, float>), grid, dim3(256), 0, st, frames, F, H, W, GH, GW, (float*)out, ld_out);
+      else hipLaunchKernelGGL((patchify_p16_kernel<4, float>), grid, dim3(256), 0, st, frames, F, H, W, GH, GW, (float*)out, ld_out);
+    } else {
+      if (channels == 3) hipLaunchKernelGGL((patchify_p16_kernel<3, bf16>), grid, dim3(256), 0, st, frames, F, H, W, GH, GW, (bf16*)out, ld_out);
+      else hipLaunchKernelGGL((patchify_p16_kernel<4, bf16>), grid, dim3(256), 0, st, frames, F, H, W, GH, GW, (bf16*)out, ld_out);
+    }
+    return check_launch("patchify");
+  }
   if (dtype == QVL_DTYPE_F32) {
     if (vec) hipLaunchKernelGGL((patchify_kernel<4, float>), grid, dim3(256), 0, st, frames, F, H, W, channels, P, Tp, m, GH, GW, (float*)out, ld_out);
     else hipLaunchKernelGGL((patchify_kernel<1, float>), grid, dim3(256), 0, st, frames, F, H, W, channels, P, Tp, m, GH, GW, (float*)out, ld_out);
