@@ -182,6 +182,94 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(HT* __restrict__ hidd
   }
 }
 
+// Vector loads / stores of N (4 or 8) consecutive elements as floats: bf16 in 8- or 16-byte
+// pieces, fp32 in 16-byte pieces. Stores round to the element type.
+template <int N> __device__ __forceinline__ void ld_vec(const bf16* p, float (&v)[N]) {
+  static_assert(N == 4 || N == 8, "ld_vec");
+  if constexpr (N == 8) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+    v[0] = bf16_lo(w.x); v[1] = bf16_hi(w.x); v[2] = bf16_lo(w.y); v[3] = bf16_hi(w.y);
+    v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
+  } else {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+    v[0] = bf16_lo(w.x); v[1] = bf16_hi(w.x); v[2] = bf16_lo(w.y); v[3] = bf16_hi(w.y);
+  }
+}
+template <int N> __device__ __forceinline__ void ld_vec(const float* p, float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    const f32x4 w = *reinterpret_cast<const f32x4*>(p + i);
+    v[i] = w[0]; v[i + 1] = w[1]; v[i + 2] = w[2]; v[i + 3] = w[3];
+  }
+}
+template <int N> __device__ __forceinline__ void st_vec(bf16* p, const float (&v)[N]) {
+  static_assert(N == 4 || N == 8, "st_vec");
+  if constexpr (N == 8)
+    *reinterpret_cast<u32x4*>(p) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                         pack_bf16x2(v[6], v[7])};
+  else
+    *reinterpret_cast<u32x2*>(p) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+template <int N> __device__ __forceinline__ void st_vec(float* p, const float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) *reinterpret_cast<f32x4*>(p + i) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+}
+template <typename T> __device__ __forceinline__ float round_to(float v) {
+  if constexpr (std::is_same<T, bf16>::value) return round_bf16(v);
+  else return v;
+}
+
+// Same scatter, one wave per row and 16 bytes of hidden per lane step (CH elements: 8 bf16 or 4
+// fp32), for rows of a multiple of 8 elements on 16-byte aligned rows; work item n_rows of each
+// batch row is the trailing "+0" on row 0. Same roundings as scatter_rows_kernel.
+template <int MODE, typename HT, typename RT>
+__global__ __launch_bounds__(256) void scatter_rows_vec_kernel(HT* __restrict__ hidden, int64_t S, int64_t D,
+                                                               const RT* __restrict__ rows, int64_t rows_bstride,
+                                                               int64_t n_rows, const int32_t* __restrict__ pos,
+                                                               const int32_t* __restrict__ count) {
+  constexpr int CH = 16 / sizeof(HT);
+  const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.y;
+  if (j > n_rows) return;
+  const int64_t cnt = count[b];
+  const bool unfilled = cnt < n_rows;
+  HT* hb = hidden + (int64_t)b * S * D;
+  if (j == n_rows) {
+    if (MODE == QVL_SCATTER_ADD && unfilled && pos[(int64_t)b * n_rows] != 0)
+      for (int64_t d = (int64_t)lane * CH; d < D; d += 64 * CH) {
+        float h[CH];
+        ld_vec<CH>(hb + d, h);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) h[e] += 0.0f;
+        st_vec<CH>(hb + d, h);
+      }
+    return;
+  }
+  const int p = pos[(int64_t)b * n_rows + j];
+  if (p < 0) return;
+  if (MODE == QVL_SCATTER_SET && p == 0 && unfilled) return;   // overwritten by the old row 0 afterwards
+  HT* h = hb + (int64_t)p * D;
+  const RT* r = rows + (int64_t)b * rows_bstride + j * D;
+  for (int64_t d = (int64_t)lane * CH; d < D; d += 64 * CH) {
+    float u[CH];
+    ld_vec<CH>(r + d, u);
+#pragma unroll
+    for (int e = 0; e < CH; ++e) u[e] = round_to<HT>(u[e]);        // feat.astype(h.dtype)
+    if (MODE == QVL_SCATTER_ADD) {
+      float hv[CH];
+      ld_vec<CH>(h + d, hv);
+#pragma unroll
+      for (int e = 0; e < CH; ++e) {
+        float v = round_to<HT>(hv[e] + u[e]);                      // h + u in the hidden dtype
+        if (p == 0 && unfilled) v = round_to<HT>(v + 0.0f);
+        u[e] = v;
+      }
+    }
+    st_vec<CH>(h + d, u);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Row gather (model.py:809-812 shuffle / 845-848 unshuffle of the window path): out row r is
 // in row idx[r / group] * group + r % group, cast to the output dtype. VEC elements per step.
@@ -319,10 +407,17 @@ int qvl_scatter_vision_rows(void* stream, int32_t mode, int32_t hidden_dtype, vo
   if (batch > 65535 || n_rows >= 0x7fffffffLL) return set_error(QVL_ERR_UNSUPPORTED, "scatter_vision_rows: sizes");
   if (!hidden || !rows || !pos || !count) return set_error(QVL_ERR_INVALID_ARG, "scatter_vision_rows: NULL pointer");
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)(n_rows + 1), (unsigned)batch);
-#define QVL_SCATTER(M, HT, RT)                                                                               \
-  hipLaunchKernelGGL((scatter_rows_kernel<M, HT, RT>), grid, dim3(256), 0, st, (HT*)hidden, seq_len, dim,      \
-                     (const RT*)rows, rows_batch_stride, n_rows, pos, count)
+  const int64_t rb_bytes = rows_dtype == QVL_DTYPE_BF16 ? 2 : 4;
+  const bool vec = dim % 8 == 0 && (uintptr_t)hidden % 16 == 0 && (uintptr_t)rows % 16 == 0 &&
+                   (rows_batch_stride * rb_bytes) % 16 == 0;
+  const dim3 grid(vec ? (unsigned)((n_rows + 1 + 3) / 4) : (unsigned)(n_rows + 1), (unsigned)batch);
+#define QVL_SCATTER(M, HT, RT)                                                                                 \
+  do {                                                                                                          \
+    if (vec) hipLaunchKernelGGL((scatter_rows_vec_kernel<M, HT, RT>), grid, dim3(256), 0, st, (HT*)hidden,     \
+                                seq_len, dim, (const RT*)rows, rows_batch_stride, n_rows, pos, count);          \
+    else hipLaunchKernelGGL((scatter_rows_kernel<M, HT, RT>), grid, dim3(256), 0, st, (HT*)hidden, seq_len, dim, \
+                            (const RT*)rows, rows_batch_stride, n_rows, pos, count);                            \
+  } while (0)
   const bool hb = hidden_dtype == QVL_DTYPE_BF16, rb = rows_dtype == QVL_DTYPE_BF16;
   if (mode == QVL_SCATTER_SET) {
     if (hb && rb) QVL_SCATTER(QVL_SCATTER_SET, bf16, bf16);

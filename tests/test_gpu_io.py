@@ -101,6 +101,7 @@ def _case(seed, B, S, D, V, pad, n_pad, pad_at0=False):
     (3, 2100, 96, 30, 20, False),      # fewer pads, none at 0: the trailing +0 on row 0
     (2, 500, 64, 10, 50, False),       # more pads than rows
     (1, 100, 32, 8, 0, False),         # no pads
+    (2, 400, 36, 20, 10, True),        # rows not a multiple of 8 elements: the element-wise kernel
 ])
 def test_inject_and_deepstack_bit_exact(pkg, hdt, rdt, B, S, D, V, n_pad, pad_at0):
     io = pkg.decoder_io
