@@ -151,9 +151,19 @@ def main():
     seg = [2304] * 8
     ln_g = torch.ones(D, device=dev)
     ln_b = torch.zeros(D, device=dev)
-    px_b = torch.empty((N, spec.patch_volume), dtype=torch.bfloat16, device=dev)
+    # The two pixel-sized HBM kernels write (and the cast reads) 113-170 MB per launch; launched back
+    # to back on one buffer their data stays in the 256 MB Infinity Cache and the rate reads above
+    # the HBM peak. They rotate over 3 buffers instead (340 MB / 510 MB), as a fresh batch of
+    # frames would find them, so each launch's bytes go to and come from HBM.
+    px_b = [torch.empty((N, spec.patch_volume), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    px_c = [px] + [px.clone() for _ in range(2)]
     frames_u8 = torch.randint(0, 256, (8, 768, 768, 3), dtype=torch.uint8, device=dev)
-    px_p = torch.empty((N, spec.patch_volume), dtype=torch.float32, device=dev)
+    px_p = [torch.empty((N, spec.patch_volume), dtype=torch.float32, device=dev) for _ in range(3)]
+    rot = {"cast": 0, "patchify": 0}
+
+    def rotate(name):
+        rot[name] += 1
+        return rot[name] % 3
     V, Dtxt = N // 4, spec.out_hidden_size
     S_txt = V + 512
     tok_txt = torch.zeros((1, S_txt), dtype=torch.int32, device=dev)
@@ -194,13 +204,13 @@ def main():
                                       tens["tap_w"].data_ptr(), yk.data_ptr(), N, D),
             N * D * 2 + N * 4 * 8 + spec.num_position_embeddings * D * 2, "hbm", 1),
         "cast pixels f32->bf16 (18432x1536)": (
-            lambda: lib.qvl_cast(s_, BF, px.data_ptr(), px_b.data_ptr(), N * spec.patch_volume),
-            N * spec.patch_volume * 6.0, "hbm", 1),
+            lambda: (lambda i: lib.qvl_cast(s_, BF, px_c[i].data_ptr(), px_b[i].data_ptr(), N * spec.patch_volume))(
+                rotate("cast")), N * spec.patch_volume * 6.0, "hbm", 1),
         # the steps either side of the tower (not in the step time): on-device patchify of the 8
         # uint8 frames, and the decoder-side injection / deepstack add of the 4608 vision rows
         "patchify (8 x 768x768x3 uint8 -> 18432x1536 f32)": (
             lambda: lib.qvl_patchify(s_, cp.QVL_DTYPE_F32, frames_u8.data_ptr(), 8, 768, 768, 3, 16, 2, 2,
-                                     px_p.data_ptr(), spec.patch_volume),
+                                     px_p[rotate("patchify")].data_ptr(), spec.patch_volume),
             8 * 768 * 768 * 3 + N * spec.patch_volume * 4.0, "hbm", 0),
         "inject vision rows (4608 x 2048 bf16 into 5120 x 2048)": (
             lambda: lib.qvl_scatter_vision_rows(s_, cp.QVL_SCATTER_SET, BF, hid.data_ptr(), 1, S_txt, Dtxt, BF,
