@@ -195,9 +195,87 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
     __syncthreads();
   };
 
+  // Every tile after the first, one 32-key block at a time: block 0's softmax is independent of
+  // block 1's S MFMAs and block 1's softmax of block 0's PV MFMAs, so each wave has VALU work to
+  // issue beside its own MFMAs. Each block checks its own partial row sum; a raise rescales O and
+  // l, which already hold block 0's PV when block 1 raises (exact), and shifts the blocks not yet
+  // exponentiated by the same amount.
+  auto step_blocks = [&](auto edge_tag, int it) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    const int cur = it & 1;
+    const int kb = k_begin + it * kAttnBN;
+    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
+    const bf16* sK = smem + cur * (2 * kAttnBN * kHD);
+    const bf16* sV = sK + kAttnBN * kHD;
+    f32x16 s[2] = {negm, negm};
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k_off(b * 32 + l32, ks * 2 + hh)]);
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
+      }
+    if constexpr (EDGE) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      uint32_t pk[8];
+      float ts;
+      auto exp_block = [&]() {
+        float ta = 0.f, tb = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j]), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1]);
+          pk[j] = pack_bf16x2(e0, e1);
+          ta += e0;
+          tb += e1;
+        }
+        ts = ta + tb;
+      };
+      exp_block();
+      if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
+        // Some row of this block outgrew the stale max: raise it by the block's max.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+        const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
+#pragma unroll
+        for (int bb = b; bb < 2; ++bb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[bb][r] -= sh;
+        exp_block();
+        const float alpha = __builtin_amdgcn_exp2f(-sh);
+        m_run += sh;
+        l_run *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; negm[r] = -m_run; }
+      }
+      l_run += ts;
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * e2], pk[4 * e2 + 1], pk[4 * e2 + 2], pk[4 * e2 + 3]});
+        const int g = 2 * b + e2;   // 16-key group within the tile
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * g + hh)]);
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
+        }
+      }
+    }
+    wait_dma();
+    __syncthreads();
+  };
+
   step(std::true_type{}, 0);
-  for (int it = 1; it + 1 < n_kt; ++it) step(std::false_type{}, it);
-  if (n_kt > 1) step(std::true_type{}, n_kt - 1);
+  for (int it = 1; it + 1 < n_kt; ++it) step_blocks(std::false_type{}, it);
+  if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l_tot;
