@@ -136,7 +136,10 @@ int layer_norm_bf16(const bf16* x, int64_t ldx, const float* g, const float* b, 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pos-embed bilinear gather (model.py:751-764): one wave per token, 4 table rows weighted.
+// Pos-embed bilinear gather (model.py:751-764): one wave per token, 4 table rows weighted. Taps
+// whose weight is 0 (every tap but one when the grid side equals the table side, e.g. 768-pixel
+// images on the 48 x 48 table) are skipped: their products are exact zeros and leave the sum
+// unchanged, and the wave-uniform test saves their row reads.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void pos_embed_bf16_kernel(const bf16* __restrict__ table,
                                                              const int* __restrict__ idx,
@@ -152,6 +155,7 @@ __global__ __launch_bounds__(256) void pos_embed_bf16_kernel(const bf16* __restr
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      if (tw[j] == 0.f) continue;
       const u32x4 w = *reinterpret_cast<const u32x4*>(table + (int64_t)ti[j] * dim + c * 8);
       acc[0] += tw[j] * bf16_lo(w.x); acc[1] += tw[j] * bf16_hi(w.x);
       acc[2] += tw[j] * bf16_lo(w.y); acc[3] += tw[j] * bf16_hi(w.y);

@@ -106,11 +106,13 @@ def test_layer_norm_vs_oracle(pkg, lib, cols):
     assert np.all(np.abs(got - ref) <= 2 * 2 ** -8 * np.abs(ref) + 1e-6)
 
 
-def test_pos_embed_vs_oracle(pkg, lib):
+@pytest.mark.parametrize("grids", [[(8, 32, 32)], [(2, 48, 48)]])
+def test_pos_embed_vs_oracle(pkg, lib, grids):
     """4-tap gather: fp32 accumulate, one rounding (the reference rounds each tap in bf16):
-    rel-L2 <= 4e-3 vs the oracle's bf16 pos-embed on config 3's video grid (repeat quirk)."""
+    rel-L2 <= 4e-3 vs the oracle's bf16 pos-embed on config 3's video grid (repeat quirk). On a
+    48 x 48 grid (the table's own side) every token has one tap of weight 1 and three of weight 0,
+    which the kernel skips: the output is exactly that table row."""
     cp = pkg.capi
-    grids = [(8, 32, 32)]
     spec = vt.VisionSpec()
     table = np.random.default_rng(0).standard_normal((2304, 1024)).astype(np.float32) * 0.02
     m = pkg.grid_metadata(grids)
@@ -121,6 +123,11 @@ def test_pos_embed_vs_oracle(pkg, lib):
                                out.data_ptr(), m.n_tokens, 1024))
     ref = vt.pos_embed(table, grids, spec, vt._P("bf16"))
     assert rel_l2(to_np(out), ref) <= 4e-3
+    if grids[0][1] == 48:
+        wn = m.tap_w.reshape(4, -1)
+        assert np.all(np.sort(wn, axis=0)[-1] == 1.0) and np.all(np.sort(wn, axis=0)[:-1] == 0.0)
+        row = m.tap_idx.reshape(4, -1)[np.argmax(wn, axis=0), np.arange(m.n_tokens)]
+        np.testing.assert_array_equal(to_np(out), vt.bf16_round(table)[row])
 
 
 def test_rotary_table_vs_oracle(pkg, lib):
