@@ -73,9 +73,12 @@ __device__ __forceinline__ void epi_store_quad(const GemmParams& p, int m, int n
   *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldc + n) = o;
 }
 
-// Rounds a and b to bf16 (kept as floats) with one packed conversion.
+// Rounds a and b to bf16 (kept as floats) with one packed conversion (round to nearest even).
+// Written as the instruction itself: from the C form the compiler splits the pair into two
+// single-value conversions, one per half it extracts.
 __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
-  const uint32_t w = pack_bf16x2(a, b);
+  uint32_t w;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(w) : "v"(a), "v"(b));
   a = bf16_lo(w);
   b = bf16_hi(w);
 }
