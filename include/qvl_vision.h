@@ -162,8 +162,8 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t l
 
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
- * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][80] (dims 72..79 zero) and
- * v^T [H][96][Np] (rows 72..95 zero), keys at the same quad-swapped positions. fp32: q, k
+ * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][88] (dims 72..87 zero) and
+ * v^T [H][72][Np], keys at the same quad-swapped positions. fp32: q, k
  * [H][Np][head_dim], v^T [H][32*ceil(head_dim/32)][Np] (extra rows zero), keys in order. */
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const void* d_k, const void* d_vt,
                             const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,

@@ -18,10 +18,10 @@
 // preloaded with -m (the running row max), the accumulator already holds s - m, and p = exp2(acc)
 // costs one instruction per score. The max is only raised on the first tile, or when a tile's
 // partial row sum exceeds 2^64 (softmax is shift-invariant; each raise rescales O and l exactly).
-// P is rounded to bf16 pairs for the PV MFMA (its B operand, straight from registers) and the row
-// sum is taken over those same bf16 values with v_dot2_f32_bf16, so the normalisation matches
-// the weights the MFMA applied. V^T's quad-swapped key layout makes each lane's 8 PV keys one
-// 16-byte LDS chunk.
+// P is rounded to bf16 pairs for the PV MFMA (its B operand, straight from registers); the row sum
+// adds the fp32 values (the reference normalises by the fp32 sum, model.py:595), with fp32 adds
+// rather than v_dot2_f32_bf16 over the packed pairs, which would share the matrix pipe. V^T's
+// quad-swapped key layout makes each lane's 8 PV keys one 16-byte LDS chunk.
 #include <math.h>
 #include <type_traits>
 #include "qvl_kernels.h"
@@ -37,13 +37,6 @@ constexpr int kHD = 64;
 // rows' worth), and the 16 rows one such read touches land in 16 distinct bank groups.
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * kHD + ((chunk ^ ((row >> 1) & 7)) << 3); }
 __device__ __forceinline__ int v_off(int d, int chunk) { return d * kAttnBN + ((chunk ^ ((d >> 1) & 7)) << 3); }
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float dot2_ones(uint32_t packed, float acc) {
-  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), one, acc, false);
-}
 
 __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
@@ -148,8 +141,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          pk[b][j] = pack_bf16x2(__builtin_amdgcn_exp2f(s[b][2 * j] - sh), __builtin_amdgcn_exp2f(s[b][2 * j + 1] - sh));
-          if (j & 1) ts2 = dot2_ones(pk[b][j], ts2); else ts = dot2_ones(pk[b][j], ts);
+          const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j] - sh), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1] - sh);
+          pk[b][j] = pack_bf16x2(e0, e1);
+          ts += e0;
+          ts2 += e1;
         }
       ts += ts2;
     };
@@ -294,194 +289,226 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// General head_dim (72 for the 8B tower): Q/K [H][Np][HDP] with dims [hd, HDP) zero, V^T
-// [H][32*NDB][Np] with rows [hd, 32*NDB) zero (keys at vt_pos). Same softmax pipeline as the hd-64
-// kernel; K / V^T tiles are staged through registers into LDS rows padded to an odd number of
-// 16-byte chunks (HDP + 8 and 64 + 8 elements), which keeps the 16-row fragment reads on 16
-// distinct bank groups without a swizzle.
+// head_dim 72 (the 8B tower): Q/K [H][Np][88] (dims 72..87 zero; the QK MFMAs use dims 0..79),
+// V^T [H][72][Np] (keys at vt_pos). Same work items, softmax pipeline and block-at-a-time steady
+// state as the hd-64 kernel. K tiles arrive by LDS DMA as contiguous 176-byte rows: 11 16-byte
+// chunks, an odd count, so the 16 rows one fragment read touches fall on 16 distinct bank groups
+// without a swizzle. V^T tiles arrive as 128-byte rows with the hd-64 kernel's XOR swizzle; the
+// third 32-row PV block reads LDS rows 72..95, which the DMA never writes: they only feed output
+// rows 72..95, which are not stored (an MFMA output row depends on its own A row only).
 // ---------------------------------------------------------------------------------------------
-template <int HDP, int NDB>
-__global__ __launch_bounds__(256, 2) void attn_fwd_general_kernel(
-    const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
-    const int* __restrict__ tiles, int Np, int H, int hd, bf16* __restrict__ O, int64_t ldo) {
-  constexpr int KS = HDP / 16;                 // QK k-steps
-  constexpr int KLD = HDP + 8;                 // LDS row stride of the K tile (elements)
-  constexpr int VLD = kAttnBN + 8;             // LDS row stride of the V^T tile
-  constexpr int VROWS = 32 * NDB;
-  constexpr int KCH = kAttnBN * HDP / 8;       // 16-byte chunks per K tile
-  constexpr int VCH = VROWS * kAttnBN / 8;     // 16-byte chunks per V^T tile
-  constexpr int KPT = (KCH + 255) / 256, VPT = (VCH + 255) / 256;
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][kAttnBN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][VROWS * VLD];
+constexpr int kHD72 = 72;
+constexpr int kQK72 = 88;                  // Q/K row length (elements)
+constexpr int kKS72 = 5;                   // QK k-steps (dims 0..79)
+constexpr int kVR72 = 72;                  // V^T rows written by the DMA
+constexpr int kNDB72 = 3;                  // 32-row PV blocks (rows 0..95)
+constexpr int kKTile72 = kAttnBN * kQK72;  // K tile elements (11 KB)
+constexpr int kVTile72 = 96 * kAttnBN;     // V^T tile elements (12 KB)
 
-  // Work item: (segment start, segment end, first query, head); empty items pad short queues.
+__device__ __forceinline__ int k72_off(int row, int chunk) { return row * kQK72 + (chunk << 3); }
+
+__global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
+    const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
+    const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (kKTile72 + kVTile72)];   // [stage][K 64x88 | V^T 96x64]
+
   const int item = blockIdx.x;
   const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2], head = tiles[4 * item + 3];
   if (seg_e <= seg_s) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const size_t qk_head = (size_t)Np * HDP, v_head = (size_t)VROWS * Np;
+
+  const size_t qk_head = (size_t)Np * kQK72, v_head = (size_t)kVR72 * Np;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + head * qk_head, (uint32_t)(qk_head * 2));
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + head * qk_head, (uint32_t)(qk_head * 2));
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vt + head * v_head, (uint32_t)(v_head * 2));
-
   const int qrow = q0 + wave * 32 + l32;
-  bf16x8 qf[KS];
+  bf16x8 qf[kKS72];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * HDP + ks * 16 + hh * 8) * 2)));
+  for (int ks = 0; ks < kKS72; ++ks)
+    qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * kQK72 + ks * 16 + hh * 8) * 2)));
 
-  u32x4 stk[KPT], stv[VPT];
-  auto load_tile = [&](int kb) {
+  // Tile DMA, 20 instructions of 1 KB, 5 per wave: K instructions 0..10 copy the tile's 11264
+  // contiguous bytes (lane j -> byte 16j of the kilobyte); V^T instructions 0..8 fill rows
+  // [8i, 8i+8), lane j in row 8i + j/8 at physical chunk j%8, fetching the logical chunk the read
+  // swizzle maps there ((row/2)%8 alternates with the parity of i).
+  const u32x4 rk = rsrc_words(K + head * qk_head, (uint32_t)(qk_head * 2));
+  const u32x4 rv = rsrc_words(Vt + head * v_head, (uint32_t)(v_head * 2));
+  const uint32_t k_lane = (uint32_t)(lane * 16);
+  const int vr = lane >> 3;
+  const uint32_t v_lane[2] = {(uint32_t)(((int64_t)vr * Np + (((lane & 7) ^ ((vr >> 1) & 7)) << 3)) * 2),
+                              (uint32_t)(((int64_t)vr * Np + (((lane & 7) ^ (((vr >> 1) + 4) & 7)) << 3)) * 2)};
+  const uint32_t lds0 = lds_addr_of(smem);
+  constexpr uint32_t kStageBytes = (kKTile72 + kVTile72) * 2;
+  auto dma_tile = [&](int kb, int stage) {
+    const uint32_t kl = lds0 + stage * kStageBytes, vl = kl + kKTile72 * 2;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int c = i * 256 + tid;
-      const int row = c / (HDP / 8), ch = c % (HDP / 8);
-      if (c < KCH) stk[i] = buf_load16(rk, (uint32_t)(((int64_t)(kb + row) * HDP + ch * 8) * 2));
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int c = i * 256 + tid;
-      const int row = c >> 3, ch = c & 7;
-      if (c < VCH) stv[i] = buf_load16(rv, (uint32_t)(((int64_t)row * Np + kb + ch * 8) * 2));
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int c = i * 256 + tid;
-      const int row = c / (HDP / 8), ch = c % (HDP / 8);
-      if (c < KCH) *reinterpret_cast<u32x4*>(&sK[buf][row * KLD + ch * 8]) = stk[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int c = i * 256 + tid;
-      const int row = c >> 3, ch = c & 7;
-      if (c < VCH) *reinterpret_cast<u32x4*>(&sV[buf][row * VLD + ch * 8]) = stv[i];
+    for (int j = 0; j < 5; ++j) {
+      const int n = wave + 4 * j;             // instruction 0..19, wave-uniform
+      if (n < 11) {
+        dma16(rk, k_lane, (uint32_t)(kb * kQK72 * 2 + n * 1024), kl + n * 1024);
+      } else {
+        const int i = n - 11;                 // V^T rows [8i, 8i+8)
+        dma16(rv, v_lane[i & 1], (uint32_t)(((int64_t)8 * i * Np + kb) * 2), vl + 8 * i * kAttnBN * 2);
+      }
     }
   };
 
-  f32x16 oacc[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) oacc[db] = f32x16{};
+  f32x16 oacc[kNDB72] = {f32x16{}, f32x16{}, f32x16{}};
   float m_run = 0.f, l_run = 0.f;
   f32x16 negm = f32x16{};
+
   const int k_begin = seg_s & ~(kAttnBN - 1);
   const int n_kt = (seg_e - k_begin + kAttnBN - 1) / kAttnBN;
-  load_tile(k_begin);
-  store_tile(0);
+  dma_tile(k_begin, 0);
+  wait_dma();
   __syncthreads();
 
-  auto step = [&](auto edge_tag, int it) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    const int cur = it & 1;
-    const int kb = k_begin + it * kAttnBN;
-    const bool more = it + 1 < n_kt;
-    if (more) load_tile(kb + kAttnBN);
-    const bool first = EDGE && it == 0;
-    f32x16 s[2];
+  auto s_blocks = [&](const bf16* sK, f32x16 (&s)[2], bool first) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       s[b] = first ? f32x16{} : negm;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[cur][(b * 32 + l32) * KLD + (ks * 2 + hh) * 8]);
+      for (int ks = 0; ks < kKS72; ++ks) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k72_off(b * 32 + l32, ks * 2 + hh)]);
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
       }
     }
-    if constexpr (EDGE) {
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
-        }
-    }
-    float shift = 0.f;
-    if (first) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      shift = fmaxf(mx, __shfl_xor(mx, 32));
-    }
-    uint32_t pk[2][8];
-    float ts = 0.f, ts2 = 0.f;
-    auto exp_pack = [&](float sh) {
-      ts = 0.f; ts2 = 0.f;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pk[b][j] = pack_bf16x2(__builtin_amdgcn_exp2f(s[b][2 * j] - sh), __builtin_amdgcn_exp2f(s[b][2 * j + 1] - sh));
-          if (j & 1) ts2 = dot2_ones(pk[b][j], ts2); else ts = dot2_ones(pk[b][j], ts);
-        }
-      ts += ts2;
-    };
-    exp_pack(shift);
-    if (first) {
-      m_run = shift;
-    } else if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
-      exp_pack(sh);
-      const float alpha = __builtin_amdgcn_exp2f(-sh);
-      m_run += sh;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-    }
-    if (first || !EDGE) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) negm[r] = -m_run;
-    }
-    l_run += ts;
+  };
+  auto mask_edge = [&](f32x16 (&s)[2], int kb) {
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[b][4 * e2], pk[b][4 * e2 + 1], pk[b][4 * e2 + 2],
-                                                           pk[b][4 * e2 + 3]});
-        const int g = 2 * b + e2;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[cur][(db * 32 + l32) * VLD + (2 * g + hh) * 8]);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
       }
-    if (more) store_tile(cur ^ 1);
+  };
+  auto pv_block = [&](const bf16* sV, int b, const uint32_t (&pk)[8]) {
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2) {
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * e2], pk[4 * e2 + 1], pk[4 * e2 + 2], pk[4 * e2 + 3]});
+      const int g = 2 * b + e2;   // 16-key group within the tile
+#pragma unroll
+      for (int db = 0; db < kNDB72; ++db) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * g + hh)]);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
+      }
+    }
+  };
+  auto rescale = [&](float sh) {
+    const float alpha = __builtin_amdgcn_exp2f(-sh);
+    m_run += sh;
+    l_run *= alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+      for (int db = 0; db < kNDB72; ++db) oacc[db][r] *= alpha;
+      negm[r] = -m_run;
+    }
+  };
+
+  // First tile: the running max is set exactly from both blocks.
+  auto step_first = [&]() {
+    const int kb = k_begin;
+    if (n_kt > 1) dma_tile(kb + kAttnBN, 1);
+    const bf16* sK = smem;
+    const bf16* sV = sK + kKTile72;
+    f32x16 s[2];
+    s_blocks(sK, s, true);
+    mask_edge(s, kb);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+    m_run = fmaxf(mx, __shfl_xor(mx, 32));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negm[r] = -m_run;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      uint32_t pk[8];
+      float ta = 0.f, tb = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j] - m_run), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1] - m_run);
+        pk[j] = pack_bf16x2(e0, e1);
+        ta += e0;
+        tb += e1;
+      }
+      l_run += ta + tb;
+      pv_block(sV, b, pk);
+    }
+    wait_dma();
     __syncthreads();
   };
 
-  step(std::true_type{}, 0);
-  for (int it = 1; it + 1 < n_kt; ++it) step(std::false_type{}, it);
-  if (n_kt > 1) step(std::true_type{}, n_kt - 1);
+  // Later tiles, one 32-key block at a time (see attn_fwd_hd64_kernel's step_blocks).
+  auto step_blocks = [&](auto edge_tag, int it) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    const int cur = it & 1;
+    const int kb = k_begin + it * kAttnBN;
+    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
+    const bf16* sK = smem + cur * (kKTile72 + kVTile72);
+    const bf16* sV = sK + kKTile72;
+    f32x16 s[2];
+    s_blocks(sK, s, false);
+    if constexpr (EDGE) mask_edge(s, kb);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      uint32_t pk[8];
+      float ts;
+      auto exp_block = [&]() {
+        float ta = 0.f, tb = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j]), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1]);
+          pk[j] = pack_bf16x2(e0, e1);
+          ta += e0;
+          tb += e1;
+        }
+        ts = ta + tb;
+      };
+      exp_block();
+      if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+        const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
+#pragma unroll
+        for (int bb = b; bb < 2; ++bb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[bb][r] -= sh;
+        exp_block();
+        rescale(sh);
+      }
+      l_run += ts;
+      pv_block(sV, b, pk);
+    }
+    wait_dma();
+    __syncthreads();
+  };
+
+  step_first();
+  for (int it = 1; it + 1 < n_kt; ++it) step_blocks(std::false_type{}, it);
+  if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l_tot;
   if (qrow < seg_e) {
-    bf16* orow = O + (int64_t)qrow * ldo + head * hd;
+    bf16* orow = O + (int64_t)qrow * ldo + head * kHD72;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < kNDB72; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + 8 * g + 4 * hh;
-        if (d < hd) {   // hd % 4 == 0: the 4-wide piece is all in or all out
-          u32x2 o = {pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
-                     pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv)};
-          *reinterpret_cast<u32x2*>(orow + d) = o;
-        }
+        if (d >= kHD72) continue;
+        u32x2 o = {pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
+                   pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = o;
       }
   }
 }
+
 
 // Relayout for the general kernel: q/k/v [N, H*hd] (row stride ld) -> rotated, scaled Q and
 // rotated K [H][Np][HDP] (dims >= hd zero), V^T [H][VROWS][Np] (rows >= hd zero, keys at vt_pos);
@@ -525,16 +552,10 @@ __global__ __launch_bounds__(256) void attn_relayout_general_kernel(
 int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
                       int H, int hd, bf16* out, int64_t ldo, hipStream_t stream) {
   if (n_tiles == 0) return QVL_OK;
-  if (hd == 72) {
-    hipLaunchKernelGGL((attn_fwd_general_kernel<80, 3>), dim3((unsigned)n_tiles), dim3(256), 0, stream,
-                       Qb, Kb, Vtb, d_tiles, Np, H, hd, out, ldo);
-  } else if (hd == 64) {
-    hipLaunchKernelGGL((attn_fwd_general_kernel<64, 2>), dim3((unsigned)n_tiles), dim3(256), 0, stream,
-                       Qb, Kb, Vtb, d_tiles, Np, H, hd, out, ldo);
-  } else {
-    return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
-  }
-  return check_launch("attn_fwd_general");
+  if (hd != kHD72) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (general kernel: 72)", hd);
+  hipLaunchKernelGGL(attn_fwd_hd72_kernel, dim3((unsigned)n_tiles), dim3(256), 0, stream, Qb, Kb, Vtb, d_tiles, Np, H,
+                     out, ldo);
+  return check_launch("attn_fwd_hd72");
 }
 
 int attention_relayout_general(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,

@@ -396,13 +396,14 @@ int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* pos_hw, int64_t
 static int64_t attn_np(int64_t n) { return round_up(std::max<int64_t>(n, 1), 64); }
 
 // Head-major attention operand geometry: Q/K rows of `hdp` dims, V^T of `vrows` rows. bf16
-// pads head_dim 72 to 80 (Q/K) and 96 (V^T); fp32 keeps Q/K exact and pads V^T to 32-row blocks.
+// head_dim 72 stores Q/K rows of 88 (176 bytes, the hd-72 kernel's DMA / LDS row) and V^T rows
+// 0..71; fp32 keeps Q/K exact and pads V^T to 32-row blocks.
 static int attn_dims(int dtype, int hd, int* hdp, int* vrows) {
   if (hd != 64 && hd != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
   if (dtype == QVL_DTYPE_F32) { *hdp = hd; *vrows = (int)round_up(hd, 32); return QVL_OK; }
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
-  *hdp = hd == 64 ? 64 : 80;
-  *vrows = hd == 64 ? 64 : 96;
+  *hdp = hd == 64 ? 64 : 88;
+  *vrows = hd == 64 ? 64 : 72;
   return QVL_OK;
 }
 

@@ -148,7 +148,7 @@ def test_workspace_sizes(pkg):
     cfg.dtype = pkg.capi.QVL_DTYPE_BF16
     cfg.spatial_merge_size = 3
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == -2
-    for dt, hd, want in ((pkg.capi.QVL_DTYPE_BF16, 72, 16 * 64 * (80 + 80 + 96) * 2),
+    for dt, hd, want in ((pkg.capi.QVL_DTYPE_BF16, 72, 16 * 64 * (88 + 88 + 72) * 2),
                          (pkg.capi.QVL_DTYPE_F32, 72, 16 * 64 * (72 + 72 + 96) * 4),
                          (pkg.capi.QVL_DTYPE_F32, 64, 16 * 64 * (64 + 64 + 64) * 4)):
         assert lib.qvl_vision_attention_workspace_size(dt, 10, 16, hd, C.byref(nb)) == 0

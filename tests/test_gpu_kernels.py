@@ -220,7 +220,7 @@ def test_attention_segment_isolation_exact(pkg, lib):
 
 def test_attention_config4_hd72_vs_oracle(pkg, lib):
     """BASELINE config 4's attention: one 7056-token segment (grid 1x84x84), 16 heads x head_dim 72
-    (Q/K padded to 80 dims, V^T to 96 rows inside the library): rel-L2 <= 1e-2 vs the oracle."""
+    (Q/K rows of 88 dims, V^T of 72 rows inside the library): rel-L2 <= 1e-2 vs the oracle."""
     got, ref, _ = _attention_case(pkg, lib, [(1, 84, 84)], H=16, hd=72, seed=9)
     assert np.isfinite(got).all()
     assert rel_l2(got, ref) <= 1e-2
