@@ -148,6 +148,21 @@ def main():
     cp.check(lib.qvl_dense_workspace_size(C.byref(pb)), "dense ws")
     part = torch.empty(pb.value, dtype=torch.uint8, device=dev)
     pp, pn = part.data_ptr(), pb.value
+    # attention runs the tower's work list: split (attention + combine launches) when the tower
+    # builds one, else whole items
+    ab = C.c_size_t()
+    if md.split_tiles:
+        cp.check(lib.qvl_attention_split_workspace_size(64, md.n_split_tiles, md.n_split_whole, C.byref(ab)),
+                 "attention split ws")
+    apart = torch.empty(max(ab.value, 256), dtype=torch.uint8, device=dev)
+
+    def attention_launch():
+        if md.split_tiles:
+            return lib.qvl_attention_headmajor_split(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
+                                                     md.split_tiles, md.n_split_tiles, md.n_split_whole, N, H, 64,
+                                                     yk.data_ptr(), D, apart.data_ptr(), ab.value)
+        return lib.qvl_attention_headmajor(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
+                                           tens["tiles"].data_ptr(), md.n_tiles, N, H, 64, yk.data_ptr(), D)
     seg = [2304] * 8
     ln_g = torch.ones(D, device=dev)
     ln_b = torch.zeros(D, device=dev)
@@ -192,8 +207,7 @@ def main():
                                              qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn),
             2.0 * N * D * 3 * D, "mfma", spec.depth),
         "attention (varlen, 8 x 2304 tokens, 16x64)": (
-            lambda: lib.qvl_attention_headmajor(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
-                                                tens["tiles"].data_ptr(), md.n_tiles, N, H, 64, yk.data_ptr(), D),
+            attention_launch,
             float(sum(4 * L * L * D for L in seg)), "mfma", spec.depth),
         # memory-bound kernels: algorithmic bytes = every operand read once + every output written once
         "layer_norm (18432x1024 bf16)": (

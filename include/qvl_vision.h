@@ -81,6 +81,16 @@ int qvl_vision_metadata(const int32_t* h_grid_thw, int64_t n_grids, int32_t merg
 int qvl_attention_worklist(const int32_t* h_cu_seqlens, int64_t n_segments, int32_t num_heads,
                            int32_t* h_items, int64_t capacity, int64_t* n_items);
 
+/* The same work list balanced for the last round of workgroup slots (bf16 kernels, head_dim 64
+ * or 72; `n_cus` compute units, 4 or 3 workgroups each): the items that would run in the last,
+ * partial round leave the list (their entries become empty items) and are appended as up to 8
+ * parts each that split their key tiles (head field: head | part << 12 | parts << 20). Items
+ * [0, *n_whole) are whole, [*n_whole, *n_items) parts, in item order. Same call convention as
+ * qvl_attention_worklist. The per-segment loop of model.py:585-598, scheduled for one GPU. */
+int qvl_attention_worklist_split(const int32_t* h_cu_seqlens, int64_t n_segments, int32_t num_heads,
+                                 int32_t head_dim, int32_t n_cus, int32_t* h_items, int64_t capacity,
+                                 int64_t* n_items, int64_t* n_whole);
+
 /* Rotary inverse frequencies theta^(-2j/(head_dim/2)), j < head_dim/4, float32
  * (VisionRotaryEmbedding, model.py:540-546 with dim = head_dim/2, model.py:672). */
 int qvl_rotary_inv_freq(int32_t head_dim, float theta, float* h_inv_freq);
@@ -169,6 +179,16 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const 
                             const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,
                             int32_t head_dim, void* d_out, int64_t ld_out);
 
+/* qvl_attention_headmajor on a qvl_attention_worklist_split list (bf16): the parts write their
+ * unnormalised outputs and softmax state to the workspace
+ * (qvl_attention_split_workspace_size(head_dim, n_tiles, n_whole) bytes) and a combine kernel
+ * writes those items' rows (model.py:585-600). */
+int qvl_attention_split_workspace_size(int32_t head_dim, int64_t n_tiles, int64_t n_whole, size_t* bytes);
+int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* d_q, const void* d_k,
+                                  const void* d_vt, const int32_t* d_tiles, int64_t n_tiles, int64_t n_whole,
+                                  int64_t n_tokens, int32_t num_heads, int32_t head_dim, void* d_out,
+                                  int64_t ld_out, void* d_workspace, size_t workspace_bytes);
+
 /* ------------------------------------------------------------------------------------------ */
 /* Whole tower: Qwen3VisionTransformer.__call__ (model.py:801-851) / encode_vision (940-944).   */
 /* ------------------------------------------------------------------------------------------ */
@@ -249,6 +269,11 @@ typedef struct qvl_vision_metadata_dev {
   const int32_t* window_tiles;    /* [n_window_tiles, 4]                                     */
   const int32_t* window_index;    /* [n_tokens/4] merge group at each window-order position  */
   const int32_t* window_reverse;  /* [n_tokens/4] argsort(window_index)                      */
+  /* optional (bf16): a qvl_attention_worklist_split list of the full-attention segments, used
+   * instead of `tiles` when split_tiles is not NULL. */
+  int64_t n_split_tiles;
+  int64_t n_split_whole;
+  const int32_t* split_tiles;     /* [n_split_tiles, 4]                                      */
 } qvl_vision_metadata_dev;
 
 int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tokens, size_t* bytes);

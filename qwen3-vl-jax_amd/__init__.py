@@ -6,8 +6,8 @@ build into `libqvl.so` next to this file (`build.py`).
 """
 from . import capi
 from .vision import (GridMetadata, Qwen3VisionTransformer, Qwen3VLModel, VisionBackboneSpec, VisionEmbeddings,
-                     grid_metadata, random_params, spec_2b, spec_8b)
-from . import decoder_io, preprocess, weights
+                     attention_worklist_split, grid_metadata, random_params, spec_2b, spec_8b)
+from . import decoder_io, preprocess, vision, weights
 
 __all__ = ["capi", "GridMetadata", "Qwen3VisionTransformer", "Qwen3VLModel", "VisionBackboneSpec", "VisionEmbeddings",
-           "grid_metadata", "random_params", "spec_2b", "spec_8b", "decoder_io", "preprocess", "weights"]
+           "attention_worklist_split", "grid_metadata", "random_params", "spec_2b", "spec_8b", "decoder_io", "preprocess", "weights"]

@@ -53,7 +53,7 @@ class VisionWeights(C.Structure):
 class VisionMetadataDev(C.Structure):
     _fields_ = [("n_tokens", _i64), ("n_tiles", _i64), ("pos_hw", _p), ("tap_idx", _p), ("tap_w", _p),
                 ("tiles", _p), ("n_window_tiles", _i64), ("window_tiles", _p), ("window_index", _p),
-                ("window_reverse", _p)]
+                ("window_reverse", _p), ("n_split_tiles", _i64), ("n_split_whole", _i64), ("split_tiles", _p)]
 
 
 # name -> (restype, argtypes); every function in include/qvl_vision.h
@@ -64,6 +64,8 @@ SIGNATURES = {
     "qvl_grid_counts": (C.c_int, [_pi32, _i64, _i32, C.POINTER(_i64), C.POINTER(_i64)]),
     "qvl_vision_metadata": (C.c_int, [_pi32, _i64, _i32, _i32, _i32, _pi32, _pi32, _pi32, _pf32]),
     "qvl_attention_worklist": (C.c_int, [_pi32, _i64, _i32, _pi32, _i64, C.POINTER(_i64)]),
+    "qvl_attention_worklist_split": (C.c_int, [_pi32, _i64, _i32, _i32, _i32, _pi32, _i64, C.POINTER(_i64),
+                                               C.POINTER(_i64)]),
     "qvl_rotary_inv_freq": (C.c_int, [_i32, _f32, _pf32]),
     "qvl_pack_dense_weight": (C.c_int, [_p, _i32, _p, _i64, _i64, _p]),
     "qvl_cast": (C.c_int, [_p, _i32, _p, _p, _i64]),
@@ -78,6 +80,9 @@ SIGNATURES = {
                                        _p, _sz]),
     "qvl_dense_qkv_rotary": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _sz]),
     "qvl_attention_headmajor": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _p, _i64]),
+    "qvl_attention_split_workspace_size": (C.c_int, [_i32, _i64, _i64, C.POINTER(_sz)]),
+    "qvl_attention_headmajor_split": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64,
+                                                _p, _sz]),
     "qvl_encode_vision_workspace_size": (C.c_int, [C.POINTER(VisionConfig), _i64, C.POINTER(_sz)]),
     "qvl_encode_vision": (C.c_int, [_p, C.POINTER(VisionConfig), C.POINTER(VisionWeights),
                                     C.POINTER(VisionMetadataDev), _p, _p, C.POINTER(_p), _p, _sz]),

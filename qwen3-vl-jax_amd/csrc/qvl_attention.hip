@@ -38,15 +38,21 @@ constexpr int kHD = 64;
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * kHD + ((chunk ^ ((row >> 1) & 7)) << 3); }
 __device__ __forceinline__ int v_off(int d, int chunk) { return d * kAttnBN + ((chunk ^ ((d >> 1) & 7)) << 3); }
 
-__global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
+__global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
-    const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo) {
+    const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo, int n_whole,
+    float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * kAttnBN * kHD];   // [stage][K | V^T][64][64]
 
-  // Work item: (segment start, segment end, first query, head); empty items pad short queues.
+  // Work item: (segment start, segment end, first query, head [| part, parts]); empty items pad
+  // short queues.
   const int item = blockIdx.x;
-  const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2], head = tiles[4 * item + 3];
-  if (seg_e <= seg_s) return;
+  const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2];
+  const int hraw = tiles[4 * item + 3];
+  const int head = hraw & kAttnHeadMask;
+  const int part_i = (hraw >> kAttnSplitShift) & 0xff, parts = (hraw >> kAttnPartsShift) & 0xff;
+  // parts live after the whole items and need the partial buffer
+  if (seg_e <= seg_s || (parts && (!part || item < n_whole))) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
@@ -86,8 +92,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
   float m_run = 0.f, l_run = 0.f;
   f32x16 negm = f32x16{};
 
-  const int k_begin = seg_s & ~(kAttnBN - 1);
-  const int n_kt = (seg_e - k_begin + kAttnBN - 1) / kAttnBN;
+  // Key tiles of 64 from the segment start rounded down to 64; a part of a split item takes its
+  // share [t0, t1) of them.
+  const int n_all = (seg_e - (seg_s & ~(kAttnBN - 1)) + kAttnBN - 1) / kAttnBN;
+  const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
+  const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
+  const int n_kt = t1 - t0;
   dma_tile(k_begin, 0);
   wait_dma();
   __syncthreads();
@@ -273,6 +283,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_hd64_kernel(
   if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (parts) {
+    // Part of a split item: unnormalised O^T, running max and row sum, for the combine kernel.
+    if (qrow < seg_e) {
+      float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(kHD);
+      const int ql = wave * 32 + l32;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(pp + ql * kHD + db * 32 + 8 * g + 4 * hh) =
+              f32x4{oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]};
+      if (hh == 0) *reinterpret_cast<f32x2*>(pp + kAttnBM * kHD + 2 * ql) = f32x2{m_run, l_tot};
+    }
+    return;
+  }
   const float inv = 1.0f / l_tot;
   if (qrow < seg_e) {
     bf16* orow = O + (int64_t)qrow * ldo + head * kHD;
@@ -309,12 +334,17 @@ __device__ __forceinline__ int k72_off(int row, int chunk) { return row * kQK72 
 
 __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
-    const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo) {
+    const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo, int n_whole,
+    float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * (kKTile72 + kVTile72)];   // [stage][K 64x88 | V^T 96x64]
 
   const int item = blockIdx.x;
-  const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2], head = tiles[4 * item + 3];
-  if (seg_e <= seg_s) return;
+  const int seg_s = tiles[4 * item], seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2];
+  const int hraw = tiles[4 * item + 3];
+  const int head = hraw & kAttnHeadMask;
+  const int part_i = (hraw >> kAttnSplitShift) & 0xff, parts = (hraw >> kAttnPartsShift) & 0xff;
+  // parts live after the whole items and need the partial buffer
+  if (seg_e <= seg_s || (parts && (!part || item < n_whole))) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
@@ -357,8 +387,10 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   float m_run = 0.f, l_run = 0.f;
   f32x16 negm = f32x16{};
 
-  const int k_begin = seg_s & ~(kAttnBN - 1);
-  const int n_kt = (seg_e - k_begin + kAttnBN - 1) / kAttnBN;
+  const int n_all = (seg_e - (seg_s & ~(kAttnBN - 1)) + kAttnBN - 1) / kAttnBN;
+  const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
+  const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
+  const int n_kt = t1 - t0;
   dma_tile(k_begin, 0);
   wait_dma();
   __syncthreads();
@@ -493,6 +525,23 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (parts) {
+    if (qrow < seg_e) {
+      float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(kHD72);
+      const int ql = wave * 32 + l32;
+#pragma unroll
+      for (int db = 0; db < kNDB72; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = db * 32 + 8 * g + 4 * hh;
+          if (d >= kHD72) continue;
+          *reinterpret_cast<f32x4*>(pp + ql * kHD72 + d) =
+              f32x4{oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]};
+        }
+      if (hh == 0) *reinterpret_cast<f32x2*>(pp + kAttnBM * kHD72 + 2 * ql) = f32x2{m_run, l_tot};
+    }
+    return;
+  }
   const float inv = 1.0f / l_tot;
   if (qrow < seg_e) {
     bf16* orow = O + (int64_t)qrow * ldo + head * kHD72;
@@ -509,6 +558,68 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// Combine of split items: the parts of an item sit in consecutive partial slots; workgroup
+// (slot, chunk) works if `slot` holds part 0 of its item (the others return) and covers 256
+// (query, 4 dims) pairs of it: out = sum_i O_i 2^(m_i - M) / sum_i l_i 2^(m_i - M),
+// M = max_i m_i (scores in log2 units). All parts' loads issue before any use.
+// ---------------------------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict__ tiles, int n_whole, int n_slots,
+                                                           const float* __restrict__ part, bf16* __restrict__ O,
+                                                           int64_t ldo) {
+  constexpr int kChunks = (kAttnBM * (HD / 4) + 255) / 256;
+  const int slot = blockIdx.x / kChunks, chunk = blockIdx.x % kChunks;
+  const int item = n_whole + slot;
+  const int hraw = tiles[4 * item + 3];
+  const int part_i = (hraw >> kAttnSplitShift) & 0xff, parts = (hraw >> kAttnPartsShift) & 0xff;
+  if (part_i != 0 || parts == 0 || parts > kAttnMaxSplit || slot + parts > n_slots) return;
+  const int idx = chunk * 256 + threadIdx.x;
+  if (idx >= kAttnBM * (HD / 4)) return;
+  const int seg_e = tiles[4 * item + 1], q0 = tiles[4 * item + 2], head = hraw & kAttnHeadMask;
+  const int ql = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
+  if (q0 + ql >= seg_e) return;
+  const int64_t slot_floats = attn_partial_floats(HD);
+  const float* p0 = part + (int64_t)slot * slot_floats;
+  f32x2 ml[kAttnMaxSplit];
+  f32x4 o[kAttnMaxSplit];
+#pragma unroll
+  for (int i = 0; i < kAttnMaxSplit; ++i) {
+    if (i < parts) {
+      ml[i] = *reinterpret_cast<const f32x2*>(p0 + i * slot_floats + kAttnBM * HD + 2 * ql);
+      o[i] = *reinterpret_cast<const f32x4*>(p0 + i * slot_floats + ql * HD + d);
+    }
+  }
+  float M = ml[0][0];
+#pragma unroll
+  for (int i = 1; i < kAttnMaxSplit; ++i)
+    if (i < parts) M = fmaxf(M, ml[i][0]);
+  float L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kAttnMaxSplit; ++i) {
+    if (i < parts) {
+      const float sc = __builtin_amdgcn_exp2f(ml[i][0] - M);
+      L = fmaf(ml[i][1], sc, L);
+      acc[0] = fmaf(o[i][0], sc, acc[0]); acc[1] = fmaf(o[i][1], sc, acc[1]);
+      acc[2] = fmaf(o[i][2], sc, acc[2]); acc[3] = fmaf(o[i][3], sc, acc[3]);
+    }
+  }
+  const float inv = 1.0f / L;
+  *reinterpret_cast<u32x2*>(O + (int64_t)(q0 + ql) * ldo + head * HD + d) =
+      u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+}
+
+template <int HD>
+static int launch_combine(const int* d_tiles, int64_t n_tiles, int64_t n_whole, const float* part, bf16* out,
+                          int64_t ldo, hipStream_t stream) {
+  constexpr int kChunks = (kAttnBM * (HD / 4) + 255) / 256;
+  const int64_t n_slots = n_tiles - n_whole;
+  hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3((unsigned)(n_slots * kChunks)), dim3(256), 0, stream, d_tiles,
+                     (int)n_whole, (int)n_slots, part, out, ldo);
+  return check_launch("attn_combine");
+}
 
 // Relayout for the general kernel: q/k/v [N, H*hd] (row stride ld) -> rotated, scaled Q and
 // rotated K [H][Np][HDP] (dims >= hd zero), V^T [H][VROWS][Np] (rows >= hd zero, keys at vt_pos);
@@ -550,12 +661,15 @@ __global__ __launch_bounds__(256) void attn_relayout_general_kernel(
 }
 
 int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
-                      int H, int hd, bf16* out, int64_t ldo, hipStream_t stream) {
+                      int H, int hd, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole, float* part) {
   if (n_tiles == 0) return QVL_OK;
   if (hd != kHD72) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (general kernel: 72)", hd);
+  if (n_whole < 0) n_whole = n_tiles;
   hipLaunchKernelGGL(attn_fwd_hd72_kernel, dim3((unsigned)n_tiles), dim3(256), 0, stream, Qb, Kb, Vtb, d_tiles, Np, H,
-                     out, ldo);
-  return check_launch("attn_fwd_hd72");
+                     out, ldo, (int)n_whole, part);
+  int rc = check_launch("attn_fwd_hd72");
+  if (rc || n_whole >= n_tiles || !part) return rc;
+  return launch_combine<kHD72>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
 }
 
 int attention_relayout_general(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
@@ -606,11 +720,14 @@ __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
 }
 
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles,
-                   int Np, int H, bf16* out, int64_t ldo, hipStream_t stream) {
+                   int Np, int H, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole, float* part) {
   if (n_tiles == 0) return QVL_OK;
+  if (n_whole < 0) n_whole = n_tiles;
   hipLaunchKernelGGL(attn_fwd_hd64_kernel, dim3((unsigned)n_tiles), dim3(256), 0, stream,
-                     Qb, Kb, Vtb, d_tiles, Np, H, out, ldo);
-  return check_launch("attn_fwd_hd64");
+                     Qb, Kb, Vtb, d_tiles, Np, H, out, ldo, (int)n_whole, part);
+  int rc = check_launch("attn_fwd_hd64");
+  if (rc || n_whole >= n_tiles || !part) return rc;
+  return launch_combine<kHD>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
 }
 
 int attention_relayout_hd64(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N,

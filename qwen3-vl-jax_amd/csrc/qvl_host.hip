@@ -269,6 +269,64 @@ int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, 
   return QVL_OK;
 }
 
+int qvl_attention_worklist_split(const int32_t* cu, int64_t n_seg, int32_t num_heads, int32_t head_dim,
+                                 int32_t n_cus, int32_t* items, int64_t capacity, int64_t* n_items,
+                                 int64_t* n_whole) {
+  if (!n_items || !n_whole) return set_error(QVL_ERR_INVALID_ARG, "worklist_split: n_items / n_whole is NULL");
+  if (head_dim != 64 && head_dim != 72)
+    return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: head_dim=%d (supported: 64, 72)", head_dim);
+  if (n_cus <= 0) return set_error(QVL_ERR_INVALID_ARG, "worklist_split: n_cus=%d", n_cus);
+  if (num_heads > kAttnHeadMask) return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: num_heads=%d", num_heads);
+  int64_t n = 0;
+  QVL_TRY_RC(qvl_attention_worklist(cu, n_seg, num_heads, nullptr, 0, &n));
+  std::vector<int32_t> base(4 * (size_t)std::max<int64_t>(n, 1));
+  QVL_TRY_RC(qvl_attention_worklist(cu, n_seg, num_heads, base.data(), n, &n));
+  // The last round of workgroup slots: the kernels run 4 (head_dim 64) or 3 (72) workgroups per
+  // CU. When that round's items leave at least half of the CUs idle, each is split along its key
+  // tiles into up to 8 parts (at least 2 tiles each) so that the parts fill the slots. A round
+  // with one workgroup on most CUs is not split: a CU's lone workgroup runs faster than one of
+  // four, and the parts' partial outputs and the combine cost more than the idle slots (MI355X,
+  // 2304 items on 1024 slots: split 195 us, whole 190 us; 896 items on 768 slots: split 5.5 %
+  // faster over the whole tower).
+  const int64_t slots = (int64_t)n_cus * (head_dim == 64 ? 4 : 3);
+  std::vector<int64_t> real;
+  for (int64_t k = 0; k < n; ++k)
+    if (base[4 * k + 1] > base[4 * k]) real.push_back(k);
+  const int64_t nr = (int64_t)real.size();
+  const int64_t t = nr >= slots ? nr % slots : nr;
+  const int64_t f = t > 0 && 2 * t <= n_cus ? std::min<int64_t>(kAttnMaxSplit, slots / t) : 1;
+  std::vector<std::pair<int64_t, int>> tail;     // (item, parts)
+  if (f >= 2) {
+    for (int64_t i = nr - t; i < nr; ++i) {
+      const int64_t k = real[i];
+      const int32_t s0 = base[4 * k], s1 = base[4 * k + 1];
+      const int64_t n_kt = (s1 - (s0 & ~63) + 63) / 64;
+      const int parts = (int)std::min<int64_t>(f, n_kt / 2);
+      if (parts >= 2) tail.push_back({k, parts});
+    }
+  }
+  int64_t total = n;
+  for (auto& tp : tail) total += tp.second;
+  *n_whole = n;
+  *n_items = total;
+  if (!items) return QVL_OK;
+  if (capacity < total)
+    return set_error(QVL_ERR_INVALID_ARG, "worklist_split capacity %lld < %lld", (long long)capacity, (long long)total);
+  std::copy(base.begin(), base.begin() + 4 * n, items);
+  int64_t w = n;
+  for (auto& tp : tail) {
+    const int32_t* it = &base[4 * tp.first];
+    for (int sp = 0; sp < tp.second; ++sp, ++w) {
+      items[4 * w] = it[0];
+      items[4 * w + 1] = it[1];
+      items[4 * w + 2] = it[2];
+      items[4 * w + 3] = it[3] | (sp << kAttnSplitShift) | (tp.second << kAttnPartsShift);
+    }
+    for (int c = 0; c < 4; ++c) items[4 * tp.first + c] = 0;   // the whole item leaves the main list
+  }
+  return QVL_OK;
+}
+
 int qvl_rotary_inv_freq(int32_t head_dim, float theta, float* inv) {
   if (head_dim <= 0 || head_dim % 4 || head_dim > 128 || !inv)
     return set_error(QVL_ERR_INVALID_ARG, "head_dim=%d", head_dim);
@@ -508,6 +566,36 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const vo
                            hd, (bf16*)out, ld_out, (hipStream_t)stream);
 }
 
+int qvl_attention_split_workspace_size(int32_t head_dim, int64_t n_tiles, int64_t n_whole, size_t* bytes) {
+  if (!bytes || n_tiles < 0 || n_whole < 0 || n_whole > n_tiles)
+    return set_error(QVL_ERR_INVALID_ARG, "attention split ws: bad args");
+  if (head_dim != 64 && head_dim != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", head_dim);
+  *bytes = (size_t)(n_tiles - n_whole) * attn_partial_floats(head_dim) * sizeof(float);
+  return QVL_OK;
+}
+
+int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
+                                  const int32_t* tiles, int64_t n_tiles, int64_t n_whole, int64_t n_tokens, int32_t H,
+                                  int32_t hd, void* out, int64_t ld_out, void* ws, size_t ws_bytes) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention split: bf16 only");
+  if (hd != 64 && hd != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", hd);
+  if (n_tokens < 0 || H <= 0 || n_tiles < 0 || n_whole < 0 || n_whole > n_tiles || ld_out < (int64_t)H * hd ||
+      ld_out % 4)
+    return set_error(QVL_ERR_INVALID_ARG, "attention split: bad sizes");
+  if (n_tokens == 0 || n_tiles == 0) return QVL_OK;
+  if (!q || !k || !vt || !tiles || !out) return set_error(QVL_ERR_INVALID_ARG, "attention split: NULL operand");
+  if ((uintptr_t)out & 7) return set_error(QVL_ERR_MISALIGNED, "attention split: out alignment");
+  const size_t need = (size_t)(n_tiles - n_whole) * attn_partial_floats(hd) * sizeof(float);
+  if (need && (!ws || ws_bytes < need)) return set_error(QVL_ERR_WORKSPACE, "attention split: workspace %zu < %zu", ws_bytes, need);
+  if (need && !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "attention split: workspace alignment");
+  const int Np = (int)attn_np(n_tokens);
+  if (hd == 64)
+    return attention_hd64((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, Np, H, (bf16*)out, ld_out,
+                          (hipStream_t)stream, n_whole, need ? (float*)ws : nullptr);
+  return attention_general((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, Np, H, hd, (bf16*)out,
+                           ld_out, (hipStream_t)stream, n_whole, need ? (float*)ws : nullptr);
+}
+
 // ---------------------------------------------------------------------------------------------
 // whole tower
 // ---------------------------------------------------------------------------------------------
@@ -516,8 +604,12 @@ struct TowerLayout {
   size_t esz;
   int64_t N, Np, D, I_pad, PV, hd, H;
   int hdp, vrows;
-  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, total;
+  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, off_apart, apart_bytes, total;
 };
+
+// Upper bound on the parts of split attention items one work list holds (qvl_attention_
+// worklist_split: at most one per workgroup slot, 4 per CU).
+static int64_t attn_split_slots_bound() { return 4 * (int64_t)gemm_device_cus(); }
 
 static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   if (!c) return set_error(QVL_ERR_INVALID_ARG, "config is NULL");
@@ -555,6 +647,9 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   L->off_cs = take((size_t)N * (hd / 2) * 8);
   L->part_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float) : 0;
   L->off_part = take(L->part_bytes);
+  // partial outputs of split attention items: at most one per workgroup slot (4 per CU)
+  L->apart_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)attn_split_slots_bound() * attn_partial_floats((int)hd) * 4 : 0;
+  L->off_apart = take(L->apart_bytes);
   L->total = o;
   return QVL_OK;
 }
@@ -664,8 +759,15 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     }
     // window mode: blocks outside fullatt_block_indexes attend within windows (model.py:838-839)
     const bool full = !win || ((c->fullatt_mask >> i) & 1ull);
-    QVL_TRY_RC(qvl_attention_headmajor(st, dt, Qb, Kb, Vb, full ? meta->tiles : meta->window_tiles,
-                                       full ? meta->n_tiles : meta->n_window_tiles, N, (int)L.H, (int)L.hd, xn, D));
+    if (full && !f32 && meta->split_tiles) {
+      void* apart = base + L.off_apart;
+      QVL_TRY_RC(qvl_attention_headmajor_split(st, dt, Qb, Kb, Vb, meta->split_tiles, meta->n_split_tiles,
+                                               meta->n_split_whole, N, (int)L.H, (int)L.hd, xn, D, apart,
+                                               L.apart_bytes));
+    } else {
+      QVL_TRY_RC(qvl_attention_headmajor(st, dt, Qb, Kb, Vb, full ? meta->tiles : meta->window_tiles,
+                                         full ? meta->n_tiles : meta->n_window_tiles, N, (int)L.H, (int)L.hd, xn, D));
+    }
     QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, part, PB));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
     QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));

@@ -43,6 +43,14 @@ struct GemmF32Params {
 inline int64_t gemm_partials_elems(int cus) { return (int64_t)cus * 256 * 256; }
 int gemm_device_cus();
 
+// Attention work item head field (the 4th int of a work item): the head in bits 0..11; for a
+// part of a split item, the part index in bits 12..19 and the part count in bits 20..27 (both 0
+// for whole items). A part covers key tiles [n_kt*i/parts, n_kt*(i+1)/parts) of its segment and
+// writes its unnormalised output and softmax state to partial slot (item - n_whole); the combine
+// kernel then writes the item's output.
+constexpr int kAttnHeadMask = 0xfff, kAttnSplitShift = 12, kAttnPartsShift = 20, kAttnMaxSplit = 8;
+__host__ __device__ constexpr int64_t attn_partial_floats(int hd) { return 128 * (int64_t)(hd + 2); }   // per split slot
+
 // Position of key m in the V^T layout the attention kernel reads: within each 16-key group
 // (aligned to 16 in the token index) the middle two 4-key quads are swapped, so that the 8 keys a
 // lane needs as the PV MFMA's k-slots are one contiguous 16-byte chunk.
@@ -54,11 +62,12 @@ __host__ __device__ __forceinline__ int vt_pos(int m) {
 
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream);
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
-                   int H, bf16* out, int64_t ldo, hipStream_t stream);
+                   int H, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole = -1, float* part = nullptr);
 int attention_relayout_hd64(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
                             int H, float qscale, bf16* Qo, bf16* Ko, bf16* Vto, hipStream_t stream);
 int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
-                      int H, int hd, bf16* out, int64_t ldo, hipStream_t stream);
+                      int H, int hd, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole = -1,
+                      float* part = nullptr);
 int attention_relayout_general(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,
                                int H, int hd, int HDP, int VROWS, float qscale, bf16* Qo, bf16* Ko, bf16* Vto,
                                hipStream_t stream);

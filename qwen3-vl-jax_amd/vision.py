@@ -178,6 +178,20 @@ def _worklist(lib, cu: np.ndarray, num_heads: int) -> np.ndarray:
     return tiles[: n.value]
 
 
+def attention_worklist_split(cu: np.ndarray, num_heads: int, head_dim: int, n_cus: int) -> Tuple[np.ndarray, int]:
+    """(items, n_whole) of qvl_attention_worklist_split: the work list of `cu` with the items of
+    the last, partial round of workgroup slots on `n_cus` compute units split along their keys."""
+    lib = capi.load()
+    cu = np.ascontiguousarray(cu, np.int32)
+    n, nw = C.c_int64(), C.c_int64()
+    capi.check(lib.qvl_attention_worklist_split(_i32p(cu), len(cu) - 1, num_heads, head_dim, n_cus, None, 0,
+                                                C.byref(n), C.byref(nw)), "qvl_attention_worklist_split")
+    items = np.zeros((max(n.value, 1), 4), np.int32)
+    capi.check(lib.qvl_attention_worklist_split(_i32p(cu), len(cu) - 1, num_heads, head_dim, n_cus, _i32p(items),
+                                                n.value, C.byref(n), C.byref(nw)), "qvl_attention_worklist_split")
+    return items[: n.value], nw.value
+
+
 def window_metadata(grid_thw, merge: int = 2, patch_size: int = 16, window_size: int = 32):
     """(window_index [N/merge^2], cu_window, cu_full) of `_get_window_index` and the window path's
     full-attention cu_seqlens (model.py:769-799, 828-830), from qvl_window_metadata."""
@@ -238,7 +252,8 @@ class Qwen3VisionTransformer:
     """The vision tower on libqvl. Bind params once (`bind`), then call like the reference module:
     `tokens, deepstack = tower(pixel_values, grid_thw)`."""
 
-    def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0"):
+    def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0",
+                 split_attention: bool = True):
         if dtype not in ("bfloat16", "float32"):
             raise NotImplementedError(f"dtype {dtype!r}: the tower runs in bfloat16 or float32")
         if spec.spatial_merge_size != 2:
@@ -247,6 +262,9 @@ class Qwen3VisionTransformer:
         self.dtype = dtype
         self.qdtype = capi.QVL_DTYPE_BF16 if dtype == "bfloat16" else capi.QVL_DTYPE_F32
         self.device = device
+        # bf16 full attention runs a qvl_attention_worklist_split list (the last round's items split
+        # along keys) when true
+        self.split_attention = split_attention
         self._lib = capi.load()
         self._w = None
         self._keep = []
@@ -456,6 +474,14 @@ class Qwen3VisionTransformer:
             md.window_tiles = tens["window_tiles"].data_ptr()
             md.window_index = tens["window_index"].data_ptr()
             md.window_reverse = tens["window_reverse"].data_ptr()
+        if self.split_attention and self.qdtype == capi.QVL_DTYPE_BF16 and s.head_dim in (64, 72):
+            n_cus = torch.cuda.get_device_properties(torch.device(self.device)).multi_processor_count
+            cu_full = m.cu_full if s.use_window else m.cu_seqlens
+            split, n_whole = attention_worklist_split(cu_full, s.num_heads, s.head_dim, n_cus)
+            tens["split_tiles"] = dev(nz(split))
+            md.n_split_tiles = len(split)
+            md.n_split_whole = n_whole
+            md.split_tiles = tens["split_tiles"].data_ptr()
         entry = (m, tens, md)
         self._meta_cache[key] = entry
         return entry

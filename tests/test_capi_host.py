@@ -204,3 +204,66 @@ def test_window_entry_argument_checks(pkg):
     assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 8, cp.QVL_DTYPE_F32, fake, 8, fake, 6, 4, 8) == -1
     assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 4, cp.QVL_DTYPE_F32, fake, 8, fake, 8, 4, 8) == -1
     assert lib.qvl_gather_rows(None, cp.QVL_DTYPE_F32, fake, 8, cp.QVL_DTYPE_F32, fake, 8, fake, 0, 4, 8) == 0
+
+
+def _split_list(pkg, cu, heads, hd, n_cus):
+    items, n_whole = pkg.attention_worklist_split(np.asarray(cu, np.int32), heads, hd, n_cus)
+    base = pkg.vision._worklist(pkg.capi.load(), np.asarray(cu, np.int32), heads)
+    return items, n_whole, base
+
+
+@pytest.mark.parametrize("cu,heads,hd,n_cus", [([0, 4096, 8192, 18432], 16, 64, 256),   # config 2: no split
+                                               ([0, 4096, 8192, 18432], 16, 64, 280),   # 64-item tail, 8 parts
+                                               ([0, 7056], 16, 72, 256),                # config 4: 6 parts
+                                               ([0, 1024, 2048, 6144], 16, 72, 256),    # 768 items, 768 slots
+                                               ([0, 4096, 4100], 16, 72, 58),   # 1-tile items stay whole
+                                               ([0, 200], 2, 64, 8)])
+def test_attention_worklist_split(pkg, cu, heads, hd, n_cus):
+    """The split list keeps the whole items in place, empties those of the last partial round of
+    workgroup slots, and appends parts whose key tiles cover each such item's keys exactly once."""
+    items, n_whole, base = _split_list(pkg, cu, heads, hd, n_cus)
+    assert n_whole == len(base)
+    whole, parts = items[:n_whole], items[n_whole:]
+    real = lambda a: a[a[:, 1] > a[:, 0]]
+    slots = n_cus * (4 if hd == 64 else 3)
+    nb = len(real(base))
+    tail = nb % slots if nb >= slots else nb
+    gone = [k for k in range(n_whole) if base[k, 1] > base[k, 0] and whole[k, 1] == whole[k, 0]]
+    kept = np.ones(n_whole, bool)
+    kept[gone] = False
+    assert (whole[kept] == base[kept]).all() and (whole[~kept] == 0).all()
+    assert len(gone) <= tail
+    if tail == 0 or 2 * tail > n_cus:      # split only when the last round leaves half the CUs idle
+        assert len(parts) == 0 and not gone
+    head = parts[:, 3] & 0xFFF
+    part_i = (parts[:, 3] >> 12) & 0xFF
+    n_parts = parts[:, 3] >> 20
+    assert len(parts) <= slots and (n_parts >= 2).all() and (n_parts <= 8).all()
+    covered = {}
+    for it, h, p, npart in zip(parts, head, part_i, n_parts):
+        key = (it[0], it[1], it[2], h)
+        covered.setdefault(key, []).append((p, npart))
+    assert sorted(covered) == sorted(tuple(base[k]) for k in gone)
+    for key, ps in covered.items():
+        npart = ps[0][1]
+        assert sorted(p for p, _ in ps) == list(range(npart)) and all(n == npart for _, n in ps)
+        # the kernel's key-tile ranges t0 = n_kt * p / parts tile [0, n_kt) and none is below 2 tiles
+        n_kt = (key[1] - (key[0] & ~63) + 63) // 64
+        bounds = [n_kt * p // npart for p in range(npart + 1)]
+        assert bounds[0] == 0 and bounds[-1] == n_kt and min(np.diff(bounds)) >= 2
+
+
+def test_attention_worklist_split_checks(pkg):
+    lib = pkg.capi.load()
+    cu = np.array([0, 256], np.int32)
+    n, nw = C.c_int64(), C.c_int64()
+    p = cu.ctypes.data_as(C.POINTER(C.c_int32))
+    assert lib.qvl_attention_worklist_split(p, 1, 16, 80, 256, None, 0, C.byref(n), C.byref(nw)) == -2
+    assert lib.qvl_attention_worklist_split(p, 1, 16, 64, 0, None, 0, C.byref(n), C.byref(nw)) == -1
+    assert lib.qvl_attention_worklist_split(p, 1, 16, 64, 256, None, 0, C.byref(n), C.byref(nw)) == 0
+    small = np.zeros((1, 4), np.int32)
+    assert lib.qvl_attention_worklist_split(p, 1, 16, 64, 256, small.ctypes.data_as(C.POINTER(C.c_int32)), 1,
+                                            C.byref(n), C.byref(nw)) == -1
+    nb = C.c_size_t()
+    assert lib.qvl_attention_split_workspace_size(64, 10, 4, C.byref(nb)) == 0 and nb.value == 6 * 128 * 66 * 4
+    assert lib.qvl_attention_split_workspace_size(72, 10, 11, C.byref(nb)) == -1

@@ -236,6 +236,78 @@ def test_attention_hd72_ragged(pkg, lib, grids):
         assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (i, s, e)
 
 
+def _headmajor_operands(H, hd, cu, seed):
+    """Random head-major attention operands in qvl_attention_headmajor's bf16 layout: q (already
+    scaled by head_dim^-0.5 * log2 e) and k as [H][Np][hdp], v^T as [H][vrows][Np] with the keys
+    at their vt_pos positions (hdp, vrows = 64, 64 or 88, 72), padding zero."""
+    N = int(cu[-1])
+    Np = (max(N, 1) + 63) // 64 * 64
+    hdp = 64 if hd == 64 else 88
+    g = torch.Generator().manual_seed(seed)
+    q = torch.zeros((H, Np, hdp)); k = torch.zeros((H, Np, hdp)); vt = torch.zeros((H, hd, Np))
+    q[:, :N, :hd] = torch.randn((H, N, hd), generator=g) * (hd ** -0.5 * 1.4426950408889634)
+    k[:, :N, :hd] = torch.randn((H, N, hd), generator=g)
+    vt[:, :, :N] = torch.randn((H, hd, N), generator=g)
+    q, k, vt = (t.to(torch.bfloat16) for t in (q, k, vt))
+    # V^T stores key n at position vt_pos(n): the middle two groups of 4 in every 16 swap
+    n = np.arange(Np)
+    quad = (n >> 2) & 3
+    pos = (n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3)
+    vt_mem = torch.empty_like(vt)
+    vt_mem[:, :, torch.from_numpy(pos)] = vt
+    # fp32 reference on the CPU: per segment softmax_2(q k^T) v
+    ref = torch.zeros((N, H * hd))
+    for s, e in zip(cu[:-1], cu[1:]):
+        if e <= s:
+            continue
+        sc = torch.einsum("hqd,hkd->hqk", q[:, s:e, :hd].float(), k[:, s:e, :hd].float())
+        p = torch.softmax(sc * 0.6931471805599453, dim=-1)
+        o = torch.einsum("hqk,hdk->hqd", p, vt[:, :, s:e].float())
+        ref[s:e] = o.permute(1, 0, 2).reshape(e - s, H * hd)
+    return q.to(DEV), k.to(DEV), vt_mem.to(DEV), ref.numpy()
+
+
+@pytest.mark.parametrize("hd,cu,H,n_cus", [(64, [0, 4096, 8192, 18432], 16, 280),     # config 2's segments, 8 parts
+                                           (72, [0, 7056], 16, 256),                   # config 4, 6 parts
+                                           (64, [0, 1000, 1003, 5099, 5100], 4, 20),  # ragged, 1-key segments
+                                           (72, [0, 130, 4226], 2, 22)])
+def test_attention_split_items_match_whole(pkg, lib, hd, cu, H, n_cus):
+    """qvl_attention_headmajor_split on a split list agrees with qvl_attention_headmajor on the
+    whole list (rel-L2 <= 5e-3: only the bf16 rounding of P against the parts' running maxima
+    differs) and with an fp32 reference (rel-L2 <= 1e-2)."""
+    cp = pkg.capi
+    cu = np.array(cu, np.int32)
+    N = int(cu[-1])
+    q, k, vt, ref = _headmajor_operands(H, hd, cu, seed=hd + N)
+    base = pkg.vision._worklist(lib, cu, H)
+    split, n_whole = pkg.attention_worklist_split(cu, H, hd, n_cus)
+    assert len(split) > n_whole                                   # the case does split
+    outs = []
+    for items, nw in ((base, None), (split, n_whole)):
+        t = torch.from_numpy(np.ascontiguousarray(items)).to(DEV)
+        out = torch.full((N, H * hd), float("nan"), dtype=torch.bfloat16, device=DEV)
+        if nw is None:
+            cp.check(lib.qvl_attention_headmajor(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(), vt.data_ptr(),
+                                                 t.data_ptr(), len(items), N, H, hd, out.data_ptr(), H * hd))
+        else:
+            nb = C.c_size_t()
+            cp.check(lib.qvl_attention_split_workspace_size(hd, len(items), nw, C.byref(nb)))
+            ws = torch.full((max(nb.value, 16) // 4,), float("nan"), dtype=torch.float32, device=DEV)
+            for _ in range(2):                                     # stale workspace contents do not leak
+                cp.check(lib.qvl_attention_headmajor_split(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(),
+                                                           vt.data_ptr(), t.data_ptr(), len(items), nw, N, H, hd,
+                                                           out.data_ptr(), H * hd, ws.data_ptr(), nb.value))
+        torch.cuda.synchronize()
+        outs.append(to_np(out))
+    whole, parts = outs
+    assert np.isfinite(parts).all()
+    assert rel_l2(parts, whole) <= 5e-3
+    assert rel_l2(parts, ref) <= 1e-2
+    for s, e in zip(cu[:-1], cu[1:]):
+        if e > s:
+            assert rel_l2(parts[s:e], ref[s:e]) <= 1e-2, (s, e)
+
+
 PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x128:nosplit", "288x256:split", "256x256:split",
          "256x128:split", "288x128:split"]
 
