@@ -319,8 +319,9 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
 // state as the hd-64 kernel. K tiles arrive by LDS DMA as contiguous 176-byte rows: 11 16-byte
 // chunks, an odd count, so the 16 rows one fragment read touches fall on 16 distinct bank groups
 // without a swizzle. V^T tiles arrive as 128-byte rows with the hd-64 kernel's XOR swizzle; the
-// third 32-row PV block reads LDS rows 72..95, which the DMA never writes: they only feed output
-// rows 72..95, which are not stored (an MFMA output row depends on its own A row only).
+// third 32-row PV block reads LDS rows 72..95, which the DMA never writes: row 72 holds ones, so
+// output row 72 accumulates the softmax row sums (no VALU adds for them); rows 73..95 only feed
+// output rows that are not stored (an MFMA output row depends on its own A row only).
 // ---------------------------------------------------------------------------------------------
 constexpr int kHD72 = 72;
 constexpr int kQK72 = 88;                  // Q/K row length (elements)
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   };
 
   f32x16 oacc[kNDB72] = {f32x16{}, f32x16{}, f32x16{}};
-  float m_run = 0.f, l_run = 0.f;
+  float m_run = 0.f;
   f32x16 negm = f32x16{};
 
   const int n_all = (seg_e - (seg_s & ~(kAttnBN - 1)) + kAttnBN - 1) / kAttnBN;
@@ -392,6 +393,11 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
   const int n_kt = t1 - t0;
   dma_tile(k_begin, 0);
+  // Row 72 of both V^T stages holds ones (the DMA fills rows 0..71 only): the third PV block then
+  // accumulates each query's row sum of the bf16 P in O^T row 72, with the rescales of O.
+  if (tid < 16)
+    *reinterpret_cast<u32x4*>(smem + (tid >> 3) * (kKTile72 + kVTile72) + kKTile72 + kVR72 * kAttnBN + (tid & 7) * 8) =
+        u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   wait_dma();
   __syncthreads();
 
@@ -430,7 +436,6 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   auto rescale = [&](float sh) {
     const float alpha = __builtin_amdgcn_exp2f(-sh);
     m_run += sh;
-    l_run *= alpha;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
 #pragma unroll
@@ -459,15 +464,11 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       uint32_t pk[8];
-      float ta = 0.f, tb = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j] - m_run), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1] - m_run);
         pk[j] = pack_bf16x2(e0, e1);
-        ta += e0;
-        tb += e1;
       }
-      l_run += ta + tb;
       pv_block(sV, b, pk);
     }
     wait_dma();
@@ -487,21 +488,25 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
     if constexpr (EDGE) mask_edge(s, kb);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
+      // p = exp2(s) as bf16 pairs and the block's largest p (the row sums come from the ones row)
       uint32_t pk[8];
-      float ts;
+      float pmax;
       auto exp_block = [&]() {
-        float ta = 0.f, tb = 0.f;
+        float e[16];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j]), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1]);
-          pk[j] = pack_bf16x2(e0, e1);
-          ta += e0;
-          tb += e1;
+          e[2 * j] = __builtin_amdgcn_exp2f(s[b][2 * j]);
+          e[2 * j + 1] = __builtin_amdgcn_exp2f(s[b][2 * j + 1]);
+          pk[j] = pack_bf16x2(e[2 * j], e[2 * j + 1]);
         }
-        ts = ta + tb;
+        float m0 = fmaxf(fmaxf(e[0], e[1]), e[2]), m1 = fmaxf(fmaxf(e[3], e[4]), e[5]);
+        float m2 = fmaxf(fmaxf(e[6], e[7]), e[8]), m3 = fmaxf(fmaxf(e[9], e[10]), e[11]);
+        float m4 = fmaxf(fmaxf(e[12], e[13]), e[14]);
+        pmax = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), e[15]));
       };
       exp_block();
-      if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
+      // Some row of this block outgrew the stale max by 2^64 (or overflowed): raise it.
+      if (__builtin_amdgcn_ballot_w64(!(pmax <= 0x1p64f)) != 0) {
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
@@ -513,7 +518,6 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
         exp_block();
         rescale(sh);
       }
-      l_run += ts;
       pv_block(sV, b, pk);
     }
     wait_dma();
@@ -524,7 +528,9 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   for (int it = 1; it + 1 < n_kt; ++it) step_blocks(std::false_type{}, it);
   if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  // O^T row 72 (block 2, register 4 of the lanes with hh = 0) is the row sum of query l32
+  const float l_row = oacc[2][4], l_swap = __shfl_xor(l_row, 32);
+  const float l_tot = hh ? l_swap : l_row;
   if (parts) {
     if (qrow < seg_e) {
       float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(kHD72);
