@@ -89,8 +89,18 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   };
 
   f32x16 oacc[2] = {f32x16{}, f32x16{}};
+  // The running max m is kept bf16-representable and enters S^T as a fifth MFMA k-step: K gets
+  // a constant dimension 1 (kx, dims 64..79 = [1, 0, ...]) and Q the dimension -m (qx), so the
+  // MFMAs produce s - m directly, with no C operand to refill per block.
   float m_run = 0.f, l_run = 0.f;
-  f32x16 negm = f32x16{};
+  const bf16x8 kx = __builtin_bit_cast(bf16x8, u32x4{hh ? 0u : 0x3F80u, 0u, 0u, 0u});
+  uint32_t qx0 = 0;
+  auto set_m = [&](float m) {   // m rounded up to bf16 (so s - m <= the exact shift)
+    uint32_t u = __float_as_uint(m);
+    u = m >= 0.f ? (u + 0xFFFFu) & 0xFFFF0000u : u & 0xFFFF0000u;
+    m_run = __uint_as_float(u);
+    qx0 = hh ? 0u : ((u ^ 0x80000000u) >> 16);
+  };
 
   // Key tiles of 64 from the segment start rounded down to 64; a part of a split item takes its
   // share [t0, t1) of them.
@@ -117,12 +127,13 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     f32x16 s[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      s[b] = first ? f32x16{} : negm;
+      s[b] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k_off(b * 32 + l32, ks * 2 + hh)]);
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
       }
+      if (!first) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx, __builtin_bit_cast(bf16x8, u32x4{qx0, 0u, 0u, 0u}), s[b], 0, 0, 0);
     }
     if constexpr (EDGE) {
 #pragma unroll
@@ -140,7 +151,8 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      shift = fmaxf(mx, __shfl_xor(mx, 32));
+      set_m(fmaxf(mx, __shfl_xor(mx, 32)));
+      shift = m_run;
     }
     // p = exp2(s - shift) as bf16 pairs; partial row sum over the rounded values.
     uint32_t pk[2][8];
@@ -159,26 +171,21 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
       ts += ts2;
     };
     exp_pack(shift);
-    if (first) {
-      m_run = shift;
-    } else if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
+    if (!first && __builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
       // Some row of this tile outgrew the stale max: raise it (s holds score - m).
       float mx = -INFINITY;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
-      exp_pack(sh);
-      const float alpha = __builtin_amdgcn_exp2f(-sh);
-      m_run += sh;
+      const float m_old = m_run;
+      set_m(m_old + fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f));
+      const float d = m_run - m_old;
+      exp_pack(d);
+      const float alpha = __builtin_amdgcn_exp2f(-d);
       l_run *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; negm[r] = -m_run; }
-    }
-    if (first) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) negm[r] = -m_run;
+      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
     }
     l_run += ts;
 
@@ -212,14 +219,17 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
     const bf16* sK = smem + cur * (2 * kAttnBN * kHD);
     const bf16* sV = sK + kAttnBN * kHD;
-    f32x16 s[2] = {negm, negm};
+    f32x16 s[2];
+    const bf16x8 qx = __builtin_bit_cast(bf16x8, u32x4{qx0, 0u, 0u, 0u});
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < 2; ++b) {
+      s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx, qx, f32x16{}, 0, 0, 0);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k_off(b * 32 + l32, ks * 2 + hh)]);
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
       }
+    }
     if constexpr (EDGE) {
 #pragma unroll
       for (int b = 0; b < 2; ++b)
@@ -250,17 +260,18 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-        const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
+        const float m_old = m_run;
+        set_m(m_old + fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f));
+        const float d = m_run - m_old;
 #pragma unroll
         for (int bb = b; bb < 2; ++bb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[bb][r] -= sh;
+          for (int r = 0; r < 16; ++r) s[bb][r] -= d;
         exp_block();
-        const float alpha = __builtin_amdgcn_exp2f(-sh);
-        m_run += sh;
+        const float alpha = __builtin_amdgcn_exp2f(-d);
         l_run *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; negm[r] = -m_run; }
+        for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
       }
       l_run += ts;
 #pragma unroll
