@@ -396,8 +396,16 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   };
 
   f32x16 oacc[kNDB72] = {f32x16{}, f32x16{}, f32x16{}};
+  // Running max: bf16-representable, applied by an MFMA k-step as in attn_fwd_hd64_kernel.
   float m_run = 0.f;
-  f32x16 negm = f32x16{};
+  const bf16x8 kx = __builtin_bit_cast(bf16x8, u32x4{hh ? 0u : 0x3F80u, 0u, 0u, 0u});
+  uint32_t qx0 = 0;
+  auto set_m = [&](float m) {   // m rounded up to bf16
+    uint32_t u = __float_as_uint(m);
+    u = m >= 0.f ? (u + 0xFFFFu) & 0xFFFF0000u : u & 0xFFFF0000u;
+    m_run = __uint_as_float(u);
+    qx0 = hh ? 0u : ((u ^ 0x80000000u) >> 16);
+  };
 
   const int n_all = (seg_e - (seg_s & ~(kAttnBN - 1)) + kAttnBN - 1) / kAttnBN;
   const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
@@ -415,7 +423,9 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   auto s_blocks = [&](const bf16* sK, f32x16 (&s)[2], bool first) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      s[b] = first ? f32x16{} : negm;
+      s[b] = first ? f32x16{}
+                   : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx, __builtin_bit_cast(bf16x8, u32x4{qx0, 0u, 0u, 0u}),
+                                                             f32x16{}, 0, 0, 0);
 #pragma unroll
       for (int ks = 0; ks < kKS72; ++ks) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k72_off(b * 32 + l32, ks * 2 + hh)]);
@@ -444,15 +454,17 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
       }
     }
   };
-  auto rescale = [&](float sh) {
-    const float alpha = __builtin_amdgcn_exp2f(-sh);
-    m_run += sh;
+  // Raise m by at least sh; returns the exact raise d and rescales O (row sums included) by 2^-d.
+  auto raise_m = [&](float sh) {
+    const float m_old = m_run;
+    set_m(m_old + sh);
+    const float d = m_run - m_old;
+    const float alpha = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < 16; ++r)
 #pragma unroll
       for (int db = 0; db < kNDB72; ++db) oacc[db][r] *= alpha;
-      negm[r] = -m_run;
-    }
+    return d;
   };
 
   // First tile: the running max is set exactly from both blocks.
@@ -469,9 +481,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-    m_run = fmaxf(mx, __shfl_xor(mx, 32));
-#pragma unroll
-    for (int r = 0; r < 16; ++r) negm[r] = -m_run;
+    set_m(fmaxf(mx, __shfl_xor(mx, 32)));
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       uint32_t pk[8];
@@ -521,13 +531,12 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-        const float sh = fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f);
+        const float d = raise_m(fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f));
 #pragma unroll
         for (int bb = b; bb < 2; ++bb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[bb][r] -= sh;
+          for (int r = 0; r < 16; ++r) s[bb][r] -= d;
         exp_block();
-        rescale(sh);
       }
       pv_block(sV, b, pk);
     }
