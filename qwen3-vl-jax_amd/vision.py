@@ -449,7 +449,7 @@ class Qwen3VisionTransformer:
         """Device copy of the grid's integer metadata, built once per grid and cached."""
         torch = _torch()
         g = np.asarray(grid_thw, dtype=np.int32).reshape(-1, 3)
-        key = tuple(map(tuple, g.tolist()))
+        key = (tuple(map(tuple, g.tolist())), bool(self.split_attention))
         hit = self._meta_cache.get(key)
         if hit is not None:
             return hit

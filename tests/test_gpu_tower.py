@@ -148,6 +148,15 @@ def test_config4_grid_reduced_depth(pkg, params8b):
     assert tuple(tok.shape) == (1764, 4096)
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
+    # the 896 attention items over 768 workgroup slots ran as a split list (128 items x 6 parts on
+    # 256 CUs); the whole list agrees to the bf16 rounding of P against the parts' maxima
+    md = tower.metadata(np.array(grids, np.int32))[2]
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert md.n_split_tiles > md.n_split_whole
+    tower.split_attention = False
+    assert not tower.metadata(np.array(grids, np.int32))[2].split_tiles
+    tok_w, _ = tower(px, np.array(grids, np.int32))
+    assert rel_l2(to_np(tok), to_np(tok_w)) <= 5e-3
 
 
 def test_config2_full_batch_invariance(pkg, params2b):
