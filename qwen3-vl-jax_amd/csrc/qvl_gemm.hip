@@ -307,21 +307,40 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
       if (m < p.Np) *reinterpret_cast<u32x4*>(dst + ((int64_t)(head0 + c / 8) * p.Np + m) * 64 + (c % 8) * 8) = v;
     }
   } else {
+    // One lane per (head, 4 dims, 8 positions): 8 reads of 4 dims of a token, regrouped by
+    // v_perm into the 4 rows' 16-byte runs.
     constexpr int PCH = TM / 8;                   // 8-position chunks per V^T row
-#pragma unroll 2
-    for (int i = 0; i < HPW * 64 * PCH / 64; ++i) {
+    constexpr int ITEMS = HPW * 16 * PCH;
+    static_assert(ITEMS % 64 == 0, "V^T work items must fill whole waves");
+#pragma unroll 1
+    for (int i = 0; i < ITEMS / 64; ++i) {
       const int item = i * 64 + lane;
-      const int r = item / PCH, pc = item % PCH;  // r: head-in-wave * 64 + dim
-      const int h2 = r / 64, d = r % 64;
+      const int r = item / PCH, pc = item % PCH;  // r: head-in-wave * 16 + dim quad
+      const int h2 = r / 16, d = (r % 16) * 4;
       const int P = base + pc * 8;                // 8 consecutive V^T positions
-      bf16 vals[8];
+      uint32_t w01[8], w23[8];                    // dims (d, d+1) and (d+2, d+3) at position P + e
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int t = vt_pos(P + e) - base;       // the token stored at position P + e
-        vals[e] = reg[off(t, h2 * 8 + d / 8) + (d & 7)];
+        const u32x2 v = *reinterpret_cast<const u32x2*>(reg + off(t, h2 * 8 + d / 8) + (d & 7));
+        w01[e] = v.x;
+        w23[e] = v.y;
       }
-      if (P < p.Np)
-        *reinterpret_cast<u32x4*>(p.vt + ((int64_t)(head0 + h2) * 64 + d) * p.Np + P) = __builtin_bit_cast(u32x4, vals);
+      if (P < p.Np) {
+        bf16* row = p.vt + ((int64_t)(head0 + h2) * 64 + d) * p.Np + P;
+        u32x4 o0, o1, o2, o3;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          o0[k] = __builtin_amdgcn_perm(w01[2 * k + 1], w01[2 * k], 0x05040100u);   // low halves: dim d
+          o1[k] = __builtin_amdgcn_perm(w01[2 * k + 1], w01[2 * k], 0x07060302u);   // high halves: dim d+1
+          o2[k] = __builtin_amdgcn_perm(w23[2 * k + 1], w23[2 * k], 0x05040100u);
+          o3[k] = __builtin_amdgcn_perm(w23[2 * k + 1], w23[2 * k], 0x07060302u);
+        }
+        *reinterpret_cast<u32x4*>(row) = o0;
+        *reinterpret_cast<u32x4*>(row + p.Np) = o1;
+        *reinterpret_cast<u32x4*>(row + 2 * (int64_t)p.Np) = o2;
+        *reinterpret_cast<u32x4*>(row + 3 * (int64_t)p.Np) = o3;
+      }
     }
   }
 }
