@@ -10,8 +10,10 @@
  *   - Every device entry is asynchronous on the caller's `stream` (a hipStream_t; NULL = the
  *     default stream) and never allocates: scratch comes in through `workspace`.
  *   - Return 0 (QVL_OK) or a negative QVL_ERR_* code; `qvl_last_error()` returns a message for
- *     the last failure on the calling thread. No other global mutable state: entries are
- *     re-entrant and may be called concurrently from several host threads on different streams.
+ *     the last failure on the calling thread. The only other state is thread-local
+ *     (qvl_set_gemm_plan) or a write-once per-device cache (compute-unit counts, kernel
+ *     attributes set once per process): entries are re-entrant and may be called concurrently
+ *     from several host threads on different streams.
  *   - Activations are row-major [tokens, features]. "Packed" dense weights are [n_out, k_in]
  *     row-major (the transpose of the reference's Flax kernel [in, out], model.py:1152-1153),
  *     with n_out and k_in zero-padded to multiples of 64; biases and LayerNorm affine
@@ -126,6 +128,16 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
                  void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k,
                  void* d_workspace, size_t workspace_bytes);
 
+/* Tile-plan override for the bf16 GEMMs (qvl_dense / qvl_dense_ws / qvl_dense_qkv_rotary and the
+ * GEMMs inside qvl_encode_vision) launched afterwards FROM THE CALLING THREAD ONLY (thread-local;
+ * other threads keep the cost model's choice). For tests and tuning sweeps, not needed by callers:
+ *   tile       0 = cost model (default), 1 = 288x256, 2 = 256x256, 3 = 256x128, 4 = 288x128
+ *                (the rotary qkv epilogue accepts 1 and 2 only and maps 3/4 to 2);
+ *   split_mode 0 = cost model decides the tail split-K, 1 = force it, -1 = forbid it;
+ *   group_n    column tiles per panel of the tile order, 0 = default (4).
+ * (0, 0, 0) restores the defaults. No counterpart in the reference (it has no tile plans). */
+int qvl_set_gemm_plan(int32_t tile, int32_t split_mode, int32_t group_n);
+
 /* LayerNorm over the last axis: fp32 mean / biased variance / rsqrt(var + eps), affine, cast
  * back (model.py:375-388). cols must be a multiple of 8 and <= 8192. bf16 or fp32. */
 int qvl_layer_norm(void* stream, int32_t dtype, const void* d_x, int64_t ldx, const float* d_gamma,
@@ -201,7 +213,7 @@ typedef struct qvl_vision_config {
   int32_t intermediate_size;        /* I (unpadded)                        */
   int32_t patch_volume;             /* C * Tp * P * P                      */
   int32_t spatial_merge_size;       /* must be 2                           */
-  int32_t num_position_embeddings;
+  int32_t num_position_embeddings;  /* 0: no learned pos-embed (pos_table / taps unused)  */
   int32_t n_deepstack;
   int32_t deepstack_indexes[8];
   float ln_eps;                     /* 1e-6                                */
@@ -315,7 +327,8 @@ int qvl_vision_positions(void* stream, const int32_t* d_tokens, int64_t batch, i
 #define QVL_SCATTER_ADD 1   /* `_apply_deepstack`: hidden[pos] += rows  (model.py:880-886) */
 
 /* hidden [batch][seq_len][dim] (hidden_dtype) at row d_pos[b][j] gets rows[b][j] (rows_dtype,
- * cast to hidden_dtype first, `feat.astype(h.dtype)`), for j < n_rows with pos >= 0; ADD rounds
+ * cast to hidden_dtype first, `feat.astype(h.dtype)`), for j < n_rows with 0 <= pos < seq_len
+ * (a position past the row is dropped, as XLA drops out-of-bounds scatter updates); ADD rounds
  * hidden + row to hidden_dtype. `rows_batch_stride` (elements) is 0 to use one set of rows for
  * every batch row (VisionEmbeddings.with_batch_dim, model.py:47-63). `d_pos` / `d_count` come from
  * qvl_vision_positions. Where a row has fewer matches than n_rows, the reference's unfilled

@@ -152,7 +152,7 @@ class VisionSpec:
     temporal_patch_size: int = 2
     spatial_merge_size: int = 2
     in_channels: int = 3
-    num_position_embeddings: int = 2304
+    num_position_embeddings: Optional[int] = 2304          # None: no learned pos-embed table
     deepstack_visual_indexes: Tuple[int, ...] = (5, 11, 17)
     window_size: int = 32
     fullatt_block_indexes: Optional[Tuple[int, ...]] = None      # None: every block (qwen3_vl)
@@ -190,10 +190,10 @@ def init_params(spec: VisionSpec, seed: int = 0, std: float = 0.02, bias_std: fl
         return {"weight": (1.0 + rng.standard_normal(d) * ln_noise).astype(np.float32),
                 "bias": (rng.standard_normal(d) * ln_noise).astype(np.float32)}
 
-    params = {
-        "patch_embed": {"proj": dense_p(spec.patch_volume, D)},
-        "pos_embed": {"embedding": (rng.standard_normal((spec.num_position_embeddings, D)) * std).astype(np.float32)},
-    }
+    params = {"patch_embed": {"proj": dense_p(spec.patch_volume, D)}}
+    if spec.num_position_embeddings:
+        params["pos_embed"] = {"embedding": (rng.standard_normal((spec.num_position_embeddings, D)) * std).astype(
+            np.float32)}
     for i in range(spec.depth):
         params[f"blocks_{i}"] = {
             "norm1": ln_p(D), "norm2": ln_p(D),
@@ -291,9 +291,10 @@ def encode_vision(params: Dict, pixel_values, grid_thw, spec: VisionSpec, precis
     prm = params.get("visual", params)
     grid = np.asarray(grid_thw, dtype=np.int64).reshape(-1, 3)
     x = dense(p.r(pixel_values), prm["patch_embed"]["proj"]["kernel"], prm["patch_embed"]["proj"]["bias"], p)
-    pe = pos_embed(prm["pos_embed"]["embedding"], grid, spec, p)
-    if pe.shape[0] == x.shape[0]:
-        x = p.r(x + pe)
+    if spec.num_position_embeddings:      # no table: nothing added (model.py:701-702, 803-806)
+        pe = pos_embed(prm["pos_embed"]["embedding"], grid, spec, p)
+        if pe.shape[0] == x.shape[0]:
+            x = p.r(x + pe)
     embed = x.copy() if keep_layers else None
     cos, sin = rotary_cos_sin(grid, spec, p)
     cu = ix.cu_seqlens_ref(grid)

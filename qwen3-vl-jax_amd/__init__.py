@@ -5,9 +5,11 @@ Imported as `qwen3_vl_jax_amd` (the directory name `qwen3-vl-jax_amd` is not a P
 build into `libqvl.so` next to this file (`build.py`).
 """
 from . import capi
-from .vision import (GridMetadata, Qwen3VisionTransformer, Qwen3VLModel, VisionBackboneSpec, VisionEmbeddings,
-                     attention_worklist_split, grid_metadata, random_params, spec_2b, spec_8b)
+from .vision import (GridMetadata, Qwen3VisionTransformer, Qwen3VLModel, Qwen3VLSpec, VisionBackboneSpec,
+                     VisionEmbeddings, attention_worklist_split, grid_metadata, random_params, spec_2b, spec_8b,
+                     spec_from_config, vision_spec_from_config)
 from . import decoder_io, preprocess, vision, weights
 
-__all__ = ["capi", "GridMetadata", "Qwen3VisionTransformer", "Qwen3VLModel", "VisionBackboneSpec", "VisionEmbeddings",
-           "attention_worklist_split", "grid_metadata", "random_params", "spec_2b", "spec_8b", "decoder_io", "preprocess", "weights"]
+__all__ = ["capi", "GridMetadata", "Qwen3VisionTransformer", "Qwen3VLModel", "Qwen3VLSpec", "VisionBackboneSpec",
+           "VisionEmbeddings", "attention_worklist_split", "grid_metadata", "random_params", "spec_2b", "spec_8b",
+           "spec_from_config", "vision_spec_from_config", "decoder_io", "preprocess", "weights"]

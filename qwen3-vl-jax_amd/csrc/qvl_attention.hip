@@ -647,6 +647,14 @@ static int launch_combine(const int* d_tiles, int64_t n_tiles, int64_t n_whole, 
   return check_launch("attn_combine");
 }
 
+// One rotary output x*cos + rotate_half(x)*sin in the reference's bf16 arithmetic (model.py:579-582):
+// x and its pair xp are bf16 values, c = (cos, sin) bf16 values; each product and the sum is
+// rounded to bf16 (eager jnp ops). lower: d < hd/2, where rotate_half contributes -xp.
+__device__ __forceinline__ float rope_bf16(float x, float xp, f32x2 c, bool lower) {
+  const float a = round_bf16(x * c.x), b = round_bf16(xp * c.y);
+  return round_bf16(lower ? a - b : a + b);
+}
+
 // Relayout for the general kernel: q/k/v [N, H*hd] (row stride ld) -> rotated, scaled Q and
 // rotated K [H][Np][HDP] (dims >= hd zero), V^T [H][VROWS][Np] (rows >= hd zero, keys at vt_pos);
 // token rows [N, Np) zero. Rotary pairs (d, d + hd/2) with cs[n][d] (d < hd/2).
@@ -668,9 +676,10 @@ __global__ __launch_bounds__(256) void attn_relayout_general_kernel(
       const float a = (float)q[base + d], b = (float)k[base + d];
       const float ap = (float)q[base + (d < half ? d + half : d - half)];
       const float bp = (float)k[base + (d < half ? d + half : d - half)];
-      // x*cos + rotate_half(x)*sin: rotate_half = [-x2, x1]
-      qv = (d < half ? a * c.x - ap * c.y : a * c.x + ap * c.y) * qscale;
-      kv = d < half ? b * c.x - bp * c.y : b * c.x + bp * c.y;
+      // x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1], each product and the sum rounded to
+      // bf16 (model.py:579-582); q then takes the softmax pre-scale (one more rounding)
+      qv = round_bf16(rope_bf16(a, ap, c, d < half)) * qscale;
+      kv = rope_bf16(b, bp, c, d < half);
     }
     Qo[((int64_t)head * Np + n) * HDP + d] = (bf16)qv;
     Ko[((int64_t)head * Np + n) * HDP + d] = (bf16)kv;
@@ -726,8 +735,10 @@ __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
       const int64_t base = (int64_t)n * ld + head * kHD;
       const float a1 = (float)q[base + j], a2 = (float)q[base + j + 32];
       const float b1 = (float)k[base + j], b2 = (float)k[base + j + 32];
-      q1 = (a1 * c.x - a2 * c.y) * qscale; q2 = (a2 * c.x + a1 * c.y) * qscale;
-      k1 = b1 * c.x - b2 * c.y; k2 = b2 * c.x + b1 * c.y;
+      q1 = round_bf16(rope_bf16(a1, a2, c, true)) * qscale;
+      q2 = round_bf16(rope_bf16(a2, a1, c, false)) * qscale;
+      k1 = rope_bf16(b1, b2, c, true);
+      k2 = rope_bf16(b2, b1, c, false);
     }
     bf16* qd = Qo + ((int64_t)head * Np + n) * kHD;
     bf16* kd = Ko + ((int64_t)head * Np + n) * kHD;

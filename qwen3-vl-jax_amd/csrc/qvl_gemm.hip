@@ -14,8 +14,7 @@
 // 64-bank fragment reads; fragments are double-buffered across the four 16-deep k-steps and
 // interleaved one read per MFMA.
 #include <algorithm>
-#include <cstdlib>
-#include <cstring>
+#include <atomic>
 
 #include "qvl_kernels.h"
 
@@ -526,16 +525,18 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
   else epi_store_quad<EPI>(p, m, n, lo);
 }
 
+// Compute units of the current device. A write-once per-device cache: every thread that fills
+// an entry stores the same value (relaxed atomics, no other shared state).
 int gemm_device_cus() {
-  static int cus[64] = {0};   // per device; benign race (every thread stores the same value)
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 // Work plan for BM x BN tiles, one workgroup per CU (every tile shape takes 96-136 KB of LDS).
@@ -577,11 +578,16 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
   return g;
 }
 
-// Column tiles per panel of the tile order (QVL_GEMM_GROUP overrides, for the tests and sweeps).
+// Tile-plan override of the calling thread (qvl_set_gemm_plan): tile 0 = the cost model's
+// choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128; split_mode -1 forbids, 1 forces, 0 lets
+// the cost model decide the tail split; group_n 0 = the default panel width. Thread-local, so a
+// test pinning a plan on one thread does not change another thread's launches.
+struct ForcedPlan { int tile = 0, split_mode = 0, group_n = 0; };
+static thread_local ForcedPlan t_plan;
+
+// Column tiles per panel of the tile order.
 static int gemm_group_n(int tiles_n) {
-  int g = 4;
-  const char* e = getenv("QVL_GEMM_GROUP");
-  if (e && *e) g = atoi(e);
+  const int g = t_plan.group_n > 0 ? t_plan.group_n : 4;
   return std::max(1, std::min(g, tiles_n));
 }
 
@@ -589,13 +595,10 @@ template <int BM, int BN, int WM, int WN, int EPI>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
   const size_t lds = std::max(2 * S::LDS_ELEMS, BM * BN) * sizeof(bf16);
-  static bool attr_set = false;   // benign race: every thread sets the same value
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return set_error(QVL_ERR_LAUNCH, "gemm_bf16: cannot reserve %zu bytes of LDS", lds);
-    attr_set = true;
-  }
+  // once per instantiation (a C++ function-local static: initialised exactly once, thread-safe)
+  static const hipError_t attr_rc = hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr_rc != hipSuccess) return set_error(QVL_ERR_LAUNCH, "gemm_bf16: cannot reserve %zu bytes of LDS", lds);
   p.full_tiles = g.full;
   p.split = g.split;
   p.group_n = gemm_group_n((p.N + BN - 1) / BN);
@@ -619,28 +622,10 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.36e6,
                  kRate288x128 = 1.36e6;   // MACs/us/CU
 
-// Test hook: QVL_GEMM_PLAN = "<tile>[:split|:nosplit]" with tile 288x256 | 256x256 | 256x128 |
-// 288x128 pins the tile shape (and forces or forbids the tail split) so every variant can be
-// checked against the others; unset, the cost model decides.
-struct ForcedPlan { int tile = 0, split_mode = 0; };   // tile: 0 auto, 1/2/3/4 as listed
-
-static ForcedPlan forced_plan() {
-  ForcedPlan f;
-  const char* e = getenv("QVL_GEMM_PLAN");
-  if (!e || !*e) return f;
-  if (!strncmp(e, "288x256", 7)) f.tile = 1;
-  else if (!strncmp(e, "256x256", 7)) f.tile = 2;
-  else if (!strncmp(e, "256x128", 7)) f.tile = 3;
-  else if (!strncmp(e, "288x128", 7)) f.tile = 4;
-  if (strstr(e, ":nosplit")) f.split_mode = -1;
-  else if (strstr(e, ":split")) f.split_mode = 1;
-  return f;
-}
-
 template <int EPI>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const int cus = gemm_device_cus();
-  const ForcedPlan f = forced_plan();
+  const ForcedPlan f = t_plan;
   const GemmPlan a = plan_gemm<288, 256>(p, cus, kRate288x256, f.split_mode);
   const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
@@ -662,6 +647,15 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
     if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI>(p, c, stream);
     return launch_gemm<288, 128, 3, 4, EPI>(p, d, stream);
   }
+}
+
+int gemm_set_plan(int tile, int split_mode, int group_n) {
+  if (tile < 0 || tile > 4 || split_mode < -1 || split_mode > 1 || group_n < 0)
+    return set_error(QVL_ERR_INVALID_ARG, "gemm plan: tile=%d split_mode=%d group_n=%d", tile, split_mode, group_n);
+  t_plan.tile = tile;
+  t_plan.split_mode = split_mode;
+  t_plan.group_n = group_n;
+  return QVL_OK;
 }
 
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream) {

@@ -402,6 +402,10 @@ int qvl_dense(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t l
   return dense_impl(stream, dtype, epi, x, lda, w, bias, res, ldr, y, ldc, m, n, k, nullptr, 0);
 }
 
+int qvl_set_gemm_plan(int32_t tile, int32_t split_mode, int32_t group_n) {
+  return gemm_set_plan(tile, split_mode, group_n);
+}
+
 int qvl_dense_workspace_size(size_t* bytes) {
   if (!bytes) return set_error(QVL_ERR_INVALID_ARG, "bytes is NULL");
   *bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);
@@ -732,9 +736,14 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     px_in = h;
   }
   QVL_TRY_RC(qvl_rotary_table(st, dt, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
-  QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
-  QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV,
-                          part, PB));
+  if (c->num_position_embeddings > 0) {
+    QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
+                            L.PV, part, PB));
+  } else {   // no learned pos-embed table (model.py:676-680, 803-806): the patch embed alone
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, px_in, L.PV, W->patch_w, W->patch_b, nullptr, 0, x, D, N, D, L.PV,
+                            part, PB));
+  }
 
   int ds_next = 0;
   for (int i = 0; i < c->depth; ++i) {

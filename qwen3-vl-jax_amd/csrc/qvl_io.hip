@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(HT* __restrict__ hidd
     return;
   }
   const int p = pos[(int64_t)b * n_rows + j];
-  if (p < 0) return;
+  if (p < 0 || p >= S) return;                             // out of range: dropped, as XLA drops it
   if (MODE == QVL_SCATTER_SET && p == 0 && unfilled) return;   // overwritten by the old row 0 afterwards
   HT* h = hb + (int64_t)p * D;
   const RT* r = rows + (int64_t)b * rows_bstride + j * D;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void scatter_rows_vec_kernel(HT* __restrict__ 
     return;
   }
   const int p = pos[(int64_t)b * n_rows + j];
-  if (p < 0) return;
+  if (p < 0 || p >= S) return;                             // out of range: dropped, as XLA drops it
   if (MODE == QVL_SCATTER_SET && p == 0 && unfilled) return;   // overwritten by the old row 0 afterwards
   HT* h = hb + (int64_t)p * D;
   const RT* r = rows + (int64_t)b * rows_bstride + j * D;

@@ -136,10 +136,12 @@ int layer_norm_bf16(const bf16* x, int64_t ldx, const float* g, const float* b, 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pos-embed bilinear gather (model.py:751-764): one wave per token, 4 table rows weighted. Taps
+// Pos-embed bilinear gather (model.py:751-764): one wave per token, 4 table rows weighted, in
+// the reference's bf16 arithmetic: each tap product rounded to bf16, the sum taken left to right
+// ((t0 + t1) + t2) + t3 with each partial sum rounded (eager jnp ops, model.py:751-752). Taps
 // whose weight is 0 (every tap but one when the grid side equals the table side, e.g. 768-pixel
-// images on the 48 x 48 table) are skipped: their products are exact zeros and leave the sum
-// unchanged, and the wave-uniform test saves their row reads.
+// images on the 48 x 48 table) are skipped: their products are zeros and leave the sum unchanged
+// (up to the sign of a zero sum), and the wave-uniform test saves their row reads.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void pos_embed_bf16_kernel(const bf16* __restrict__ table,
                                                              const int* __restrict__ idx,
@@ -153,14 +155,19 @@ __global__ __launch_bounds__(256) void pos_embed_bf16_kernel(const bf16* __restr
   for (int j = 0; j < 4; ++j) { ti[j] = idx[(int64_t)j * n_tok + n]; tw[j] = wts[(int64_t)j * n_tok + n]; }
   for (int c = lane; c < dim / 8; c += 64) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    bool first = true;                      // wave-uniform
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (tw[j] == 0.f) continue;
       const u32x4 w = *reinterpret_cast<const u32x4*>(table + (int64_t)ti[j] * dim + c * 8);
-      acc[0] += tw[j] * bf16_lo(w.x); acc[1] += tw[j] * bf16_hi(w.x);
-      acc[2] += tw[j] * bf16_lo(w.y); acc[3] += tw[j] * bf16_hi(w.y);
-      acc[4] += tw[j] * bf16_lo(w.z); acc[5] += tw[j] * bf16_hi(w.z);
-      acc[6] += tw[j] * bf16_lo(w.w); acc[7] += tw[j] * bf16_hi(w.w);
+      const float v[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
+                          bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = round_bf16(tw[j] * v[e]);          // the bf16 product (exact in fp32, rounded once)
+        acc[e] = first ? t : round_bf16(acc[e] + t);
+      }
+      first = false;
     }
     u32x4 o = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
                pack_bf16x2(acc[6], acc[7])};

@@ -14,6 +14,7 @@ libqvl kernel launched through the C ABI (no torch math on the product path).
 from __future__ import annotations
 
 import ctypes as C
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Dict, Optional, Sequence, Tuple
 
@@ -63,6 +64,62 @@ class VisionBackboneSpec:
         return self.in_channels * self.temporal_patch_size * self.patch_size ** 2
 
 
+@dataclass
+class Qwen3VLSpec:
+    """The parts of the reference's Qwen3VLSpec (model.py:101-107) this vision path uses: the
+    vision spec and the special token ids. The text backbone is outside this build; its raw HF
+    config dict is kept as `text_config`."""
+    vision: Optional[VisionBackboneSpec]
+    text_config: Dict = field(default_factory=dict)
+    pad_token_id: Optional[int] = None
+    bos_token_id: Optional[int] = None
+    eos_token_id: Optional[int] = None
+
+
+def vision_spec_from_config(vision_cfg: Optional[Dict]) -> Optional[VisionBackboneSpec]:
+    """The vision branch of spec_from_config (model.py:1027-1043), same keys, fallbacks and
+    defaults: patch_size | spatial_patch_size; temporal_patch_size | temporal_patch | 1;
+    window_size | patch_size * spatial_merge_size; in_channels | in_chans | 3;
+    fullatt_block_indexes | deepstack_visual_indexes | [], forced to every block when the config's
+    model_type is exactly "qwen3_vl" (model.py:1033-1034; other model types, e.g. transformers'
+    "qwen3_vl_vision", keep the generic rule, as in the reference);
+    num_position_embeddings None when absent. An empty or missing config gives None."""
+    if not vision_cfg:
+        return None
+    patch = vision_cfg.get("patch_size", vision_cfg.get("spatial_patch_size"))
+    temporal = vision_cfg.get("temporal_patch_size", vision_cfg.get("temporal_patch", 1))
+    window = vision_cfg.get("window_size", patch * vision_cfg.get("spatial_merge_size", 1))
+    fullatt = vision_cfg.get("fullatt_block_indexes", vision_cfg.get("deepstack_visual_indexes", []))
+    if vision_cfg.get("model_type") == "qwen3_vl":
+        fullatt = list(range(vision_cfg["depth"]))
+    return VisionBackboneSpec(
+        hidden_size=vision_cfg["hidden_size"], out_hidden_size=vision_cfg["out_hidden_size"],
+        depth=vision_cfg["depth"], num_heads=vision_cfg["num_heads"],
+        intermediate_size=vision_cfg["intermediate_size"], patch_size=patch, temporal_patch_size=temporal,
+        spatial_merge_size=vision_cfg["spatial_merge_size"], window_size=window,
+        in_channels=vision_cfg.get("in_channels", vision_cfg.get("in_chans", 3)),
+        fullatt_block_indexes=tuple(fullatt),
+        num_position_embeddings=vision_cfg.get("num_position_embeddings"),
+        deepstack_visual_indexes=tuple(vision_cfg.get("deepstack_visual_indexes", [])))
+
+
+def spec_from_config(cfg: Dict) -> Qwen3VLSpec:
+    """HF `config.json` dict -> Qwen3VLSpec (model.py:987-1049): the vision spec from
+    `vision_config` and the token ids; like the reference, a vision model without
+    `rope_scaling.mrope_section` (or with one of other than 3 entries) is rejected."""
+    text_cfg = cfg.get("text_config", cfg)
+    rope_cfg = text_cfg.get("rope_scaling", cfg.get("rope_scaling", {}))
+    vision_cfg = cfg.get("vision_config")
+    section = rope_cfg.get("mrope_section") if isinstance(rope_cfg, dict) else None
+    if vision_cfg and section is None:
+        raise ValueError("Missing rope_scaling.mrope_section for vision model")
+    if vision_cfg and section is not None and len(section) != 3:
+        raise ValueError("mrope_section must have 3 entries for vision models")
+    return Qwen3VLSpec(vision=vision_spec_from_config(vision_cfg), text_config=dict(text_cfg),
+                       pad_token_id=cfg.get("pad_token_id"), bos_token_id=cfg.get("bos_token_id"),
+                       eos_token_id=cfg.get("eos_token_id"))
+
+
 def spec_2b() -> VisionBackboneSpec:
     """Qwen3-VL-2B vision tower shape."""
     return VisionBackboneSpec(hidden_size=1024, out_hidden_size=2048, depth=24, num_heads=16, intermediate_size=4096,
@@ -89,8 +146,10 @@ def random_params(spec: VisionBackboneSpec, seed: int = 0, std: float = 0.02) ->
     def ln(d):
         return {"weight": np.ones(d, np.float32), "bias": np.zeros(d, np.float32)}
 
-    v = {"patch_embed": {"proj": dense(spec.patch_volume, D)},
-         "pos_embed": {"embedding": rng.standard_normal((spec.num_position_embeddings, D), dtype=np.float32) * np.float32(std)}}
+    v = {"patch_embed": {"proj": dense(spec.patch_volume, D)}}
+    if spec.num_position_embeddings:
+        v["pos_embed"] = {"embedding": rng.standard_normal((spec.num_position_embeddings, D),
+                                                           dtype=np.float32) * np.float32(std)}
     for i in range(spec.depth):
         v[f"blocks_{i}"] = {"norm1": ln(D), "norm2": ln(D),
                             "attn": {"qkv": dense(D, 3 * D), "proj": dense(D, D)},
@@ -210,8 +269,10 @@ def window_metadata(grid_thw, merge: int = 2, patch_size: int = 16, window_size:
     return widx[: nt.value // (merge * merge)], cuw, cuf
 
 
-def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
+def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: Optional[int] = 2304,
                   dtype: int = capi.QVL_DTYPE_BF16, num_heads: int = 16) -> GridMetadata:
+    """Integer metadata of one grid_thw. Without a learned pos-embed table
+    (num_position_embeddings None or 0, model.py:676-680) the taps are zeros and unused."""
     g = np.ascontiguousarray(np.asarray(grid_thw, dtype=np.int32).reshape(-1, 3))
     lib = capi.load()
     nt, ns = C.c_int64(), C.c_int64()
@@ -221,8 +282,10 @@ def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: int = 2304,
     pos = np.zeros((N, 2), np.int32)
     idx = np.zeros((4, N), np.int32)
     w = np.zeros((4, N), np.float32)
-    capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, num_position_embeddings, dtype, _i32p(cu),
-                                       _i32p(pos), _i32p(idx), _f32p(w)), "qvl_vision_metadata")
+    npos = int(num_position_embeddings or 0)
+    capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, npos, dtype, _i32p(cu), _i32p(pos),
+                                       _i32p(idx) if npos else None, _f32p(w) if npos else None),
+               "qvl_vision_metadata")
     return GridMetadata(N, cu, pos, idx, w, _worklist(lib, cu, num_heads))
 
 
@@ -252,6 +315,8 @@ class Qwen3VisionTransformer:
     """The vision tower on libqvl. Bind params once (`bind`), then call like the reference module:
     `tokens, deepstack = tower(pixel_values, grid_thw)`."""
 
+    META_CACHE_SIZE = 16   # grids whose device metadata stays cached (LRU)
+
     def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0",
                  split_attention: bool = True):
         if dtype not in ("bfloat16", "float32"):
@@ -269,7 +334,8 @@ class Qwen3VisionTransformer:
         self._w = None
         self._keep = []
         self._state: Dict[str, object] = {}
-        self._meta_cache: Dict[tuple, tuple] = {}
+        # per-grid device metadata, least recently used first (at most META_CACHE_SIZE grids)
+        self._meta_cache: "OrderedDict[tuple, tuple]" = OrderedDict()
         self._ws = None
         cfg = capi.VisionConfig()
         cfg.hidden_size = spec.hidden_size
@@ -340,8 +406,9 @@ class Qwen3VisionTransformer:
             st[name + ".w"], st[name + ".b"] = self._pack_dense(p)
 
         dense("patch_embed", v["patch_embed"]["proj"])
-        st["pos_table"] = torch.from_numpy(np.ascontiguousarray(v["pos_embed"]["embedding"], np.float32)).to(
-            self.device).to(self._tdtype()).contiguous()
+        if s.num_position_embeddings:
+            st["pos_table"] = torch.from_numpy(np.ascontiguousarray(v["pos_embed"]["embedding"], np.float32)).to(
+                self.device).to(self._tdtype()).contiguous()
         for i in range(s.depth):
             b = v[f"blocks_{i}"]
             for n in ("norm1", "norm2"):
@@ -377,7 +444,8 @@ class Qwen3VisionTransformer:
             out[name + ".b"] = ((r64(nout),), "f")
 
         dense("patch_embed", PV, D)
-        out["pos_table"] = ((s.num_position_embeddings, D), "w")
+        if s.num_position_embeddings:
+            out["pos_table"] = ((s.num_position_embeddings, D), "w")
         for i in range(s.depth):
             for n in ("norm1", "norm2"):
                 out[f"blocks.{i}.{n}.w"], out[f"blocks.{i}.{n}.b"] = ((D,), "f"), ((D,), "f")
@@ -414,7 +482,8 @@ class Qwen3VisionTransformer:
         s = self.spec
         p = lambda name: st[name].data_ptr()
         W = capi.VisionWeights()
-        W.patch_w, W.patch_b, W.pos_table = p("patch_embed.w"), p("patch_embed.b"), p("pos_table")
+        W.patch_w, W.patch_b = p("patch_embed.w"), p("patch_embed.b")
+        W.pos_table = p("pos_table") if "pos_table" in st else None
         blocks = (capi.BlockWeights * s.depth)()
         for i in range(s.depth):
             bw = blocks[i]
@@ -452,6 +521,7 @@ class Qwen3VisionTransformer:
         key = (tuple(map(tuple, g.tolist())), bool(self.split_attention))
         hit = self._meta_cache.get(key)
         if hit is not None:
+            self._meta_cache.move_to_end(key)
             return hit
         s = self.spec
         m = grid_metadata(g, s.spatial_merge_size, s.num_position_embeddings, self.qdtype, s.num_heads)
@@ -484,7 +554,13 @@ class Qwen3VisionTransformer:
             md.split_tiles = tens["split_tiles"].data_ptr()
         entry = (m, tens, md)
         self._meta_cache[key] = entry
+        while len(self._meta_cache) > self.META_CACHE_SIZE:
+            self._meta_cache.popitem(last=False)
         return entry
+
+    def clear_metadata_cache(self) -> None:
+        """Drop every cached grid's device metadata."""
+        self._meta_cache.clear()
 
     def workspace(self, n_tokens: int):
         torch = _torch()
@@ -563,6 +639,66 @@ class Qwen3VisionTransformer:
                          I, N, I, D), "fc1")
         ck(lib.qvl_dense(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D,
                          x.data_ptr(), D, N, D, I), "fc2")
+
+    def _fused_ctx(self, ctx):
+        """Buffers of block_fused, added to a _staged_ctx: head-major Q/K/V^T, the split-K
+        partials of the GEMMs and the split attention's partial outputs."""
+        torch = _torch()
+        if "qb" in ctx:
+            return ctx
+        N, H, hd = ctx["N"], ctx["H"], ctx["hd"]
+        if self.qdtype != capi.QVL_DTYPE_BF16 or hd != 64:
+            raise NotImplementedError("block_fused runs the bf16 head_dim-64 fused qkv+rotary entry")
+        Np = -(-N // 64) * 64
+        dev = dict(device=self.device)
+        ctx["qb"] = torch.empty((H, Np, 64), dtype=torch.bfloat16, **dev)
+        ctx["kb"] = torch.empty_like(ctx["qb"])
+        ctx["vb"] = torch.empty_like(ctx["qb"])
+        nb = C.c_size_t()
+        capi.check(self._lib.qvl_dense_workspace_size(C.byref(nb)), "qvl_dense_workspace_size")
+        ctx["gws"] = torch.empty(max(nb.value, 256), dtype=torch.uint8, **dev)
+        ctx["gws_bytes"] = nb.value
+        md = ctx["md"]
+        ab = C.c_size_t(0)
+        if md.split_tiles:
+            capi.check(self._lib.qvl_attention_split_workspace_size(hd, md.n_split_tiles, md.n_split_whole,
+                                                                    C.byref(ab)), "attention split ws")
+        ctx["apart"] = torch.empty(max(ab.value, 256), dtype=torch.uint8, **dev)
+        ctx["apart_bytes"] = ab.value
+        return ctx
+
+    def block_fused(self, i: int, x, ctx) -> None:
+        """VisionBlock i (model.py:627-630) in place on x [N, D] through exactly the entries the
+        whole-tower call runs for a bf16 head_dim-64 tower: LayerNorm, the fused qkv Dense +
+        rotary (qvl_dense_qkv_rotary, head-major Q/K/V^T), attention on the tower's work list
+        (qvl_attention_headmajor_split when the tower builds a split list, else
+        qvl_attention_headmajor), proj + residual, LayerNorm, fc1 + GELU, fc2 + residual, the
+        GEMMs with the tower's split-K workspace."""
+        ctx = self._fused_ctx(ctx)
+        lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
+        N, D, H, hd, I = ctx["N"], ctx["D"], ctx["H"], ctx["hd"], ctx["I"]
+        xn, o, h = ctx["xn"], ctx["o"], ctx["h"]
+        qb, kb, vb = ctx["qb"].data_ptr(), ctx["kb"].data_ptr(), ctx["vb"].data_ptr()
+        gws, gwn = ctx["gws"].data_ptr(), ctx["gws_bytes"]
+        md = ctx["md"]
+        B = self._blocks_arr[i]
+        ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
+        ck(lib.qvl_dense_qkv_rotary(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb, N, D,
+                                    H, gws, gwn), "qkv_rotary")
+        if md.split_tiles:
+            ck(lib.qvl_attention_headmajor_split(st, dt, qb, kb, vb, md.split_tiles, md.n_split_tiles,
+                                                 md.n_split_whole, N, H, hd, o.data_ptr(), D,
+                                                 ctx["apart"].data_ptr(), ctx["apart_bytes"]), "attention_split")
+        else:
+            ck(lib.qvl_attention_headmajor(st, dt, qb, kb, vb, md.tiles, md.n_tiles, N, H, hd, o.data_ptr(), D),
+               "attention")
+        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D,
+                            x.data_ptr(), D, N, D, D, gws, gwn), "proj")
+        ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm2_w, B.norm2_b, xn.data_ptr(), D, N, D, 1e-6), "ln2")
+        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_GELU, xn.data_ptr(), D, B.fc1_w, B.fc1_b, None, 0, h.data_ptr(),
+                            I, N, I, D, gws, gwn), "fc1")
+        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D,
+                            x.data_ptr(), D, N, D, I, gws, gwn), "fc2")
 
     def merger_staged(self, x, ctx, which: int = -1):
         """VisionPatchMerger (model.py:648-656) on the residual stream x: main merger (which=-1) or

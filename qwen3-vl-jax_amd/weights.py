@@ -4,6 +4,8 @@
   weights [out, in], Conv3d patch embed [D, C, Tp, P, P]) -> the reference's Flax tree under
   "visual" (kernels [in, out]; the patch-embed kernel [C*Tp*P*P, D]), the vision half of
   `create_model_from_hf` (model.py:1105-1160) and its key rules (model.py:1071-1103).
+* `load_hf_vision`: config.json + safetensors -> (VisionBackboneSpec, params), through
+  `spec_from_config` (model.py:981-1049).
 * `save_packed` / `load_packed`: the tower's device-ready buffers (weights packed to [n_out, k_in]
   in the tower dtype, zero-padded to 64; fp32 biases / LayerNorm vectors; the pos-embed table) in
   one safetensors file with a JSON header naming the format, dtype and spec. Loading copies the
@@ -16,11 +18,11 @@ import glob
 import json
 import os
 import re
-from typing import Dict, Optional
+from typing import Dict, Optional, Tuple
 
 import numpy as np
 
-from .vision import Qwen3VisionTransformer, VisionBackboneSpec
+from .vision import Qwen3VisionTransformer, VisionBackboneSpec, spec_from_config
 
 PACKED_FORMAT = "qvl-packed-vision"
 PACKED_VERSION = "1"
@@ -101,16 +103,43 @@ def load_hf_vision_params(path: str) -> Dict:
     return params
 
 
+def load_hf_vision(hf_dir: str) -> Tuple[VisionBackboneSpec, Dict]:
+    """A HF checkpoint directory (config.json + *.safetensors) -> (vision spec, {"visual": params}):
+    the vision half of `create_model_from_hf` (model.py:1105-1160), the spec from config.json
+    through spec_from_config (model.py:981-1049). Raises ValueError when the config has no
+    vision backbone."""
+    with open(os.path.join(hf_dir, "config.json")) as f:
+        cfg = json.load(f)
+    spec = spec_from_config(cfg).vision
+    if spec is None:
+        raise ValueError(f"{hf_dir}/config.json has no vision_config")
+    return spec, load_hf_vision_params(hf_dir)
+
+
+def spec_to_json(spec: VisionBackboneSpec) -> str:
+    """The spec as the packed file's header stores it (sequences as lists, None kept as null)."""
+    d = dataclasses.asdict(spec)
+    return json.dumps({k: (list(v) if isinstance(v, (tuple, list)) else v) for k, v in d.items()}, sort_keys=True)
+
+
+def spec_from_json(text: str) -> VisionBackboneSpec:
+    """Inverse of spec_to_json. `fullatt_block_indexes` keeps None ("every block is full
+    attention") distinct from an empty list (window attention on every block)."""
+    d = json.loads(text)
+    fa = d.get("fullatt_block_indexes")
+    d["fullatt_block_indexes"] = None if fa is None else tuple(fa)
+    d["deepstack_visual_indexes"] = tuple(d.get("deepstack_visual_indexes") or ())
+    return VisionBackboneSpec(**d)
+
+
 def save_packed(tower: Qwen3VisionTransformer, path: str) -> None:
     """Write the bound tower's device buffers to `path` (safetensors + JSON metadata)."""
     from safetensors.torch import save_file
 
     state = {k: v.detach().contiguous().cpu() for k, v in tower.packed_state().items()}
-    spec = dataclasses.asdict(tower.spec)
-    spec = {k: (list(v) if isinstance(v, tuple) else v) for k, v in spec.items()}
     meta = {"format": PACKED_FORMAT, "version": PACKED_VERSION, "dtype": tower.dtype,
             "layout": "dense weights [n_out_pad64, k_in_pad64] row-major in dtype; vectors float32",
-            "spec": json.dumps(spec, sort_keys=True)}
+            "spec": spec_to_json(tower.spec)}
     save_file(state, path, metadata=meta)
 
 
@@ -132,10 +161,7 @@ def load_packed(path: str, device: str = "cuda:0") -> Qwen3VisionTransformer:
     from safetensors.torch import load_file
 
     meta = read_packed_metadata(path)
-    spec_d = json.loads(meta["spec"])
-    for k in ("fullatt_block_indexes", "deepstack_visual_indexes"):
-        spec_d[k] = tuple(spec_d.get(k) or ())
-    spec = VisionBackboneSpec(**spec_d)
+    spec = spec_from_json(meta["spec"])
     tower = Qwen3VisionTransformer(spec, dtype=meta["dtype"], device=device)
     state = load_file(path, device=device)
     return tower.bind_packed(state)

@@ -1,5 +1,6 @@
 """Build transformers' Qwen3VLVisionModel with the oracle's weights (an independent implementation
-of the same tower, used to pin the oracle). Helper for tests and tests/golden/make_golden.py."""
+of the same tower, used to pin the oracle). Helper for tests/test_oracle_float.py,
+tests/test_oracle_io.py and tests/test_gpu_io.py."""
 import numpy as np
 
 

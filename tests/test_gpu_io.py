@@ -202,3 +202,30 @@ def test_hf_checkpoint_into_tower(pkg, tmp_path):
     px = torch.from_numpy(np.random.default_rng(4).standard_normal((64, 1536), dtype=np.float32)).cuda()
     a, b = t1(px, grid), t2(px, grid)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1][0], b[1][0])
+
+
+@pytest.mark.parametrize("D", [64, 36])
+def test_scatter_drops_out_of_range_positions(pkg, D):
+    """Caller-supplied positions past the row (>= seq_len) are dropped, as XLA drops out-of-bounds
+    scatter updates; the in-range ones apply as usual (SET and ADD, vector and element kernels)."""
+    cp = pkg.capi
+    lib = cp.load()
+    B, S, V = 2, 50, 6
+    rng = np.random.default_rng(9)
+    hidden = rng.standard_normal((B, S, D)).astype(np.float32)
+    rows = rng.standard_normal((B, V, D)).astype(np.float32)
+    pos = np.array([[3, S, 7, S + 5, 49, 10], [S + 100, 0, 1, 2, S, 4]], np.int32)
+    cnt = np.full(B, V, np.int32)          # every row "filled": no row-0 bookkeeping
+    st = torch.cuda.current_stream().cuda_stream
+    for mode in (cp.QVL_SCATTER_SET, cp.QVL_SCATTER_ADD):
+        h = torch.from_numpy(hidden).cuda()
+        r = torch.from_numpy(rows).cuda()
+        p, c = torch.from_numpy(pos).cuda(), torch.from_numpy(cnt).cuda()
+        cp.check(lib.qvl_scatter_vision_rows(st, mode, cp.QVL_DTYPE_F32, h.data_ptr(), B, S, D, cp.QVL_DTYPE_F32,
+                                             r.data_ptr(), V * D, V, p.data_ptr(), c.data_ptr()), "scatter")
+        ref = hidden.copy()
+        for b in range(B):
+            for j in range(V):
+                if 0 <= pos[b, j] < S:
+                    ref[b, pos[b, j]] = rows[b, j] if mode == cp.QVL_SCATTER_SET else ref[b, pos[b, j]] + rows[b, j]
+        assert np.array_equal(bits(h.cpu().numpy()), bits(ref)), mode

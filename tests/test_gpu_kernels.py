@@ -106,12 +106,13 @@ def test_layer_norm_vs_oracle(pkg, lib, cols):
     assert np.all(np.abs(got - ref) <= 2 * 2 ** -8 * np.abs(ref) + 1e-6)
 
 
-@pytest.mark.parametrize("grids", [[(8, 32, 32)], [(2, 48, 48)]])
+@pytest.mark.parametrize("grids", [[(8, 32, 32)], [(2, 48, 48)], [(1, 84, 84), (3, 10, 6)]])
 def test_pos_embed_vs_oracle(pkg, lib, grids):
-    """4-tap gather: fp32 accumulate, one rounding (the reference rounds each tap in bf16):
-    rel-L2 <= 4e-3 vs the oracle's bf16 pos-embed on config 3's video grid (repeat quirk). On a
-    48 x 48 grid (the table's own side) every token has one tap of weight 1 and three of weight 0,
-    which the kernel skips: the output is exactly that table row."""
+    """4-tap gather in the reference's bf16 arithmetic (each tap product and each partial sum
+    rounded, left to right, model.py:751-752): bit-identical to the oracle's bf16 pos-embed, on
+    config 3's video grid (repeat quirk), config 4's grid and a ragged batch. On a 48 x 48 grid
+    (the table's own side) every token has one tap of weight 1 and three of weight 0, which the
+    kernel skips: the output is exactly that table row."""
     cp = pkg.capi
     spec = vt.VisionSpec()
     table = np.random.default_rng(0).standard_normal((2304, 1024)).astype(np.float32) * 0.02
@@ -122,7 +123,7 @@ def test_pos_embed_vs_oracle(pkg, lib, grids):
     cp.check(lib.qvl_pos_embed(stream(), cp.QVL_DTYPE_BF16, tt.data_ptr(), idx.data_ptr(), w.data_ptr(),
                                out.data_ptr(), m.n_tokens, 1024))
     ref = vt.pos_embed(table, grids, spec, vt._P("bf16"))
-    assert rel_l2(to_np(out), ref) <= 4e-3
+    np.testing.assert_array_equal(to_np(out), ref)
     if grids[0][1] == 48:
         wn = m.tap_w.reshape(4, -1)
         assert np.all(np.sort(wn, axis=0)[-1] == 1.0) and np.all(np.sort(wn, axis=0)[:-1] == 0.0)
@@ -308,6 +309,18 @@ def test_attention_split_items_match_whole(pkg, lib, hd, cu, H, n_cus):
             assert rel_l2(parts[s:e], ref[s:e]) <= 1e-2, (s, e)
 
 
+_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4}
+
+
+def set_plan(lib, cp, plan):
+    """Pin the calling thread's GEMM tile plan ("<tile>:split|:nosplit"); None restores the cost model."""
+    if plan is None:
+        cp.check(lib.qvl_set_gemm_plan(0, 0, 0), "qvl_set_gemm_plan")
+        return
+    tile, mode = plan.split(":")
+    cp.check(lib.qvl_set_gemm_plan(_TILES[tile], 1 if mode == "split" else -1, 0), "qvl_set_gemm_plan")
+
+
 PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x128:nosplit", "288x256:split", "256x256:split",
          "256x128:split", "288x128:split"]
 
@@ -323,7 +336,7 @@ def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
 @pytest.mark.parametrize("epi", [0, 1, 2])
 @pytest.mark.parametrize("m,n,k", [(18432, 1024, 1024), (4600, 2048, 4096), (2304, 4096, 1024), (300, 192, 128),
                                    (18000, 1152, 4352)])
-def test_dense_tile_plans_agree(pkg, lib, monkeypatch, epi, m, n, k):
+def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
     """Every tile shape (288x256 / 256x256 / 256x128 / 288x128) gives bit-identical results without the
     tail split (same K order per output); with the split (fp32 partials summed by the reduce
     kernel) within rel-L2 2e-3 of them; all within rel-L2 4e-3 of torch fp32 on the same bf16
@@ -338,10 +351,12 @@ def test_dense_tile_plans_agree(pkg, lib, monkeypatch, epi, m, n, k):
     cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
     outs = {}
-    for plan in PLANS:
-        monkeypatch.setenv("QVL_GEMM_PLAN", plan)
-        outs[plan] = dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws)
-    monkeypatch.delenv("QVL_GEMM_PLAN")
+    try:
+        for plan in PLANS:
+            set_plan(lib, cp, plan)
+            outs[plan] = dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws)
+    finally:
+        set_plan(lib, cp, None)
     outs["auto"] = dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws)
     ref = ref_dense(x, w, bias, res, epi, n, k).cpu().numpy()
     base = outs["256x256:nosplit"]
@@ -354,7 +369,7 @@ def test_dense_tile_plans_agree(pkg, lib, monkeypatch, epi, m, n, k):
 
 
 @pytest.mark.parametrize("grids", [[(1, 48, 48)] * 8, [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
-def test_qkv_rotary_tile_plans_agree(pkg, lib, monkeypatch, grids):
+def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     """The fused qkv+rotary GEMM writes bit-identical head-major Q/K/V^T (including the zeroed
     padding rows [N, Np)) with 288x256 and 256x256 tiles; with the tail split within rel-L2 2e-3."""
     cp = pkg.capi
@@ -373,16 +388,14 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, monkeypatch, grids):
     Np = -(-N // 64) * 64
     outs = {}
     for plan in ["256x256:nosplit", "288x256:nosplit", "256x256:split", "288x256:split", None]:
-        if plan:
-            monkeypatch.setenv("QVL_GEMM_PLAN", plan)
-        else:
-            monkeypatch.delenv("QVL_GEMM_PLAN")
+        set_plan(lib, cp, plan)
         q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
         k, vt = q.clone(), q.clone()
         cp.check(lib.qvl_dense_qkv_rotary(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, w.data_ptr(), bias.data_ptr(),
                                           cs.data_ptr(), q.data_ptr(), k.data_ptr(), vt.data_ptr(), N, D, H,
                                           ws.data_ptr(), nb.value))
         outs[plan] = [to_np(t) for t in (q, k, vt)]
+    set_plan(lib, cp, None)
     base = outs["256x256:nosplit"]
     for plan, got in outs.items():
         for a, b in zip(got, base):
@@ -392,3 +405,79 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, monkeypatch, grids):
                 assert rel_l2(a, b) <= 2e-3, plan
         q, k, vt = got
         assert not q[:, N:].any() and not k[:, N:].any(), plan
+
+
+def vt_positions(n):
+    """vt_pos of key index n: the middle two 4-key quads of each 16-key group swap."""
+    n = np.asarray(n)
+    quad = (n >> 2) & 3
+    return (n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3)
+
+
+@pytest.mark.parametrize("grids", [[(1, 48, 48)], [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
+def test_qkv_rotary_matches_oracle_rotary(pkg, lib, grids):
+    """The fused qkv Dense + rotary epilogue (qvl_dense_qkv_rotary, the entry the tower runs)
+    against the oracle's bf16 apply_rotary (model.py:579-582: each product and the sum rounded to
+    bf16) applied to the GPU's own qkv Dense output and cos/sin table: bit-exact once the layout is
+    undone (Q = bf16(q_rot * head_dim^-0.5 * log2 e) as [H][Np][64], K = k_rot, V^T[h][d][vt_pos(n)]
+    = v[n][h][d]), padding rows zero. The Dense output itself is within one bf16 ulp of the oracle's
+    Dense on the same operands for every element (equal for >= 99 %)."""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    N, D, H = m.n_tokens, 1024, 16
+    Np = -(-N // 64) * 64
+    rng = np.random.default_rng(N)
+    x_h = vt.bf16_round(rng.standard_normal((N, D)).astype(np.float32))
+    w_h = (rng.standard_normal((D, 3 * D)) * 0.03).astype(np.float32)
+    b_h = vt.bf16_round((rng.standard_normal(3 * D) * 0.1).astype(np.float32))
+    x = bf(x_h)
+    w = pack(lib, cp, w_h)
+    bias = torch.from_numpy(b_h).to(DEV)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    cs = torch.empty((N, 32, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, 64, 10000.0, cs.data_ptr()))
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    qkv = torch.empty((N, 3 * D), dtype=torch.bfloat16, device=DEV)
+    q = torch.full((H, Np, 64), 3.0, dtype=torch.bfloat16, device=DEV)
+    k, vtm = q.clone(), q.clone()
+    try:
+        cp.check(lib.qvl_set_gemm_plan(0, -1, 0))          # no tail split: one K order for both entries
+        cp.check(lib.qvl_dense(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS, x.data_ptr(), D, w.data_ptr(),
+                               bias.data_ptr(), None, 0, qkv.data_ptr(), 3 * D, N, 3 * D, D))
+        cp.check(lib.qvl_dense_qkv_rotary(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, w.data_ptr(), bias.data_ptr(),
+                                          cs.data_ptr(), q.data_ptr(), k.data_ptr(), vtm.data_ptr(), N, D, H,
+                                          ws.data_ptr(), nb.value))
+    finally:
+        cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
+    torch.cuda.synchronize()
+    qkv_h = to_np(qkv)
+    # the Dense against the oracle's (fp32 accumulation in another order: bf16(x.W) may differ by
+    # one ulp of the product, which the bias add carries over, plus one ulp of the output)
+    ref_qkv = vt.dense(x_h, w_h, b_h, vt._P("bf16"))
+    prod = vt.bf16_round(x_h @ vt.bf16_round(w_h))
+    ulp = lambda a: np.exp2(np.floor(np.log2(np.maximum(np.abs(a), 1e-30))) - 7)
+    assert np.all(np.abs(qkv_h - ref_qkv) <= ulp(prod) + ulp(ref_qkv) + 1e-30)
+    assert np.mean(qkv_h == ref_qkv) >= 0.99
+    # rotary, oracle arithmetic on the GPU's qkv and table
+    c_h = cs.cpu().numpy()
+    cos = np.concatenate([c_h[..., 0], c_h[..., 0]], axis=1)
+    sin = np.concatenate([c_h[..., 1], c_h[..., 1]], axis=1)
+    P = vt._P("bf16")
+    qr = vt.apply_rotary(qkv_h[:, :D].reshape(N, H, 64), cos, sin, P)
+    kr = vt.apply_rotary(qkv_h[:, D:2 * D].reshape(N, H, 64), cos, sin, P)
+    vv = qkv_h[:, 2 * D:].reshape(N, H, 64)
+    qscale = np.float32(np.float32(1.0) / np.float32(8.0)) * np.float32(1.4426950408889634)
+    want_q = vt.bf16_round(qr * qscale).transpose(1, 0, 2)
+    got_q, got_k, got_vt = to_np(q), to_np(k), to_np(vtm).reshape(H, 64, Np)      # V^T is [H][64][Np]
+    np.testing.assert_array_equal(got_q[:, :N], want_q)
+    np.testing.assert_array_equal(got_k[:, :N], kr.transpose(1, 0, 2))
+    np.testing.assert_array_equal(got_vt[:, :, vt_positions(np.arange(N))], vv.transpose(1, 2, 0))
+    assert not got_q[:, N:].any() and not got_k[:, N:].any()
+    assert not got_vt[:, :, vt_positions(np.arange(N, Np))].any()
+    # and equal to the oracle's rotary on its own Dense wherever the Dense values agree
+    qr_ref = vt.apply_rotary(ref_qkv[:, :D].reshape(N, H, 64), cos, sin, P).transpose(1, 0, 2)
+    same = (qkv_h[:, :D] == ref_qkv[:, :D]).reshape(N, H, 64).transpose(1, 0, 2)
+    same &= same[..., list(range(32, 64)) + list(range(32))]        # the rotary pair as well
+    np.testing.assert_array_equal(got_q[:, :N][same], vt.bf16_round(qr_ref * qscale)[same])

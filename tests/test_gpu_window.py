@@ -20,13 +20,13 @@ def to_np(t):
     return t.float().cpu().numpy()
 
 
-def window_specs(pkg, depth=4, fullatt=(1, 3), ds=(0, 2), window=64, shape="2b"):
+def window_specs(pkg, depth=4, fullatt=(1, 3), ds=(0, 2), window=64, shape="2b", npos=2304):
     s = pkg.spec_2b() if shape == "2b" else pkg.spec_8b()
     s = dataclasses.replace(s, depth=depth, deepstack_visual_indexes=tuple(ds), fullatt_block_indexes=tuple(fullatt),
-                            window_size=window)
+                            window_size=window, num_position_embeddings=npos)
     o = vt.VisionSpec(hidden_size=s.hidden_size, out_hidden_size=s.out_hidden_size, depth=depth,
                       num_heads=s.num_heads, intermediate_size=s.intermediate_size, deepstack_visual_indexes=tuple(ds),
-                      window_size=window, fullatt_block_indexes=tuple(fullatt))
+                      window_size=window, fullatt_block_indexes=tuple(fullatt), num_position_embeddings=npos)
     return s, o
 
 
@@ -55,6 +55,29 @@ def test_window_tower_vs_oracle(pkg, grids, window, dtype):
     full = pkg.Qwen3VisionTransformer(dataclasses.replace(spec, fullatt_block_indexes=None), dtype=dtype).bind(params)
     tf, _ = full(px, np.array(grids, np.int32))
     assert rel_l2(to_np(tf), to_np(tok)) > 1e-3
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_window_tower_without_pos_embed(pkg, dtype):
+    """A Qwen2.5-style spec: window attention and no learned pos-embed table
+    (num_position_embeddings None, model.py:676-680 / 803-806): the tower runs the patch embed
+    alone and matches the oracle (fp32 <= 1e-4 of fp64, bf16 <= 1e-2 of the bf16 oracle)."""
+    spec, ospec = window_specs(pkg, window=64, npos=None)
+    params = pkg.random_params(spec, seed=32)
+    assert "pos_embed" not in params["visual"]
+    grids = [(1, 8, 12), (2, 4, 4)]
+    n = sum(t * h * w for t, h, w in grids)
+    px = np.random.default_rng(6).standard_normal((n, 1536), dtype=np.float32)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype=dtype).bind(params)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    if dtype == "float32":
+        ref = vt.encode_vision(params, px, grids, ospec, "fp64")
+        bound = 1e-4
+    else:
+        ref = vt.encode_vision(params, px, grids, ospec, "bf16")
+        bound = 1e-2
+    for got, r in zip([tok, *ds], [ref.tokens, *ref.deepstack]):
+        assert rel_l2(to_np(got), r) <= bound
 
 
 @pytest.mark.parametrize("sdt,ddt", [("float32", "bfloat16"), ("float32", "float32"), ("bfloat16", "bfloat16"),
