@@ -201,6 +201,22 @@ int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* d_q, 
                                   int64_t n_tokens, int32_t num_heads, int32_t head_dim, void* d_out,
                                   int64_t ld_out, void* d_workspace, size_t workspace_bytes);
 
+/* qvl_attention_headmajor_split without a workspace argument: the parts' partial outputs go to a
+ * scratch array inside the library (a static device array of qvl_noalloc_scratch_bytes() = 40 MiB,
+ * one per GPU, held until the process ends), so the call allocates nothing and needs no caller
+ * workspace. No counterpart in the reference: it exists for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * A list whose parts need more than the scratch (qvl_attention_split_workspace_size) is refused
+ * with QVL_ERR_WORKSPACE; every other check is qvl_attention_headmajor_split's. All calls on one
+ * GPU share its scratch: calls that overlap in time on one GPU (several streams, or host threads)
+ * race on it and must be serialised by the caller. Nothing in it needs clearing between calls
+ * (each part writes every partial row the combine reads). */
+size_t qvl_noalloc_scratch_bytes(void);
+int qvl_attention_headmajor_split_noalloc(void* stream, int32_t dtype, const void* d_q, const void* d_k,
+                                          const void* d_vt, const int32_t* d_tiles, int64_t n_tiles,
+                                          int64_t n_whole, int64_t n_tokens, int32_t num_heads, int32_t head_dim,
+                                          void* d_out, int64_t ld_out);
+
 /* ------------------------------------------------------------------------------------------ */
 /* Whole tower: Qwen3VisionTransformer.__call__ (model.py:801-851) / encode_vision (940-944).   */
 /* ------------------------------------------------------------------------------------------ */

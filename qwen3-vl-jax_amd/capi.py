@@ -84,6 +84,9 @@ SIGNATURES = {
     "qvl_attention_split_workspace_size": (C.c_int, [_i32, _i64, _i64, C.POINTER(_sz)]),
     "qvl_attention_headmajor_split": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64,
                                                 _p, _sz]),
+    "qvl_noalloc_scratch_bytes": (_sz, []),
+    "qvl_attention_headmajor_split_noalloc": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p,
+                                                        _i64]),
     "qvl_encode_vision_workspace_size": (C.c_int, [C.POINTER(VisionConfig), _i64, C.POINTER(_sz)]),
     "qvl_encode_vision": (C.c_int, [_p, C.POINTER(VisionConfig), C.POINTER(VisionWeights),
                                     C.POINTER(VisionMetadataDev), _p, _p, C.POINTER(_p), _p, _sz]),
