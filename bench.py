@@ -8,7 +8,8 @@ resident in HBM before the timed region; the per-grid integer metadata is built 
 
 Prints ONE JSON line (rank 0): metric/value/unit, timing, `roofline` for the dominant kernel
 (algorithmic FLOPs per launch / average launch time, timed with HIP events on the launch
-stream) and `cpu_baseline` (the numpy oracle on a bounded sample, same process, host cores).
+stream) and `cpu_baseline` (a torch-CPU restatement of the reference on a bounded sample of the
+workload, same process, host cores).
 """
 from __future__ import annotations
 
@@ -56,23 +57,69 @@ def hbm_traffic(kernel):
     return None
 
 
-def cpu_baseline(params, px_one, grid_one, depth=24):
-    """The numpy oracle (fp32, the reference's default dtype) on one image of the workload."""
+def _median_time(fn, reps=3, warmup=1):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), ts
+
+
+def cpu_baseline(params, px_one, grid_one, compiled=True):
+    """The reference's encode_vision restated with torch-CPU kernels (oracle/torch_tower.py; JAX
+    is not installed on the box), timed on this host's cores in this run: config 2's workload on
+    one of its 8 identical images (grid 1x48x48, 2304 patches; every image is an independent
+    segment of the same shape, so patches/s carries over to the batch), 1 warm-up + 3 timed
+    reps, median. Headline `value`: eager fp32 (the reference's default dtype, eager like its
+    run.py:75-80). Also reported: eager bf16, torch.compile'd fp32 (the jitted variant; compile
+    time stated) and config 0 (448x448, 784 patches, fp32)."""
+    import torch
+    from oracle import torch_tower as tt
     from oracle import vision_tower as vt
+
+    threads = torch.get_num_threads()
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    ospec = vt.VisionSpec(depth=depth)
-    vt.encode_vision(params, px_one[:16], [(1, 4, 4)], vt.VisionSpec(depth=1), "fp32")   # warm
-    t0 = time.perf_counter()
-    vt.encode_vision(params, px_one, grid_one, ospec, "fp32")
-    dt = time.perf_counter() - t0
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    spec = vt.VisionSpec(depth=24)
     n = px_one.shape[0]
-    return {"value": n / dt, "unit": "patches/s", "cores": int(threads), "kind": "port",
-            "sample": f"1 of the 8 images (grid 1x48x48, {n} patches), full 24-block tower + mergers, "
-                      f"numpy oracle in fp32 (the reference's default dtype), 1 run of {dt:.1f} s"}
+    variants = {}
+    eager32 = tt.TorchTower(params, spec, "fp32")
+    med, ts = _median_time(lambda: eager32(px_one, grid_one))
+    variants["eager_fp32_config2"] = {"patches_per_s": round(n / med, 1), "median_s": round(med, 3),
+                                      "reps_s": [round(t, 3) for t in ts]}
+    eager16 = tt.TorchTower(params, spec, "bf16")
+    med16, ts16 = _median_time(lambda: eager16(px_one, grid_one))
+    variants["eager_bf16_config2"] = {"patches_per_s": round(n / med16, 1), "median_s": round(med16, 3),
+                                      "reps_s": [round(t, 3) for t in ts16]}
+    px0 = np.random.default_rng(7).standard_normal((784, px_one.shape[1]), dtype=np.float32)
+    med0, ts0 = _median_time(lambda: eager32(px0, [(1, 28, 28)]))
+    variants["eager_fp32_config0"] = {"patches_per_s": round(784 / med0, 1), "median_s": round(med0, 3),
+                                      "reps_s": [round(t, 3) for t in ts0]}
+    if compiled:
+        try:
+            comp = tt.TorchTower(params, spec, "fp32")
+            for name in ("_attention", "_dense", "_ln", "_gelu"):
+                setattr(comp, name, torch.compile(getattr(comp, name), dynamic=False))
+            t0 = time.perf_counter()
+            comp(px_one, grid_one)
+            compile_s = time.perf_counter() - t0
+            medc, tsc = _median_time(lambda: comp(px_one, grid_one), warmup=0)
+            variants["compiled_fp32_config2"] = {"patches_per_s": round(n / medc, 1), "median_s": round(medc, 3),
+                                                 "reps_s": [round(t, 3) for t in tsc],
+                                                 "compile_and_first_run_s": round(compile_s, 1)}
+        except Exception as e:   # the compiled variant is a side figure; report why it is missing
+            variants["compiled_fp32_config2"] = {"error": f"{type(e).__name__}: {str(e)[:200]}"}
+    return {"value": round(n / med, 2), "unit": "patches/s", "cores": int(threads), "kind": "port",
+            "sample": f"config 2 workload, 1 of its 8 identical 768x768 images (grid 1x48x48, {n} patches), full "
+                      f"24-block tower + deepstack + merger; torch-CPU eager restatement of the reference in fp32 "
+                      f"(its default dtype), 1 warm-up + 3 timed reps, median {med:.2f} s; {threads} threads "
+                      f"(affinity mask {affinity} cores)",
+            "affinity_cores": affinity, "variants": variants}
 
 
 def main():
@@ -81,6 +128,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu-compiled", action="store_true", help="skip the torch.compile CPU variant (~35 s)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--only", default=None,
                     help="launch only this kernel class (name prefix, or 'copy') --kernel-reps times; for rocprofv3 runs")
@@ -132,6 +180,7 @@ def main():
     m, tens, md = tower.metadata(grids)
     blk = tower._blocks_arr[0]
     dev = "cuda:0"
+    torch.manual_seed(0)
     xk = torch.randn((N, D), device=dev).to(torch.bfloat16)
     hk = torch.randn((N, I), device=dev).to(torch.bfloat16)
     yk = torch.empty((N, D), dtype=torch.bfloat16, device=dev)
@@ -148,6 +197,11 @@ def main():
     cp.check(lib.qvl_dense_workspace_size(C.byref(pb)), "dense ws")
     part = torch.empty(pb.value, dtype=torch.uint8, device=dev)
     pp, pn = part.data_ptr(), pb.value
+    # attention operands as the tower feeds them: the fused qkv+rotary GEMM on seeded activations
+    # (qkv of block 0), so the attention classes (and `--only attention` counter runs) see real
+    # scores, not uninitialised memory
+    cp.check(lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(), qb.data_ptr(),
+                                      kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn), "qkv operands")
     # attention runs the tower's work list: split (attention + combine launches) when the tower
     # builds one, else whole items
     ab = C.c_size_t()
@@ -318,7 +372,7 @@ def main():
     }
     if not args.no_cpu:
         one = np.array([(1, 48, 48)], np.int32)
-        out["cpu_baseline"] = cpu_baseline(params, px_host[:2304], one)
+        out["cpu_baseline"] = cpu_baseline(params, px_host[:2304], one, compiled=not args.no_cpu_compiled)
         out["gpu_over_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
     print(json.dumps(out), flush=True)
 

@@ -1,6 +1,6 @@
 """Build libqvl.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc.
 
-Every .hip file under csrc/ is compiled for gfx950 in parallel, then linked into
+Every .hip (and host-only .cpp) file under csrc/ is compiled with hipcc for gfx950 in parallel, then linked into
 `qwen3-vl-jax_amd/libqvl.so`. Packed-fp32 VALU ops are disabled for all device code.
 """
 from __future__ import annotations
@@ -37,7 +37,7 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     cc = hipcc()
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no sources under {CSRC}")
 

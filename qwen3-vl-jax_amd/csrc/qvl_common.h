@@ -90,7 +90,8 @@ __device__ __forceinline__ int xcd_remap(int wg, int n) {
 
 }  // namespace qvl
 
-// Error plumbing shared by the host entry points (defined in qvl_host.cpp).
+// Error plumbing shared by the host entry points (set_error in qvl_meta.cpp, check_launch in
+// qvl_host.hip).
 namespace qvl {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);

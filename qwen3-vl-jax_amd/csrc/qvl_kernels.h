@@ -3,6 +3,7 @@
 #include <algorithm>
 
 #include "qvl_common.h"
+#include "qvl_host_common.h"
 
 namespace qvl {
 
@@ -43,12 +44,7 @@ struct GemmF32Params {
 inline int64_t gemm_partials_elems(int cus) { return (int64_t)cus * 256 * 256; }
 int gemm_device_cus();
 
-// Attention work item head field (the 4th int of a work item): the head in bits 0..11; for a
-// part of a split item, the part index in bits 12..19 and the part count in bits 20..27 (both 0
-// for whole items). A part covers key tiles [n_kt*i/parts, n_kt*(i+1)/parts) of its segment and
-// writes its unnormalised output and softmax state to partial slot (item - n_whole); the combine
-// kernel then writes the item's output.
-constexpr int kAttnHeadMask = 0xfff, kAttnSplitShift = 12, kAttnPartsShift = 20, kAttnMaxSplit = 8;
+// (work item head-field layout: qvl_host_common.h)
 __host__ __device__ constexpr int64_t attn_partial_floats(int hd) { return 128 * (int64_t)(hd + 2); }   // per split slot
 
 // Position of key m in the V^T layout the attention kernel reads: within each 16-key group
