@@ -122,11 +122,28 @@ def cpu_baseline(params, px_one, grid_one, compiled=True):
             "affinity_cores": affinity, "variants": variants}
 
 
+# Workloads: BASELINE configs 2 (the headline), 3 and 4; each a tower shape, a grid list and the
+# frames patchify would take (frames, height, width) for the on-device patchify class.
+WORKLOADS = {
+    2: ("2b", [(1, 48, 48)] * 8, (8, 768, 768, 16),
+        "BASELINE config 2: 2B vision tower, 8 x 768x768 images, grid (1,48,48) each, 18432 patches in 8 "
+        "cu_seqlens segments, deepstack after blocks 5/11/17"),
+    3: ("2b", [(8, 32, 32)], (16, 512, 512, 1),
+        "BASELINE config 3: 2B vision tower, 16-frame 512x512 video, grid (8,32,32) = 8192 patches in 8 per-frame "
+        "segments of 1024, deepstack after blocks 5/11/17"),
+    4: ("8b", [(1, 84, 84)], (1, 1344, 1344, 1),
+        "BASELINE config 4: 8B vision tower (depth 27, hidden 1152, 16 x head_dim 72, MLP 4304), one 1344x1344 "
+        "image, grid (1,84,84) = 7056 patches in one segment, deepstack after blocks 8/16/24"),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS),
+                    help="BASELINE config to run (2 = the headline metric's workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cpu-compiled", action="store_true", help="skip the torch.compile CPU variant (~35 s)")
     ap.add_argument("--kernel-reps", type=int, default=20)
@@ -145,9 +162,11 @@ def main():
     cp = pkg.capi
     lib = cp.load()
 
-    spec = pkg.spec_2b()
-    grids = np.array([(1, 48, 48)] * 8, np.int32)
+    shape, grid_list, (n_frames, fh, fw, f_per_seg), workload = WORKLOADS[args.config]
+    spec = pkg.spec_2b() if shape == "2b" else pkg.spec_8b()
+    grids = np.array(grid_list, np.int32)
     N = int(grids[:, 0].dot(grids[:, 1] * grids[:, 2]))
+    seg = [int(h * w) for t, h, w in grid_list for _ in range(t)]
     params = pkg.random_params(spec, seed=0)
     px_host = np.random.default_rng(1).standard_normal((N, spec.patch_volume), dtype=np.float32)
     tower = pkg.Qwen3VisionTransformer(spec).bind(params)
@@ -171,25 +190,29 @@ def main():
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / max(steps, 1)
     value = N / (ms / 1e3)
-    flops = tower_flops(N, [2304] * 8)
+    D, I, H, hd = spec.hidden_size, spec.intermediate_size, spec.num_heads, spec.head_dim
+    Dout, depth, nds = spec.out_hidden_size, spec.depth, len(spec.deepstack_visual_indexes)
+    flops = tower_flops(N, seg, D=D, I=I, depth=depth, n_ds=nds, Dout=Dout, pv=spec.patch_volume)
     step_tflops = flops / (ms / 1e3) / 1e12
 
     # Per-kernel timing (HIP events on the launch stream, over `kernel_reps` back-to-back
     # launches of each kernel class at the workload's shapes, inputs resident in HBM).
-    D, I, H = spec.hidden_size, spec.intermediate_size, spec.num_heads
+    Ip = -(-I // 64) * 64                         # the packed (zero-padded) MLP width the GEMMs run
     m, tens, md = tower.metadata(grids)
     blk = tower._blocks_arr[0]
     dev = "cuda:0"
     torch.manual_seed(0)
     xk = torch.randn((N, D), device=dev).to(torch.bfloat16)
-    hk = torch.randn((N, I), device=dev).to(torch.bfloat16)
+    hk = torch.randn((N, Ip), device=dev).to(torch.bfloat16)
     yk = torch.empty((N, D), dtype=torch.bfloat16, device=dev)
-    hout = torch.empty((N, I), dtype=torch.bfloat16, device=dev)
+    hout = torch.empty((N, Ip), dtype=torch.bfloat16, device=dev)
     Np = -(-N // 64) * 64
-    qb = torch.empty((H, Np, 64), dtype=torch.bfloat16, device=dev)
-    kb, vb = torch.empty_like(qb), torch.empty_like(qb)
-    cs = torch.empty((N, 32, 2), dtype=torch.float32, device=dev)
-    cp.check(lib.qvl_rotary_table(st.cuda_stream, cp.QVL_DTYPE_BF16, tens["pos_hw"].data_ptr(), N, 64, 10000.0,
+    hdp = 64 if hd == 64 else 88
+    qb = torch.empty((H, Np, hdp), dtype=torch.bfloat16, device=dev)
+    kb = torch.empty_like(qb)
+    vb = torch.empty((H, hd, Np), dtype=torch.bfloat16, device=dev)
+    cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, device=dev)
+    cp.check(lib.qvl_rotary_table(st.cuda_stream, cp.QVL_DTYPE_BF16, tens["pos_hw"].data_ptr(), N, hd, 10000.0,
                                   cs.data_ptr()), "rotary")
     s_ = st.cuda_stream
     BF = cp.QVL_DTYPE_BF16
@@ -206,27 +229,26 @@ def main():
     # builds one, else whole items
     ab = C.c_size_t()
     if md.split_tiles:
-        cp.check(lib.qvl_attention_split_workspace_size(64, md.n_split_tiles, md.n_split_whole, C.byref(ab)),
+        cp.check(lib.qvl_attention_split_workspace_size(hd, md.n_split_tiles, md.n_split_whole, C.byref(ab)),
                  "attention split ws")
     apart = torch.empty(max(ab.value, 256), dtype=torch.uint8, device=dev)
 
     def attention_launch():
         if md.split_tiles:
             return lib.qvl_attention_headmajor_split(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
-                                                     md.split_tiles, md.n_split_tiles, md.n_split_whole, N, H, 64,
+                                                     md.split_tiles, md.n_split_tiles, md.n_split_whole, N, H, hd,
                                                      yk.data_ptr(), D, apart.data_ptr(), ab.value)
         return lib.qvl_attention_headmajor(s_, BF, qb.data_ptr(), kb.data_ptr(), vb.data_ptr(),
-                                           tens["tiles"].data_ptr(), md.n_tiles, N, H, 64, yk.data_ptr(), D)
-    seg = [2304] * 8
+                                           tens["tiles"].data_ptr(), md.n_tiles, N, H, hd, yk.data_ptr(), D)
     ln_g = torch.ones(D, device=dev)
     ln_b = torch.zeros(D, device=dev)
-    # The two pixel-sized HBM kernels write (and the cast reads) 113-170 MB per launch; launched back
-    # to back on one buffer their data stays in the 256 MB Infinity Cache and the rate reads above
-    # the HBM peak. They rotate over 3 buffers instead (340 MB / 510 MB), as a fresh batch of
-    # frames would find them, so each launch's bytes go to and come from HBM.
+    # The two pixel-sized HBM kernels write (and the cast reads) 113-170 MB per launch at config 2;
+    # launched back to back on one buffer their data stays in the 256 MB Infinity Cache and the rate
+    # reads above the HBM peak. They rotate over 3 buffers instead (340 MB / 510 MB at config 2), as a
+    # fresh batch of frames would find them, so each launch's bytes go to and come from HBM.
     px_b = [torch.empty((N, spec.patch_volume), dtype=torch.bfloat16, device=dev) for _ in range(3)]
     px_c = [px] + [px.clone() for _ in range(2)]
-    frames_u8 = torch.randint(0, 256, (8, 768, 768, 3), dtype=torch.uint8, device=dev)
+    frames_u8 = torch.randint(0, 256, (n_frames, fh, fw, 3), dtype=torch.uint8, device=dev)
     px_p = [torch.empty((N, spec.patch_volume), dtype=torch.float32, device=dev) for _ in range(3)]
     rot = {"cast": 0, "patchify": 0}
 
@@ -243,48 +265,50 @@ def main():
     vcnt = torch.empty((1,), dtype=torch.int32, device=dev)
     cp.check(lib.qvl_vision_positions(s_, tok_txt.data_ptr(), 1, S_txt, 1, V, vpos.data_ptr(), vcnt.data_ptr()),
              "positions")
+    segs = f"{len(seg)} x {seg[0]}" if len(set(seg)) == 1 else "+".join(map(str, seg))
+    PV = spec.patch_volume
     kernels = {
         # name: (callable, "mfma" FLOPs or "hbm" bytes per launch, bound, launches per step)
-        "fc1 (gemm, bias+GELU) 18432x4096x1024": (
+        f"fc1 (gemm, bias+GELU) {N}x{I}x{D}": (
             lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
-                                     hout.data_ptr(), I, N, I, D, pp, pn), 2.0 * N * D * I, "mfma", spec.depth),
-        "fc2 (gemm, bias+residual) 18432x1024x4096": (
-            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), I, blk.fc2_w, blk.fc2_b,
-                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, I, pp, pn), 2.0 * N * I * D, "mfma",
-            spec.depth),
-        "proj (gemm, bias+residual) 18432x1024x1024": (
+                                     hout.data_ptr(), Ip, N, Ip, D, pp, pn), 2.0 * N * D * I, "mfma", depth),
+        f"fc2 (gemm, bias+residual) {N}x{D}x{I}": (
+            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), Ip, blk.fc2_w, blk.fc2_b,
+                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, Ip, pp, pn), 2.0 * N * I * D, "mfma",
+            depth),
+        f"proj (gemm, bias+residual) {N}x{D}x{D}": (
             lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, xk.data_ptr(), D, blk.proj_w, blk.proj_b,
                                      yk.data_ptr(), D, yk.data_ptr(), D, N, D, D, pp, pn), 2.0 * N * D * D, "mfma",
-            spec.depth),
-        "qkv+rotary (gemm) 18432x3072x1024": (
+            depth),
+        f"qkv+rotary (gemm) {N}x{3 * D}x{D}": (
             lambda: lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(),
                                              qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn),
-            2.0 * N * D * 3 * D, "mfma", spec.depth),
-        "attention (varlen, 8 x 2304 tokens, 16x64)": (
+            2.0 * N * D * 3 * D, "mfma", depth),
+        f"attention (varlen, {segs} tokens, {H}x{hd})": (
             attention_launch,
-            float(sum(4 * L * L * D for L in seg)), "mfma", spec.depth),
+            float(sum(4 * L * L * D for L in seg)), "mfma", depth),
         # memory-bound kernels: algorithmic bytes = every operand read once + every output written once
-        "layer_norm (18432x1024 bf16)": (
+        f"layer_norm ({N}x{D} bf16)": (
             lambda: lib.qvl_layer_norm(s_, BF, xk.data_ptr(), D, ln_g.data_ptr(), ln_b.data_ptr(), yk.data_ptr(), D,
-                                       N, D, 1e-6), 2.0 * N * D * 2 + 2 * D * 4, "hbm", 2 * spec.depth + 4),
-        "pos_embed (18432x1024, 4 bilinear taps)": (
+                                       N, D, 1e-6), 2.0 * N * D * 2 + 2 * D * 4, "hbm", 2 * depth + 1 + nds),
+        f"pos_embed ({N}x{D}, 4 bilinear taps)": (
             lambda: lib.qvl_pos_embed(s_, BF, tower._w.pos_table, tens["tap_idx"].data_ptr(),
                                       tens["tap_w"].data_ptr(), yk.data_ptr(), N, D),
             N * D * 2 + N * 4 * 8 + spec.num_position_embeddings * D * 2, "hbm", 1),
-        "cast pixels f32->bf16 (18432x1536)": (
-            lambda: (lambda i: lib.qvl_cast(s_, BF, px_c[i].data_ptr(), px_b[i].data_ptr(), N * spec.patch_volume))(
-                rotate("cast")), N * spec.patch_volume * 6.0, "hbm", 1),
-        # the steps either side of the tower (not in the step time): on-device patchify of the 8
-        # uint8 frames, and the decoder-side injection / deepstack add of the 4608 vision rows
-        "patchify (8 x 768x768x3 uint8 -> 18432x1536 f32)": (
-            lambda: lib.qvl_patchify(s_, cp.QVL_DTYPE_F32, frames_u8.data_ptr(), 8, 768, 768, 3, 16, 2, 2,
-                                     px_p[rotate("patchify")].data_ptr(), spec.patch_volume),
-            8 * 768 * 768 * 3 + N * spec.patch_volume * 4.0, "hbm", 0),
-        "inject vision rows (4608 x 2048 bf16 into 5120 x 2048)": (
+        f"cast pixels f32->bf16 ({N}x{PV})": (
+            lambda: (lambda i: lib.qvl_cast(s_, BF, px_c[i].data_ptr(), px_b[i].data_ptr(), N * PV))(
+                rotate("cast")), N * PV * 6.0, "hbm", 1),
+        # the steps either side of the tower (not in the step time): on-device patchify of the
+        # uint8 frames, and the decoder-side injection / deepstack add of the vision rows
+        f"patchify ({n_frames} x {fh}x{fw}x3 uint8 -> {N}x{PV} f32)": (
+            lambda: lib.qvl_patchify(s_, cp.QVL_DTYPE_F32, frames_u8.data_ptr(), n_frames, fh, fw, 3, 16, 2, 2,
+                                     px_p[rotate("patchify")].data_ptr(), PV),
+            n_frames * fh * fw * 3 + N * PV * 4.0, "hbm", 0),
+        f"inject vision rows ({V} x {Dtxt} bf16 into {S_txt} x {Dtxt})": (
             lambda: lib.qvl_scatter_vision_rows(s_, cp.QVL_SCATTER_SET, BF, hid.data_ptr(), 1, S_txt, Dtxt, BF,
                                                 vrows.data_ptr(), 0, V, vpos.data_ptr(), vcnt.data_ptr()),
             2.0 * V * Dtxt * 2, "hbm", 0),
-        "deepstack add (4608 x 2048 bf16)": (
+        f"deepstack add ({V} x {Dtxt} bf16)": (
             lambda: lib.qvl_scatter_vision_rows(s_, cp.QVL_SCATTER_ADD, BF, hid.data_ptr(), 1, S_txt, Dtxt, BF,
                                                 vrows.data_ptr(), 0, V, vpos.data_ptr(), vcnt.data_ptr()),
             3.0 * V * Dtxt * 2, "hbm", 0),
@@ -353,15 +377,13 @@ def main():
                             "bytes_per_launch": work}
     dom = max((k for k in kstats if kstats[k]["bound"] == "mfma"), key=lambda k: kstats[k]["ms_per_step"])
     dk = kstats[dom]
-    traffic = hbm_traffic(dom)
+    traffic = hbm_traffic(dom) if args.config == 2 else None
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "patches/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights N(0,0.02), patches N(0,1))",
-        "config": {"workload": "BASELINE config 2: 2B vision tower, 8 x 768x768 images, grid (1,48,48) each, "
-                               "18432 patches in 8 cu_seqlens segments, deepstack after blocks 5/11/17",
-                   "global_batch": 8, "patches": N, "parallelism": "single GPU"},
+        "config": {"workload": workload, "global_batch": len(grid_list), "patches": N, "parallelism": "single GPU"},
         "mfma_frac_step": round(step_tflops / PEAK_BF16_TFLOPS, 4),
         "step_tflops": round(step_tflops, 1),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": dk["tflops"], "peak": PEAK_BF16_TFLOPS,
@@ -370,7 +392,10 @@ def main():
         "kernels": kstats,
         "wall_s_timed": round(wall, 3),
     }
-    if not args.no_cpu:
+    if args.config != 2:
+        out["metric"] = METRIC.replace("2B tower", "2B tower" if shape == "2b" else "8B tower")
+        out["secondary"] = f"BASELINE config {args.config}: a parity config, not the headline bench line"
+    if not args.no_cpu and args.config == 2:
         one = np.array([(1, 48, 48)], np.int32)
         out["cpu_baseline"] = cpu_baseline(params, px_host[:2304], one, compiled=not args.no_cpu_compiled)
         out["gpu_over_cpu"] = round(value / out["cpu_baseline"]["value"], 1)

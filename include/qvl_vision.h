@@ -171,12 +171,17 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const voi
                          void* d_workspace, size_t workspace_bytes);
 
 /* Fused qkv Dense + rotary (model.py:570-582): one GEMM x[N, D] . Wqkv[3D, D]^T + b whose
- * epilogue applies the 2D rotary to q and k with `d_cos_sin` and writes the head-major operands
- * of qvl_attention_headmajor: q (scaled by head_dim^-0.5 * log2(e)) and k as [H][Np][64],
- * v transposed as [H][64][Np], Np = n_tokens rounded up to 64 (rows [n_tokens, Np) zeroed).
- * head_dim must be 64 and D a multiple of 128; bf16 only (the fp32 tower runs qvl_dense and
- * qvl_vision_attention). The optional workspace (qvl_dense_workspace_size bytes, may be NULL)
- * enables tail split-K as in qvl_dense_ws. */
+ * epilogue applies the 2D rotary to q and k with `d_cos_sin` (qvl_rotary_table of this head_dim)
+ * and writes the head-major operands of qvl_attention_headmajor, Np = n_tokens rounded up to 64,
+ * rows / positions [n_tokens, Np) zeroed:
+ *   head_dim 64 (D a multiple of 128): q (scaled by head_dim^-0.5 * log2(e)) and k as
+ *     [H][Np][64], v transposed as [H][64][Np] (keys at their vt_pos positions);
+ *   head_dim 72 (num_heads a multiple of 4): q (scaled) and k as [H][Np][88] with dims 72..87
+ *     zero, v transposed as [H][72][Np].
+ * Every rounding is the reference's (bf16 Dense output, bias add, each rotary product and sum).
+ * bf16 only (the fp32 tower runs qvl_dense and qvl_vision_attention). The optional workspace
+ * (qvl_dense_workspace_size bytes, may be NULL) enables tail split-K for head_dim 64 as in
+ * qvl_dense_ws. */
 int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
                          const float* d_bias, const void* d_cos_sin, void* d_q, void* d_k, void* d_vt,
                          int64_t n_tokens, int64_t hidden, int32_t num_heads,

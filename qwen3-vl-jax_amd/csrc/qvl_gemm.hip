@@ -226,12 +226,12 @@ __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int 
   }
 #pragma unroll
   for (int e = 0; e < 4; e += 2) { round_bf16_pair(lo[e], lo[e + 1]); round_bf16_pair(hi[e], hi[e + 1]); }
-  const f32x4* csr = reinterpret_cast<const f32x4*>(p.cs + (int64_t)m * 32 + d);
+  const f32x4* csr = reinterpret_cast<const f32x4*>(p.cs + (int64_t)m * p.cs_half + d);
   const f32x4 c01 = csr[0], c23 = csr[1];       // (cos, sin) of dims d, d+1 | d+2, d+3
   const float cs_c[4] = {c01[0], c01[2], c23[0], c23[2]};
   const float cs_s[4] = {c01[1], c01[3], c23[1], c23[3]};
   // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582):
-  // dims < 32: lo*cos - hi*sin; dims + 32: hi*cos + lo*sin.
+  // dims < hd/2: lo*cos - hi*sin; dims + hd/2: hi*cos + lo*sin.
   float lc[4], hs[4], hc[4], ls[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) { lc[e] = lo[e] * cs_c[e]; hs[e] = hi[e] * cs_s[e]; hc[e] = hi[e] * cs_c[e]; ls[e] = lo[e] * cs_s[e]; }
@@ -340,6 +340,90 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
         *reinterpret_cast<u32x4*>(row + 2 * (int64_t)p.Np) = o2;
         *reinterpret_cast<u32x4*>(row + 3 * (int64_t)p.Np) = o3;
       }
+    }
+  }
+}
+
+// Rotary epilogue of the head_dim-72 qkv GEMM (tile 256 x 288 = 4 whole heads of one of q, k, v):
+// the waves stage bf16(acc) in the (free) LDS as a row-major 256 x 288 tile (row stride kR72),
+// then the workgroup walks it. q / k: items (token, head, 4 rotary pairs), each the 4 dims d..d+3
+// and d+36..d+39 through rope_values (bias, the reference's roundings, the q pre-scale), stored
+// to rows of 88 dims [H][Np][88] whose dims 72..87 are zero. v: items (head, 2 dims, 8 key
+// positions), 8 LDS reads of one token's pair each, stored as two 16-byte runs of V^T [H][72][Np]
+// at the vt_pos positions. Tokens in [M, Np) get zeros.
+constexpr int kR72 = 296;   // LDS row stride (elements) of the staged tile: 592 bytes, 16-byte multiple
+
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void gemm_epilogue_rope72_lds(const GemmParams& p,
+                                                         f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
+                                                         int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem) {
+  using S = GemmShape<BM, BN, WM, WN>;
+  static_assert(BN == 4 * 72 && BM % 8 == 0, "four 72-dim heads per tile");
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int a = 0; a < S::NB; ++a)
+#pragma unroll
+    for (int b = 0; b < S::MB; ++b)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = wm * S::TM + b * 32 + l32;
+        const int c = wn * S::TN + a * 32 + 8 * g + 4 * hh;
+        *reinterpret_cast<u32x2*>(smem + r * kR72 + c) = u32x2{pack_bf16x2(acc[a][b][4 * g], acc[a][b][4 * g + 1]),
+                                                                 pack_bf16x2(acc[a][b][4 * g + 2], acc[a][b][4 * g + 3])};
+      }
+  __syncthreads();
+  const int which = n0 / p.D;                    // tiles never straddle q | k | v (D % 288 == 0)
+  const int head0 = (n0 % p.D) / 72;
+  if (which < 2) {
+    bf16* dst = which == 0 ? p.q : p.k;
+    constexpr int ITEMS = BM * 4 * 9;            // (token, head, group of 4 rotary pairs)
+    for (int it = tid; it < ITEMS; it += S::THREADS) {
+      const int r = it / 36, rem = it % 36, h = rem / 9, d = (rem % 9) * 4;
+      const int m = m0 + r;
+      if (m >= p.Np) continue;
+      const int n = n0 + h * 72 + d;
+      const bf16* src = smem + r * kR72 + h * 72 + d;
+      const u32x2 lr = *reinterpret_cast<const u32x2*>(src);
+      const u32x2 hr = *reinterpret_cast<const u32x2*>(src + 36);
+      const float lo[4] = {bf16_lo(lr.x), bf16_hi(lr.x), bf16_lo(lr.y), bf16_hi(lr.y)};
+      const float hi[4] = {bf16_lo(hr.x), bf16_hi(hr.x), bf16_lo(hr.y), bf16_hi(hr.y)};
+      const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
+      const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 36);
+      u32x2 o1, o2;
+      rope_values(p, which, m, d, blo, bhi, lo, hi, o1, o2);
+      bf16* row = dst + ((int64_t)(head0 + h) * p.Np + m) * 88;
+      *reinterpret_cast<u32x2*>(row + d) = o1;
+      *reinterpret_cast<u32x2*>(row + 36 + d) = o2;
+    }
+    for (int it = tid; it < BM * 8; it += S::THREADS) {     // dims 72..87: two 16-byte zero runs per row
+      const int r = it / 8, h = (it / 2) % 4, half = it % 2;
+      const int m = m0 + r;
+      if (m < p.Np)
+        *reinterpret_cast<u32x4*>(dst + ((int64_t)(head0 + h) * p.Np + m) * 88 + 72 + 8 * half) = u32x4{0u, 0u, 0u, 0u};
+    }
+  } else {
+    constexpr int PCH = BM / 8;                  // 8-position chunks of the tile's V^T rows
+    constexpr int ITEMS = 4 * 36 * PCH;          // (head, dim pair, position chunk)
+    for (int it = tid; it < ITEMS; it += S::THREADS) {
+      const int pc = it % PCH, rest = it / PCH, dp = rest % 36, h = rest / 36;
+      const int d = 2 * dp, P = m0 + pc * 8;
+      if (P >= p.Np) continue;
+      const int n = n0 + h * 72 + d;
+      const float b0 = p.bias[n], b1 = p.bias[n + 1];
+      float v0[8], v1[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int m = vt_pos(P + e);             // the token stored at position P + e
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(smem + (m - m0) * kR72 + h * 72 + d);
+        const bool live = m < p.M;
+        v0[e] = live ? bf16_lo(w) + b0 : 0.f;
+        v1[e] = live ? bf16_hi(w) + b1 : 0.f;
+      }
+      bf16* row = p.vt + ((int64_t)(head0 + h) * 72 + d) * p.Np + P;
+      *reinterpret_cast<u32x4*>(row) = u32x4{pack_bf16x2(v0[0], v0[1]), pack_bf16x2(v0[2], v0[3]),
+                                             pack_bf16x2(v0[4], v0[5]), pack_bf16x2(v0[6], v0[7])};
+      *reinterpret_cast<u32x4*>(row + p.Np) = u32x4{pack_bf16x2(v1[0], v1[1]), pack_bf16x2(v1[2], v1[3]),
+                                                    pack_bf16x2(v1[4], v1[5]), pack_bf16x2(v1[6], v1[7])};
     }
   }
 }
@@ -487,6 +571,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   if constexpr (EPI == kEpiQkvRope) {
     __syncthreads();                    // every wave is done with the last stage
     gemm_epilogue_rope_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, wave, smem);
+  } else if constexpr (EPI == kEpiQkvRope72) {
+    gemm_epilogue_rope72_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, tid, smem);
   } else {
     gemm_epilogue_lds<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane, tid, smem);
   }
@@ -594,7 +680,7 @@ static int gemm_group_n(int tiles_n) {
 template <int BM, int BN, int WM, int WN, int EPI>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
-  const size_t lds = std::max(2 * S::LDS_ELEMS, BM * BN) * sizeof(bf16);
+  const size_t lds = std::max(2 * S::LDS_ELEMS, EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN) * sizeof(bf16);
   // once per instantiation (a C++ function-local static: initialised exactly once, thread-safe)
   static const hipError_t attr_rc = hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -658,8 +744,17 @@ int gemm_set_plan(int tile, int split_mode, int group_n) {
   return QVL_OK;
 }
 
+// head_dim-72 qkv GEMM: 256 x 288 tiles (4 heads each, 12 waves of 64 x 96), no tail split.
+constexpr double kRate256x288 = 1.50e6;
+
+static int dispatch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
+  const GemmPlan g = plan_gemm<256, 288>(p, gemm_device_cus(), kRate256x288, -1);
+  return launch_gemm<256, 288, 4, 3, kEpiQkvRope72>(p, g, stream);
+}
+
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream) {
   switch (epi) {
+    case kEpiQkvRope72: return dispatch_qkv_rope72(p, stream);
     case kEpiBias: return dispatch_gemm<kEpiBias>(p, stream);
     case kEpiBiasGelu: return dispatch_gemm<kEpiBiasGelu>(p, stream);
     case kEpiBiasResidual: return dispatch_gemm<kEpiBiasResidual>(p, stream);

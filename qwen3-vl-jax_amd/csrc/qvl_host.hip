@@ -213,8 +213,11 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda
                          const void* cs, void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H,
                          void* ws, size_t ws_bytes) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: dtype %d", dtype);
-  if (H <= 0 || hidden != (int64_t)H * 64) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64");
-  if (hidden % 128) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: hidden %% 128 != 0");
+  if (H <= 0 || (hidden != (int64_t)H * 64 && hidden != (int64_t)H * 72))
+    return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64 or 72");
+  const int hd = (int)(hidden / H);
+  if (hd == 64 && hidden % 128) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: hidden %% 128 != 0");
+  if (hd == 72 && H % 4) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim 72 needs num_heads %% 4 == 0");
   if (n_tokens < 0 || lda < hidden || lda % 8) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: n_tokens / lda");
   if (n_tokens == 0) return QVL_OK;
   if (!x || !w || !bias || !cs || !q || !k || !vt) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
@@ -227,10 +230,11 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda
   p.M = (int)n_tokens; p.N = (int)(3 * hidden); p.K = (int)hidden;
   p.q = (bf16*)q; p.k = (bf16*)k; p.vt = (bf16*)vt; p.cs = (const f32x2*)cs;
   p.Np = (int)attn_np(n_tokens); p.D = (int)hidden;
-  p.qscale = (1.0f / sqrtf(64.0f)) * kLog2e;
+  p.cs_half = hd / 2;
+  p.qscale = (1.0f / sqrtf((float)hd)) * kLog2e;
   if (ws && !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: workspace alignment");
   p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
-  return gemm_bf16(p, kEpiQkvRope, (hipStream_t)stream);
+  return gemm_bf16(p, hd == 64 ? kEpiQkvRope : kEpiQkvRope72, (hipStream_t)stream);
 }
 
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
@@ -301,6 +305,12 @@ struct TowerLayout {
 // worklist_split: at most one per workgroup slot, 4 per CU).
 static int64_t attn_split_slots_bound() { return 4 * (int64_t)gemm_device_cus(); }
 
+// Whether the tower's qkv Dense runs qvl_dense_qkv_rotary (rotary + head-major operands in its
+// epilogue): bf16 with head_dim 64, or head_dim 72 with whole 4-head tiles.
+static bool fused_qkv_rotary(int dtype, int hd, int H) {
+  return dtype == QVL_DTYPE_BF16 && (hd == 64 || (hd == 72 && H % 4 == 0));
+}
+
 static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   if (!c) return set_error(QVL_ERR_INVALID_ARG, "config is NULL");
   if (c->dtype != QVL_DTYPE_BF16 && c->dtype != QVL_DTYPE_F32)
@@ -320,7 +330,7 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   L->esz = dtype_size(c->dtype);
   L->N = N; L->Np = attn_np(N); L->D = c->hidden_size; L->I_pad = round_up(c->intermediate_size, 64);
   L->PV = c->patch_volume; L->hd = hd; L->H = c->num_heads; L->hdp = hdp; L->vrows = vrows;
-  const bool fused_qkv = c->dtype == QVL_DTYPE_BF16 && hd == 64;
+  const bool fused_qkv = fused_qkv_rotary(c->dtype, (int)hd, c->num_heads);
   // h hosts the bf16 pixels, the MLP hidden, the merger hidden and (unless the qkv GEMM writes
   // head-major operands itself) the qkv output.
   int64_t hcols = std::max<int64_t>({L->I_pad, L->PV, (int64_t)c->hidden_size});
@@ -436,7 +446,7 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     const qvl_block_weights& B = W->blocks[i];
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
     QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
-    if (!f32 && L.hd == 64) {
+    if (fused_qkv_rotary(dt, (int)L.hd, (int)L.H)) {
       // qkv Dense with rotary + head-major relayout fused into its epilogue.
       QVL_TRY_RC(qvl_dense_qkv_rotary(st, dt, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
     } else {

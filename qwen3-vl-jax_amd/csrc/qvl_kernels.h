@@ -7,7 +7,7 @@
 
 namespace qvl {
 
-enum : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiBiasResidual = 2, kEpiQkvRope = 3 };
+enum : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiBiasResidual = 2, kEpiQkvRope = 3, kEpiQkvRope72 = 4 };
 
 struct GemmParams {
   const bf16* x; int64_t lda;
@@ -17,8 +17,10 @@ struct GemmParams {
   bf16* y; int64_t ldc;
   int M, N, K;
   // kEpiQkvRope: q/k written [H][Np][64] (rotated; q scaled by qscale), v written [H][64][Np].
+  // kEpiQkvRope72: q/k written [H][Np][88] (dims 72..87 zero), v written [H][72][Np].
   bf16* q; bf16* k; bf16* vt;
-  const f32x2* cs;               // [M, 32] (cos, sin)
+  const f32x2* cs;               // [M, cs_half] (cos, sin), cs_half = head_dim / 2
+  int cs_half;
   int Np, D;
   float qscale;
   // Tail split-K: fp32 partials workspace (NULL: no splitting) and its capacity in floats; the

@@ -647,13 +647,15 @@ class Qwen3VisionTransformer:
         if "qb" in ctx:
             return ctx
         N, H, hd = ctx["N"], ctx["H"], ctx["hd"]
-        if self.qdtype != capi.QVL_DTYPE_BF16 or hd != 64:
-            raise NotImplementedError("block_fused runs the bf16 head_dim-64 fused qkv+rotary entry")
+        if self.qdtype != capi.QVL_DTYPE_BF16 or not (hd == 64 or (hd == 72 and H % 4 == 0)):
+            raise NotImplementedError("block_fused runs the bf16 fused qkv+rotary entry (head_dim 64, or 72 "
+                                      "with num_heads % 4 == 0)")
         Np = -(-N // 64) * 64
+        hdp = 64 if hd == 64 else 88            # Q/K row length of the attention kernels
         dev = dict(device=self.device)
-        ctx["qb"] = torch.empty((H, Np, 64), dtype=torch.bfloat16, **dev)
+        ctx["qb"] = torch.empty((H, Np, hdp), dtype=torch.bfloat16, **dev)
         ctx["kb"] = torch.empty_like(ctx["qb"])
-        ctx["vb"] = torch.empty_like(ctx["qb"])
+        ctx["vb"] = torch.empty((H, hd, Np), dtype=torch.bfloat16, **dev)
         nb = C.c_size_t()
         capi.check(self._lib.qvl_dense_workspace_size(C.byref(nb)), "qvl_dense_workspace_size")
         ctx["gws"] = torch.empty(max(nb.value, 256), dtype=torch.uint8, **dev)
@@ -669,7 +671,7 @@ class Qwen3VisionTransformer:
 
     def block_fused(self, i: int, x, ctx) -> None:
         """VisionBlock i (model.py:627-630) in place on x [N, D] through exactly the entries the
-        whole-tower call runs for a bf16 head_dim-64 tower: LayerNorm, the fused qkv Dense +
+        whole-tower call runs for a bf16 tower (head_dim 64 or 72): LayerNorm, the fused qkv Dense +
         rotary (qvl_dense_qkv_rotary, head-major Q/K/V^T), attention on the tower's work list
         (qvl_attention_headmajor_split when the tower builds a split list, else
         qvl_attention_headmajor), proj + residual, LayerNorm, fc1 + GELU, fc2 + residual, the

@@ -414,17 +414,21 @@ def vt_positions(n):
     return (n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3)
 
 
-@pytest.mark.parametrize("grids", [[(1, 48, 48)], [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
-def test_qkv_rotary_matches_oracle_rotary(pkg, lib, grids):
+@pytest.mark.parametrize("hd,grids", [(64, [(1, 48, 48)]), (64, [(1, 16, 16), (2, 10, 14), (1, 6, 8)]),
+                                      (72, [(1, 84, 84)]), (72, [(1, 16, 16), (2, 10, 14), (1, 6, 8)])])
+def test_qkv_rotary_matches_oracle_rotary(pkg, lib, hd, grids):
     """The fused qkv Dense + rotary epilogue (qvl_dense_qkv_rotary, the entry the tower runs)
     against the oracle's bf16 apply_rotary (model.py:579-582: each product and the sum rounded to
     bf16) applied to the GPU's own qkv Dense output and cos/sin table: bit-exact once the layout is
-    undone (Q = bf16(q_rot * head_dim^-0.5 * log2 e) as [H][Np][64], K = k_rot, V^T[h][d][vt_pos(n)]
-    = v[n][h][d]), padding rows zero. The Dense output itself is within one bf16 ulp of the oracle's
-    Dense on the same operands for every element (equal for >= 99 %)."""
+    undone (Q = bf16(q_rot * head_dim^-0.5 * log2 e) as [H][Np][hdp], K = k_rot, V^T[h][d][vt_pos(n)]
+    = v[n][h][d]), padding rows zero; head_dim 64 (hdp 64) and head_dim 72 (the 8B tower: hdp 88,
+    dims 72..87 zero). The Dense output itself is within one bf16 ulp of the oracle's Dense on the
+    same operands for every element (equal for >= 99 %)."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
-    N, D, H = m.n_tokens, 1024, 16
+    H = 16
+    N, D = m.n_tokens, H * hd
+    hdp, half = (64 if hd == 64 else 88), hd // 2
     Np = -(-N // 64) * 64
     rng = np.random.default_rng(N)
     x_h = vt.bf16_round(rng.standard_normal((N, D)).astype(np.float32))
@@ -434,14 +438,15 @@ def test_qkv_rotary_matches_oracle_rotary(pkg, lib, grids):
     w = pack(lib, cp, w_h)
     bias = torch.from_numpy(b_h).to(DEV)
     pos = torch.from_numpy(m.pos_hw).to(DEV)
-    cs = torch.empty((N, 32, 2), dtype=torch.float32, device=DEV)
-    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, 64, 10000.0, cs.data_ptr()))
+    cs = torch.empty((N, half, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
     nb = C.c_size_t()
     cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
     qkv = torch.empty((N, 3 * D), dtype=torch.bfloat16, device=DEV)
-    q = torch.full((H, Np, 64), 3.0, dtype=torch.bfloat16, device=DEV)
-    k, vtm = q.clone(), q.clone()
+    q = torch.full((H, Np, hdp), 3.0, dtype=torch.bfloat16, device=DEV)   # every element must be written
+    k = q.clone()
+    vtm = torch.full((H, hd, Np), 3.0, dtype=torch.bfloat16, device=DEV)
     try:
         cp.check(lib.qvl_set_gemm_plan(0, -1, 0))          # no tail split: one K order for both entries
         cp.check(lib.qvl_dense(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS, x.data_ptr(), D, w.data_ptr(),
@@ -465,19 +470,20 @@ def test_qkv_rotary_matches_oracle_rotary(pkg, lib, grids):
     cos = np.concatenate([c_h[..., 0], c_h[..., 0]], axis=1)
     sin = np.concatenate([c_h[..., 1], c_h[..., 1]], axis=1)
     P = vt._P("bf16")
-    qr = vt.apply_rotary(qkv_h[:, :D].reshape(N, H, 64), cos, sin, P)
-    kr = vt.apply_rotary(qkv_h[:, D:2 * D].reshape(N, H, 64), cos, sin, P)
-    vv = qkv_h[:, 2 * D:].reshape(N, H, 64)
-    qscale = np.float32(np.float32(1.0) / np.float32(8.0)) * np.float32(1.4426950408889634)
+    qr = vt.apply_rotary(qkv_h[:, :D].reshape(N, H, hd), cos, sin, P)
+    kr = vt.apply_rotary(qkv_h[:, D:2 * D].reshape(N, H, hd), cos, sin, P)
+    vv = qkv_h[:, 2 * D:].reshape(N, H, hd)
+    qscale = np.float32(np.float32(1.0) / np.sqrt(np.float32(hd))) * np.float32(1.4426950408889634)
     want_q = vt.bf16_round(qr * qscale).transpose(1, 0, 2)
-    got_q, got_k, got_vt = to_np(q), to_np(k), to_np(vtm).reshape(H, 64, Np)      # V^T is [H][64][Np]
-    np.testing.assert_array_equal(got_q[:, :N], want_q)
-    np.testing.assert_array_equal(got_k[:, :N], kr.transpose(1, 0, 2))
+    got_q, got_k, got_vt = to_np(q), to_np(k), to_np(vtm)
+    np.testing.assert_array_equal(got_q[:, :N, :hd], want_q)
+    np.testing.assert_array_equal(got_k[:, :N, :hd], kr.transpose(1, 0, 2))
     np.testing.assert_array_equal(got_vt[:, :, vt_positions(np.arange(N))], vv.transpose(1, 2, 0))
     assert not got_q[:, N:].any() and not got_k[:, N:].any()
+    assert not got_q[:, :, hd:].any() and not got_k[:, :, hd:].any()
     assert not got_vt[:, :, vt_positions(np.arange(N, Np))].any()
     # and equal to the oracle's rotary on its own Dense wherever the Dense values agree
-    qr_ref = vt.apply_rotary(ref_qkv[:, :D].reshape(N, H, 64), cos, sin, P).transpose(1, 0, 2)
-    same = (qkv_h[:, :D] == ref_qkv[:, :D]).reshape(N, H, 64).transpose(1, 0, 2)
-    same &= same[..., list(range(32, 64)) + list(range(32))]        # the rotary pair as well
-    np.testing.assert_array_equal(got_q[:, :N][same], vt.bf16_round(qr_ref * qscale)[same])
+    qr_ref = vt.apply_rotary(ref_qkv[:, :D].reshape(N, H, hd), cos, sin, P).transpose(1, 0, 2)
+    same = (qkv_h[:, :D] == ref_qkv[:, :D]).reshape(N, H, hd).transpose(1, 0, 2)
+    same &= same[..., list(range(half, hd)) + list(range(half))]    # the rotary pair as well
+    np.testing.assert_array_equal(got_q[:, :N, :hd][same], vt.bf16_round(qr_ref * qscale)[same])

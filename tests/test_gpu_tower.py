@@ -85,7 +85,7 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
         x = torch.from_numpy(np.ascontiguousarray(xin)).to("cuda:0").to(torch.bfloat16)
         tower.block_staged(i, x, ctx)
         assert rel_l2(to_np(x), ref.layers[i]) <= TOL, f"block {i}"
-        if spec.head_dim == 64:    # the entries the whole-tower call runs (fused qkv + rotary, split list)
+        if True:                   # the entries the whole-tower call runs (fused qkv + rotary, split list)
             x = torch.from_numpy(np.ascontiguousarray(xin)).to("cuda:0").to(torch.bfloat16)
             tower.block_fused(i, x, ctx)
             assert rel_l2(to_np(x), ref.layers[i]) <= TOL, f"fused block {i}"
