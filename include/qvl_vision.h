@@ -187,6 +187,21 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* d_x, int64_t l
                          int64_t n_tokens, int64_t hidden, int32_t num_heads,
                          void* d_workspace, size_t workspace_bytes);
 
+/* Per-position rotary table for qvl_dense_qkv_rotary_pos: table[p][j] = bf16(cos) | bf16(sin) << 16
+ * of p * inv_freq[j] for p < n_positions, j < head_dim/4 (uint32 [n_positions][head_dim/4]): the
+ * (cos, sin) qvl_rotary_table gives a token at rotary id p, bit for bit (model.py:540-546,
+ * 694-698, 821-823 with the angle's two axes sharing one table). */
+int qvl_rotary_pos_table(void* stream, int32_t head_dim, float theta, int32_t n_positions, uint32_t* d_table);
+
+/* qvl_dense_qkv_rotary with (cos, sin) looked up by each token's rotary (h, w) ids (`d_pos_hw`
+ * [n_tokens][2] of qvl_vision_metadata, every id < n_positions) in a qvl_rotary_pos_table table,
+ * which the kernel keeps in LDS instead of reading a per-token table: same outputs bit for bit.
+ * n_positions * head_dim/4 * 4 bytes must fit 16384 (head_dim 64) or 12288 (head_dim 72) bytes. */
+int qvl_dense_qkv_rotary_pos(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
+                             const float* d_bias, const int32_t* d_pos_hw, const uint32_t* d_table,
+                             int32_t n_positions, void* d_q, void* d_k, void* d_vt, int64_t n_tokens,
+                             int64_t hidden, int32_t num_heads, void* d_workspace, size_t workspace_bytes);
+
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
  * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][88] (dims 72..87 zero) and
@@ -307,6 +322,9 @@ typedef struct qvl_vision_metadata_dev {
   int64_t n_split_tiles;
   int64_t n_split_whole;
   const int32_t* split_tiles;     /* [n_split_tiles, 4]                                      */
+  /* optional: 1 + the largest rotary id in pos_hw (0 = unknown); lets the bf16 tower look
+   * (cos, sin) up per position (qvl_dense_qkv_rotary_pos) */
+  int64_t n_positions;
 } qvl_vision_metadata_dev;
 
 int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tokens, size_t* bytes);

@@ -53,7 +53,8 @@ class VisionWeights(C.Structure):
 class VisionMetadataDev(C.Structure):
     _fields_ = [("n_tokens", _i64), ("n_tiles", _i64), ("pos_hw", _p), ("tap_idx", _p), ("tap_w", _p),
                 ("tiles", _p), ("n_window_tiles", _i64), ("window_tiles", _p), ("window_index", _p),
-                ("window_reverse", _p), ("n_split_tiles", _i64), ("n_split_whole", _i64), ("split_tiles", _p)]
+                ("window_reverse", _p), ("n_split_tiles", _i64), ("n_split_whole", _i64), ("split_tiles", _p),
+                ("n_positions", _i64)]
 
 
 # name -> (restype, argtypes); every function in include/qvl_vision.h
@@ -80,6 +81,9 @@ SIGNATURES = {
     "qvl_vision_attention": (C.c_int, [_p, _i32, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _i32,
                                        _p, _sz]),
     "qvl_dense_qkv_rotary": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _sz]),
+    "qvl_rotary_pos_table": (C.c_int, [_p, _i32, _f32, _i32, _p]),
+    "qvl_dense_qkv_rotary_pos": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i32,
+                                           _p, _sz]),
     "qvl_attention_headmajor": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _p, _i64]),
     "qvl_attention_split_workspace_size": (C.c_int, [_i32, _i64, _i64, C.POINTER(_sz)]),
     "qvl_attention_headmajor_split": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64,

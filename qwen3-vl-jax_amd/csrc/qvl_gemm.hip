@@ -126,7 +126,49 @@ __device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n,
 
 __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int d, const f32x4& blo,
                                             const f32x4& bhi, const float (&lo_acc)[4], const float (&hi_acc)[4],
-                                            u32x2& o1, u32x2& o2);
+                                            const f32x4& c01, const f32x4& c23, u32x2& o1, u32x2& o2);
+
+// (cos, sin) of the 4 dims d..d+3 (< head_dim/2) of token m as (c_d, s_d, c_d+1, s_d+1) |
+// (c_d+2, s_d+2, c_d+3, s_d+3): from the per-token table p.cs, or from the per-position table
+// p.rtab (global memory) at the token's (h, w) ids. Tokens past M get anything (their outputs are
+// zeros).
+__device__ __forceinline__ void unpack_cs4(const uint32_t (&w)[4], f32x4& c01, f32x4& c23) {
+  c01 = f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+  c23 = f32x4{bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3])};
+}
+
+template <typename T>
+__device__ __forceinline__ void rope_cs_table(const T* tab, int q4, int ph, int pw, int d, f32x4& c01, f32x4& c23) {
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = d + e;
+    w[e] = j < q4 ? tab[ph * q4 + j] : tab[pw * q4 + j - q4];
+  }
+  unpack_cs4(w, c01, c23);
+}
+
+__device__ __forceinline__ void token_pos(const GemmParams& p, int m, int& ph, int& pw) {
+  ph = 0;
+  pw = 0;
+  if (m < p.M) {
+    ph = min(max(p.pos_hw[2 * m], 0), p.rtab_pos - 1);     // clamped: table lookups stay in bounds
+    pw = min(max(p.pos_hw[2 * m + 1], 0), p.rtab_pos - 1);
+  }
+}
+
+__device__ __forceinline__ void rope_cs_global(const GemmParams& p, int m, int d, f32x4& c01, f32x4& c23) {
+  if (p.rtab) {
+    int ph, pw;
+    token_pos(p, m, ph, pw);
+    rope_cs_table(p.rtab, p.cs_half / 2, ph, pw, d, c01, c23);
+    return;
+  }
+  if (m >= p.M) { c01 = f32x4{}; c23 = f32x4{}; return; }
+  const f32x4* csr = reinterpret_cast<const f32x4*>(p.cs + (int64_t)m * p.cs_half + d);
+  c01 = csr[0];
+  c23 = csr[1];
+}
 
 // Rotary epilogue of the qkv GEMM for one pair of quads (the split-K reduction's path): features
 // n..n+3 (dims d..d+3 < 32 of a head) and n+32..n+35 of token m, stored straight to q/k
@@ -139,7 +181,9 @@ __device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n,
   const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
   const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
   u32x2 o1, o2;
-  rope_values(p, which, m, d, blo, bhi, lo_acc, hi_acc, o1, o2);
+  f32x4 c01 = {}, c23 = {};
+  if (which < 2) rope_cs_global(p, m, d, c01, c23);
+  rope_values(p, which, m, d, blo, bhi, lo_acc, hi_acc, c01, c23, o1, o2);
   if (which == 2) {
     bf16* vt = p.vt + (int64_t)head * 64 * p.Np + vt_pos(m);
     const uint32_t w[4] = {o1.x, o1.y, o2.x, o2.y};
@@ -207,7 +251,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
 // packed conversion.
 __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int d, const f32x4& blo,
                                             const f32x4& bhi, const float (&lo_acc)[4], const float (&hi_acc)[4],
-                                            u32x2& o1, u32x2& o2) {
+                                            const f32x4& c01, const f32x4& c23, u32x2& o1, u32x2& o2) {
   if (m >= p.M) {
     o1 = u32x2{0u, 0u};
     o2 = u32x2{0u, 0u};
@@ -226,8 +270,6 @@ __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int 
   }
 #pragma unroll
   for (int e = 0; e < 4; e += 2) { round_bf16_pair(lo[e], lo[e + 1]); round_bf16_pair(hi[e], hi[e + 1]); }
-  const f32x4* csr = reinterpret_cast<const f32x4*>(p.cs + (int64_t)m * p.cs_half + d);
-  const f32x4 c01 = csr[0], c23 = csr[1];       // (cos, sin) of dims d, d+1 | d+2, d+3
   const float cs_c[4] = {c01[0], c01[2], c23[0], c23[2]};
   const float cs_s[4] = {c01[1], c01[3], c23[1], c23[3]};
   // x*cos + rotate_half(x)*sin with each product and the sum rounded (model.py:579-582):
@@ -262,7 +304,8 @@ __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int 
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
                                                        f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
-                                                       int m0, int n0, int wm, int wn, int lane, int wave, bf16* smem) {
+                                                       int m0, int n0, int wm, int wn, int lane, int wave, bf16* smem,
+                                                       const uint32_t* ltab) {
   using S = GemmShape<BM, BN, WM, WN>;
   constexpr int TM = S::TM, TN = S::TN, CPR = TN / 8, HPW = TN / 64;
   static_assert(TN % 64 == 0 && TM % 16 == 0, "the rotary epilogue needs whole heads and 16-token groups");
@@ -275,6 +318,12 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
   const int which = nw / p.D;                    // 0 = q, 1 = k, 2 = v
   const int head0 = (nw % p.D) / 64;
   const int base = m0 + wm * TM;                 // first token of the wave's block
+  // rotary (h, w) ids of the lane's tokens, for the LDS position table
+  int ph[S::MB], pw[S::MB];
+  if (ltab && which < 2) {
+#pragma unroll
+    for (int b = 0; b < S::MB; ++b) token_pos(p, base + b * 32 + l32, ph[b], pw[b]);
+  }
 #pragma unroll
   for (int h2 = 0; h2 < HPW; ++h2)
 #pragma unroll
@@ -288,8 +337,20 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
         float lo[4], hi[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
+        f32x4 c01 = {}, c23 = {};
+        if (which < 2) {
+          if (ltab) {
+            // dims d..d+3 lie in one half (d % 4 == 0, head_dim / 4 = 16): one 16-byte LDS read
+            uint32_t w[4];
+            const u32x4 q = *reinterpret_cast<const u32x4*>(ltab + (d < 16 ? ph[b] : pw[b]) * 16 + (d & 15));
+            w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+            unpack_cs4(w, c01, c23);
+          } else {
+            rope_cs_global(p, base + t, d, c01, c23);
+          }
+        }
         u32x2 o1, o2;
-        rope_values(p, which, base + t, d, blo, bhi, lo, hi, o1, o2);
+        rope_values(p, which, base + t, d, blo, bhi, lo, hi, c01, c23, o1, o2);
         *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + g) + 4 * hh) = o1;
         *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + 4 + g) + 4 * hh) = o2;
       }
@@ -356,7 +417,8 @@ constexpr int kR72 = 296;   // LDS row stride (elements) of the staged tile: 592
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void gemm_epilogue_rope72_lds(const GemmParams& p,
                                                          f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
-                                                         int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem) {
+                                                         int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem,
+                                                         const uint32_t* ltab) {
   using S = GemmShape<BM, BN, WM, WN>;
   static_assert(BN == 4 * 72 && BM % 8 == 0, "four 72-dim heads per tile");
   const int l32 = lane & 31, hh = lane >> 5;
@@ -389,8 +451,16 @@ __device__ __forceinline__ void gemm_epilogue_rope72_lds(const GemmParams& p,
       const float hi[4] = {bf16_lo(hr.x), bf16_hi(hr.x), bf16_lo(hr.y), bf16_hi(hr.y)};
       const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
       const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 36);
+      f32x4 c01, c23;
+      if (ltab) {
+        int ph, pw;
+        token_pos(p, m, ph, pw);
+        rope_cs_table(ltab, 18, ph, pw, d, c01, c23);
+      } else {
+        rope_cs_global(p, m, d, c01, c23);
+      }
       u32x2 o1, o2;
-      rope_values(p, which, m, d, blo, bhi, lo, hi, o1, o2);
+      rope_values(p, which, m, d, blo, bhi, lo, hi, c01, c23, o1, o2);
       bf16* row = dst + ((int64_t)(head0 + h) * p.Np + m) * 88;
       *reinterpret_cast<u32x2*>(row + d) = o1;
       *reinterpret_cast<u32x2*>(row + 36 + d) = o2;
@@ -440,6 +510,17 @@ __device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, 
   tm = r / width;
   tn = panel * group_n + r % width;
 }
+
+// Dynamic LDS of the GEMM (elements): the 2-stage operand ring or the epilogue staging, whichever
+// is larger; the rotary epilogues put their position table right after it.
+template <int BM, int BN, int WM, int WN, int EPI>
+__host__ __device__ constexpr int gemm_lds_elems() {
+  return (2 * GemmShape<BM, BN, WM, WN>::LDS_ELEMS > (EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN))
+             ? 2 * GemmShape<BM, BN, WM, WN>::LDS_ELEMS
+             : (EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN);
+}
+template <int BM, int BN, int WM, int WN, int EPI>
+__host__ __device__ constexpr int rope_tab_offset() { return (gemm_lds_elems<BM, BN, WM, WN, EPI>() + 7) / 8 * 8; }
 
 template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
@@ -495,6 +576,18 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
       if (BN % S::ROWS_PER_PASS == 0 || i * S::ROWS_PER_PASS + wave * 8 < BN)
         dma16(rww, wv, (uint32_t)((i * S::ROWS_PER_PASS * p.K + k0) * 2), wa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
   };
+
+  // The qkv rotary epilogues' per-position (cos, sin) table, copied once into LDS above the
+  // operand ring / staging area (its first barrier below publishes it).
+  const uint32_t* ltab = nullptr;
+  if constexpr (EPI == kEpiQkvRope || EPI == kEpiQkvRope72) {
+    if (p.rtab && unit < 0) {
+      uint32_t* t = reinterpret_cast<uint32_t*>(smem + rope_tab_offset<BM, BN, WM, WN, EPI>());
+      const int words = p.rtab_pos * (p.cs_half / 2);
+      for (int i = tid; i < words; i += S::THREADS) t[i] = p.rtab[i];
+      ltab = t;
+    }
+  }
 
   f32x16 acc[S::NB][S::MB];
 #pragma unroll
@@ -570,9 +663,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   }
   if constexpr (EPI == kEpiQkvRope) {
     __syncthreads();                    // every wave is done with the last stage
-    gemm_epilogue_rope_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, wave, smem);
+    gemm_epilogue_rope_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, wave, smem, ltab);
   } else if constexpr (EPI == kEpiQkvRope72) {
-    gemm_epilogue_rope72_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, tid, smem);
+    gemm_epilogue_rope72_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, tid, smem, ltab);
   } else {
     gemm_epilogue_lds<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane, tid, smem);
   }
@@ -680,11 +773,16 @@ static int gemm_group_n(int tiles_n) {
 template <int BM, int BN, int WM, int WN, int EPI>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
-  const size_t lds = std::max(2 * S::LDS_ELEMS, EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN) * sizeof(bf16);
+  constexpr bool kRope = EPI == kEpiQkvRope || EPI == kEpiQkvRope72;
+  // rotary epilogues: room for the largest position table (rope_table_lds_bytes) after the ring
+  constexpr size_t lds_max = (size_t)rope_tab_offset<BM, BN, WM, WN, EPI>() * sizeof(bf16) +
+                             (kRope ? (EPI == kEpiQkvRope ? 16384 : 12288) : 0);
+  static_assert(lds_max <= 163840, "LDS budget");
+  const size_t lds = p.rtab ? lds_max : (size_t)gemm_lds_elems<BM, BN, WM, WN, EPI>() * sizeof(bf16);
   // once per instantiation (a C++ function-local static: initialised exactly once, thread-safe)
   static const hipError_t attr_rc = hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (attr_rc != hipSuccess) return set_error(QVL_ERR_LAUNCH, "gemm_bf16: cannot reserve %zu bytes of LDS", lds);
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
+  if (attr_rc != hipSuccess) return set_error(QVL_ERR_LAUNCH, "gemm_bf16: cannot reserve %zu bytes of LDS", lds_max);
   p.full_tiles = g.full;
   p.split = g.split;
   p.group_n = gemm_group_n((p.N + BN - 1) / BN);

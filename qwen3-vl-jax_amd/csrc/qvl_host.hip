@@ -209,9 +209,16 @@ int qvl_vision_attention(void* stream, int32_t dtype, const void* q, const void*
   return attention_general(Qb, Kb, Vb, tiles, n_tiles, (int)Np, H, hd, (bf16*)out, ld_out, (hipStream_t)stream);
 }
 
-int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
-                         const void* cs, void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H,
-                         void* ws, size_t ws_bytes) {
+int qvl_rotary_pos_table(void* stream, int32_t head_dim, float theta, int32_t n_positions, uint32_t* table) {
+  float inv[32];
+  QVL_TRY_RC(qvl_rotary_inv_freq(head_dim, theta, inv));
+  if (n_positions < 0 || (n_positions > 0 && !table)) return set_error(QVL_ERR_INVALID_ARG, "rotary_pos_table: bad args");
+  return rotary_pos_table(n_positions, head_dim, inv, table, (hipStream_t)stream);
+}
+
+static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
+                           const void* cs, const int32_t* pos_hw, const uint32_t* rtab, int32_t n_pos, void* q,
+                           void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H, void* ws, size_t ws_bytes) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: dtype %d", dtype);
   if (H <= 0 || (hidden != (int64_t)H * 64 && hidden != (int64_t)H * 72))
     return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64 or 72");
@@ -220,21 +227,45 @@ int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda
   if (hd == 72 && H % 4) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim 72 needs num_heads %% 4 == 0");
   if (n_tokens < 0 || lda < hidden || lda % 8) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: n_tokens / lda");
   if (n_tokens == 0) return QVL_OK;
-  if (!x || !w || !bias || !cs || !q || !k || !vt) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
+  if (!x || !w || !bias || !q || !k || !vt || (!cs && (!pos_hw || !rtab)))
+    return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
+  if (rtab && (n_pos <= 0 || (int64_t)n_pos * (hd / 4) * 4 > rope_table_lds_bytes(hd)))
+    return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: %d rotary positions exceed the %d-byte table of head_dim %d",
+                     n_pos, rope_table_lds_bytes(hd), hd);
   if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(q) || !aligned16(k) || !aligned16(vt) ||
-      !aligned16(cs))
+      (cs && !aligned16(cs)) || (rtab && !aligned16(rtab)))
     return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: alignment");
   if (n_tokens * lda * 2 >= (int64_t)UINT32_MAX) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: operand > 4 GiB");
   GemmParams p{};
   p.x = (const bf16*)x; p.lda = lda; p.w = (const bf16*)w; p.bias = bias;
   p.M = (int)n_tokens; p.N = (int)(3 * hidden); p.K = (int)hidden;
-  p.q = (bf16*)q; p.k = (bf16*)k; p.vt = (bf16*)vt; p.cs = (const f32x2*)cs;
+  p.q = (bf16*)q; p.k = (bf16*)k; p.vt = (bf16*)vt;
+  p.cs = rtab ? nullptr : (const f32x2*)cs;
+  p.pos_hw = rtab ? pos_hw : nullptr;
+  p.rtab = rtab;
+  p.rtab_pos = rtab ? n_pos : 0;
   p.Np = (int)attn_np(n_tokens); p.D = (int)hidden;
   p.cs_half = hd / 2;
   p.qscale = (1.0f / sqrtf((float)hd)) * kLog2e;
   if (ws && !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: workspace alignment");
   p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
   return gemm_bf16(p, hd == 64 ? kEpiQkvRope : kEpiQkvRope72, (hipStream_t)stream);
+}
+
+int qvl_dense_qkv_rotary(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
+                         const void* cs, void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H,
+                         void* ws, size_t ws_bytes) {
+  if (n_tokens > 0 && !cs) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL cos/sin table");
+  return qkv_rotary_impl(stream, dtype, x, lda, w, bias, cs, nullptr, nullptr, 0, q, k, vt, n_tokens, hidden, H, ws,
+                         ws_bytes);
+}
+
+int qvl_dense_qkv_rotary_pos(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
+                             const int32_t* pos_hw, const uint32_t* table, int32_t n_positions, void* q, void* k,
+                             void* vt, int64_t n_tokens, int64_t hidden, int32_t H, void* ws, size_t ws_bytes) {
+  if (n_tokens > 0 && (!pos_hw || !table)) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary_pos: NULL positions/table");
+  return qkv_rotary_impl(stream, dtype, x, lda, w, bias, nullptr, pos_hw, table, n_positions, q, k, vt, n_tokens,
+                         hidden, H, ws, ws_bytes);
 }
 
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
@@ -431,7 +462,17 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
     px_in = h;
   }
-  QVL_TRY_RC(qvl_rotary_table(st, dt, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
+  // rotary (cos, sin): per token (the relayout kernels, the fp32 path, the head_dim-72 epilogue), or
+  // per rotary position for the head_dim-64 fused qkv epilogue when the grid's positions fit its
+  // LDS table (measured on MI355X at config 2: 126.6 vs 127.9 us per qkv launch; at head_dim 72
+  // the table's 4-byte LDS reads were slower than the per-token loads, 89.3 vs 86.5 us)
+  const bool fused_qkv = fused_qkv_rotary(dt, (int)L.hd, (int)L.H);
+  const bool pos_tab = fused_qkv && L.hd == 64 && meta->n_positions > 0 &&
+                       meta->n_positions * (L.hd / 4) * 4 <= rope_table_lds_bytes((int)L.hd);
+  if (pos_tab)
+    QVL_TRY_RC(qvl_rotary_pos_table(st, (int)L.hd, c->rope_theta, (int)meta->n_positions, (uint32_t*)cs));
+  else
+    QVL_TRY_RC(qvl_rotary_table(st, dt, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
   if (c->num_position_embeddings > 0) {
     QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
     QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
@@ -446,9 +487,13 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     const qvl_block_weights& B = W->blocks[i];
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
     QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
-    if (fused_qkv_rotary(dt, (int)L.hd, (int)L.H)) {
+    if (fused_qkv) {
       // qkv Dense with rotary + head-major relayout fused into its epilogue.
-      QVL_TRY_RC(qvl_dense_qkv_rotary(st, dt, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
+      if (pos_tab)
+        QVL_TRY_RC(qvl_dense_qkv_rotary_pos(st, dt, xn, D, B.qkv_w, B.qkv_b, meta->pos_hw, (const uint32_t*)cs,
+                                            (int)meta->n_positions, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
+      else
+        QVL_TRY_RC(qvl_dense_qkv_rotary(st, dt, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
     } else {
       // qkv Dense into h, then rotary + head-major relayout.
       QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D, D, part,

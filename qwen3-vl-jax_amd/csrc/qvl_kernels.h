@@ -21,6 +21,12 @@ struct GemmParams {
   bf16* q; bf16* k; bf16* vt;
   const f32x2* cs;               // [M, cs_half] (cos, sin), cs_half = head_dim / 2
   int cs_half;
+  // Alternatively (rtab != NULL): cos / sin looked up by rotary position from a per-position
+  // table rtab[P][head_dim / 4] of packed (bf16 cos | bf16 sin << 16), staged in LDS, with the
+  // token's (h, w) ids from pos_hw [M][2].
+  const int* pos_hw;
+  const uint32_t* rtab;
+  int rtab_pos;
   int Np, D;
   float qscale;
   // Tail split-K: fp32 partials workspace (NULL: no splitting) and its capacity in floats; the
@@ -59,6 +65,9 @@ __host__ __device__ __forceinline__ int vt_pos(int m) {
 }
 
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream);
+// LDS bytes the qkv rotary epilogue can give to a per-position rotary table (head_dim 64 / 72).
+inline int rope_table_lds_bytes(int hd) { return hd == 64 ? 16384 : 12288; }
+int rotary_pos_table(int n_pos, int head_dim, const float* inv_freq, uint32_t* table, hipStream_t stream);
 int gemm_set_plan(int tile, int split_mode, int group_n);
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
                    int H, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole = -1, float* part = nullptr);

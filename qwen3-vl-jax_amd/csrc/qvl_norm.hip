@@ -214,6 +214,27 @@ int rotary_table(const int* pos_hw, int n_tok, int head_dim, const float* inv_fr
   return check_launch("rotary_table");
 }
 
+// Per-position rotary table: t[p][j] = bf16 cos | bf16 sin << 16 of p * inv_freq[j], j < head_dim/4:
+// the same fp32 angle, cosf / sinf and rounding as rotary_table_kernel, so a token's (cos, sin) of
+// dim j equals t[pos_h][j] (j < head_dim/4) or t[pos_w][j - head_dim/4] bit for bit.
+__global__ __launch_bounds__(256) void rotary_pos_table_kernel(int n_pos, int q4, InvFreq inv, uint32_t* __restrict__ t) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_pos * q4) return;
+  const int pos = i / q4, j = i % q4;
+  const float ang = (float)pos * inv.v[j];
+  t[i] = pack_bf16x2(cosf(ang), sinf(ang));
+}
+
+int rotary_pos_table(int n_pos, int head_dim, const float* inv_freq, uint32_t* table, hipStream_t stream) {
+  if (n_pos == 0) return QVL_OK;
+  InvFreq inv{};
+  for (int j = 0; j < head_dim / 4; ++j) inv.v[j] = inv_freq[j];
+  const int total = n_pos * (head_dim / 4);
+  hipLaunchKernelGGL(rotary_pos_table_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, n_pos,
+                     head_dim / 4, inv, table);
+  return check_launch("rotary_pos_table");
+}
+
 // ---------------------------------------------------------------------------------------------
 // fp32 -> bf16 cast (pixel patches, model.py:556 `x.astype(dtype)`), 8 elements per thread.
 // ---------------------------------------------------------------------------------------------

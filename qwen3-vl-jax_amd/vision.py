@@ -224,6 +224,7 @@ class GridMetadata:
     cu_window: Optional[np.ndarray] = None
     cu_full: Optional[np.ndarray] = None
     window_tiles: Optional[np.ndarray] = None
+    n_positions: int = 0          # 1 + the largest rotary (h, w) id: max over grids of max(h, w)
 
 
 def _worklist(lib, cu: np.ndarray, num_heads: int) -> np.ndarray:
@@ -286,7 +287,8 @@ def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: Optional[in
     capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, npos, dtype, _i32p(cu), _i32p(pos),
                                        _i32p(idx) if npos else None, _f32p(w) if npos else None),
                "qvl_vision_metadata")
-    return GridMetadata(N, cu, pos, idx, w, _worklist(lib, cu, num_heads))
+    n_pos = int(g[:, 1:].max()) if len(g) else 0
+    return GridMetadata(N, cu, pos, idx, w, _worklist(lib, cu, num_heads), n_positions=n_pos)
 
 
 def window_grid_metadata(m: GridMetadata, grid_thw, merge: int, patch_size: int, window_size: int,
@@ -301,7 +303,8 @@ def window_grid_metadata(m: GridMetadata, grid_thw, merge: int, patch_size: int,
     rev = np.argsort(widx, kind="stable").astype(np.int32)
     return GridMetadata(m.n_tokens, m.cu_seqlens, np.ascontiguousarray(m.pos_hw[perm]),
                         np.ascontiguousarray(m.tap_idx[:, perm]), np.ascontiguousarray(m.tap_w[:, perm]),
-                        _worklist(lib, cuf, num_heads), widx, rev, cuw, cuf, _worklist(lib, cuw, num_heads))
+                        _worklist(lib, cuf, num_heads), widx, rev, cuw, cuf, _worklist(lib, cuw, num_heads),
+                        n_positions=m.n_positions)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -533,6 +536,7 @@ class Qwen3VisionTransformer:
                 "tap_w": dev(m.tap_w), "tiles": dev(nz(m.tiles))}
         md = capi.VisionMetadataDev()
         md.n_tokens = m.n_tokens
+        md.n_positions = m.n_positions
         md.n_tiles = len(m.tiles)
         md.pos_hw, md.tap_idx, md.tap_w, md.tiles = (tens["pos_hw"].data_ptr(), tens["tap_idx"].data_ptr(),
                                                      tens["tap_w"].data_ptr(), tens["tiles"].data_ptr())
@@ -667,6 +671,13 @@ class Qwen3VisionTransformer:
                                                                     C.byref(ab)), "attention split ws")
         ctx["apart"] = torch.empty(max(ab.value, 256), dtype=torch.uint8, **dev)
         ctx["apart_bytes"] = ab.value
+        # (cos, sin) per rotary position, as the tower looks them up when the grid's positions fit
+        n_pos = ctx["m"].n_positions
+        cap = 16384 if hd == 64 else 12288
+        if hd == 64 and 0 < n_pos and n_pos * (hd // 4) * 4 <= cap:
+            ctx["rtab"] = torch.empty((n_pos, hd // 4), dtype=torch.int32, **dev)
+            capi.check(self._lib.qvl_rotary_pos_table(self._stream(), hd, 10000.0, n_pos, ctx["rtab"].data_ptr()),
+                       "qvl_rotary_pos_table")
         return ctx
 
     def block_fused(self, i: int, x, ctx) -> None:
@@ -685,8 +696,13 @@ class Qwen3VisionTransformer:
         md = ctx["md"]
         B = self._blocks_arr[i]
         ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
-        ck(lib.qvl_dense_qkv_rotary(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb, N, D,
-                                    H, gws, gwn), "qkv_rotary")
+        if "rtab" in ctx:
+            ck(lib.qvl_dense_qkv_rotary_pos(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["tens"]["pos_hw"].data_ptr(),
+                                            ctx["rtab"].data_ptr(), ctx["rtab"].shape[0], qb, kb, vb, N, D, H, gws,
+                                            gwn), "qkv_rotary_pos")
+        else:
+            ck(lib.qvl_dense_qkv_rotary(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb, N,
+                                        D, H, gws, gwn), "qkv_rotary")
         if md.split_tiles:
             ck(lib.qvl_attention_headmajor_split(st, dt, qb, kb, vb, md.split_tiles, md.n_split_tiles,
                                                  md.n_split_whole, N, H, hd, o.data_ptr(), D,

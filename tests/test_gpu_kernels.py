@@ -487,3 +487,72 @@ def test_qkv_rotary_matches_oracle_rotary(pkg, lib, hd, grids):
     same = (qkv_h[:, :D] == ref_qkv[:, :D]).reshape(N, H, hd).transpose(1, 0, 2)
     same &= same[..., list(range(half, hd)) + list(range(half))]    # the rotary pair as well
     np.testing.assert_array_equal(got_q[:, :N, :hd][same], vt.bf16_round(qr_ref * qscale)[same])
+
+
+@pytest.mark.parametrize("hd,grids,plan", [(64, [(1, 48, 48)] * 8, None), (64, [(1, 16, 16), (2, 10, 14), (1, 6, 8)], None),
+                                           (64, [(1, 48, 48)] * 3, "288x256:split"), (72, [(1, 84, 84)], None),
+                                           (72, [(1, 16, 16), (2, 10, 14)], None)])
+def test_qkv_rotary_position_table_bit_identical(pkg, lib, hd, grids, plan):
+    """qvl_dense_qkv_rotary_pos (cos, sin looked up per rotary position from an LDS table, the
+    tower's path) writes Q, K, V^T bit-identical to qvl_dense_qkv_rotary (per-token table), with the
+    tail split's reduce kernel reading the position table from memory; and qvl_rotary_pos_table's
+    entries equal the per-token table's at every token's (h, w) ids."""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    H = 16
+    N, D = m.n_tokens, H * hd
+    Np, hdp, half, q4 = -(-N // 64) * 64, (64 if hd == 64 else 88), hd // 2, hd // 4
+    g = torch.Generator(device="cpu").manual_seed(N + hd)
+    x = torch.randn((N, D), generator=g).to(DEV).to(torch.bfloat16)
+    w = pack(lib, cp, (torch.randn((D, 3 * D), generator=g) * 0.03).numpy())
+    bias = (torch.randn(3 * D, generator=g) * 0.1).to(torch.bfloat16).float().to(DEV)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    cs = torch.empty((N, half, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
+    P = m.n_positions
+    tab = torch.empty((P, q4), dtype=torch.int32, device=DEV)
+    cp.check(lib.qvl_rotary_pos_table(stream(), hd, 10000.0, P, tab.data_ptr()))
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    outs = []
+    try:
+        set_plan(lib, cp, plan)
+        for use_tab in (False, True):
+            q = torch.full((H, Np, hdp), 5.0, dtype=torch.bfloat16, device=DEV)
+            k = q.clone()
+            vt = torch.full((H, hd, Np), 5.0, dtype=torch.bfloat16, device=DEV)
+            if use_tab:
+                cp.check(lib.qvl_dense_qkv_rotary_pos(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, w.data_ptr(),
+                                                      bias.data_ptr(), pos.data_ptr(), tab.data_ptr(), P, q.data_ptr(),
+                                                      k.data_ptr(), vt.data_ptr(), N, D, H, ws.data_ptr(), nb.value))
+            else:
+                cp.check(lib.qvl_dense_qkv_rotary(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, w.data_ptr(),
+                                                  bias.data_ptr(), cs.data_ptr(), q.data_ptr(), k.data_ptr(),
+                                                  vt.data_ptr(), N, D, H, ws.data_ptr(), nb.value))
+            torch.cuda.synchronize()
+            outs.append([t.cpu() for t in (q, k, vt)])
+    finally:
+        set_plan(lib, cp, None)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    # the table's entries are the per-token table's values at the token's ids
+    t = tab.cpu().numpy().view(np.uint32)
+    c, s_ = (t & 0xFFFF).astype(np.uint32) << 16, t & 0xFFFF0000
+    cos_t, sin_t = c.view(np.float32), s_.astype(np.uint32).view(np.float32)
+    c_h = cs.cpu().numpy()
+    ph, pw = m.pos_hw[:, 0], m.pos_hw[:, 1]
+    np.testing.assert_array_equal(c_h[:, :q4, 0], cos_t[ph]); np.testing.assert_array_equal(c_h[:, :q4, 1], sin_t[ph])
+    np.testing.assert_array_equal(c_h[:, q4:, 0], cos_t[pw]); np.testing.assert_array_equal(c_h[:, q4:, 1], sin_t[pw])
+
+
+def test_qkv_rotary_position_table_limits(pkg, lib):
+    """Tables past the epilogue's LDS room are refused before any launch."""
+    cp = pkg.capi
+    buf = torch.zeros(1 << 16, dtype=torch.bfloat16, device=DEV)
+    p = buf.data_ptr()
+    rc = lib.qvl_dense_qkv_rotary_pos(stream(), cp.QVL_DTYPE_BF16, p, 1024, p, p, p, p, 257, p, p, p, 64, 1024, 16,
+                                      None, 0)
+    assert rc == -2 and "positions" in lib.qvl_last_error().decode()
+    assert lib.qvl_dense_qkv_rotary_pos(stream(), cp.QVL_DTYPE_BF16, p, 1024, p, p, None, p, 8, p, p, p, 64, 1024, 16,
+                                        None, 0) == -1
