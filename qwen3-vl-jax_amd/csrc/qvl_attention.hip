@@ -1,5 +1,5 @@
 // Packed varlen (cu_seqlens) vision attention for gfx950: block-diagonal, non-causal softmax
-// attention per segment (model.py:585-600), bf16 MFMA with fp32 online softmax.
+// attention per segment (model.py:585-600), bf16 MFMA with fp32 softmax accumulation.
 //
 // Operand layouts (produced by the qkv GEMM's rotary epilogue or by `attn_relayout_hd64_kernel`):
 //   Q [H][Np][64]  rotated, pre-multiplied by head_dim^-0.5 * log2(e)  (scores land in log2 units)
@@ -13,15 +13,18 @@
 // source address); only the first and last tiles carry keys outside the segment and they are
 // peeled off the steady-state loop, which has no masking.
 //
-// S^T = K Q^T via v_mfma_f32_32x32x16_bf16: a lane holds one query and 16 keys of a 32-key block,
-// so softmax statistics are in-register plus one exchange with lane^32. The MFMA's C operand is
-// preloaded with -m (the running row max), the accumulator already holds s - m, and p = exp2(acc)
-// costs one instruction per score. The max is only raised on the first tile, or when a tile's
-// partial row sum exceeds 2^64 (softmax is shift-invariant; each raise rescales O and l exactly).
-// P is rounded to bf16 pairs for the PV MFMA (its B operand, straight from registers); the row sum
-// adds the fp32 values (the reference normalises by the fp32 sum, model.py:595), with fp32 adds
-// rather than v_dot2_f32_bf16 over the packed pairs, which would share the matrix pipe. V^T's
-// quad-swapped key layout makes each lane's 8 PV keys one 16-byte LDS chunk.
+// S^T = K Q^T via v_mfma_f32_32x32x16_bf16: a lane holds one query and 16 keys of a 32-key block.
+// Softmax is shift invariant, and with the tower's scores (log2 units) far inside fp32 range the
+// kernel applies no shift at all: p = exp2(s) is one instruction per score, the fp32 row sum one
+// add, and P goes to bf16 pairs for the PV MFMA (its B operand, straight from registers); there is
+// no running max, no rescale and no per-block check in the loop. After the loop each wave checks
+// its rows: a row sum outside [2^-64, 2^96] or an accumulator above 2^120 (inf / NaN included)
+// means the unshifted sum under- or overflowed, and that wave recomputes its rows shifted by the
+// exact row max (global loads: a max pass, then the sum pass), which holds for any finite scores.
+// The reference normalises by the fp32 sum of the fp32 weights (model.py:594-595) and so does the
+// kernel. V^T's quad-swapped key layout makes each lane's 8 PV keys one 16-byte LDS chunk.
+// Steady-state tiles run one 32-key block at a time (S, softmax, PV), so a block's four K and four
+// V^T fragment reads are issued ahead of its MFMAs within the 128-register budget of 4 waves/SIMD.
 #include <math.h>
 #include <type_traits>
 #include "qvl_kernels.h"
@@ -31,6 +34,9 @@ namespace qvl {
 constexpr int kAttnBM = 128;   // queries per workgroup
 constexpr int kAttnBN = 64;    // keys per K/V tile
 constexpr int kHD = 64;
+
+template <int V> using int_c = std::integral_constant<int, V>;
+
 
 // LDS offsets of (row, 16-byte chunk) in the 128-byte-row K and V^T tiles. The 16-byte chunk is
 // XOR-swizzled with (row/2) % 8: a 16-byte LDS read serves 16 lanes per clock over 64 banks (two
@@ -42,7 +48,8 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
     const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo, int n_whole,
     float* __restrict__ part) {
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * kAttnBN * kHD];   // [stage][K | V^T][64][64]
+  constexpr int kStage = 2 * kAttnBN * kHD;   // elements per stage: K [64][64] then V^T [64][64]
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
 
   // Work item: (segment start, segment end, first query, head [| part, parts]); empty items pad
   // short queues.
@@ -58,8 +65,7 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   const int l32 = lane & 31, hh = lane >> 5;
 
   const size_t head_elems = (size_t)Np * kHD;
-  const bf16* Qh = Q + head * head_elems;
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(Qh, (uint32_t)(head_elems * 2));
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + head * head_elems, (uint32_t)(head_elems * 2));
 
   // Q fragments (B operand of S^T = K Q^T): query row qrow, dims [16ks + 8hh, +8).
   const int qrow = q0 + wave * 32 + l32;
@@ -78,29 +84,25 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   const uint32_t kv_lane = (uint32_t)((drow * kHD + lch * 8) * 2);
   const uint32_t vv_lane = (uint32_t)(((int64_t)drow * Np + lch * 8) * 2);
   const uint32_t lds0 = lds_addr_of(smem);
-  constexpr uint32_t kStageBytes = 2 * kAttnBN * kHD * 2;
   auto dma_tile = [&](int kb, int stage) {
-    const uint32_t kl = lds0 + stage * kStageBytes, vl = kl + kAttnBN * kHD * 2;
+    const uint32_t kl = lds0 + stage * kStage * 2, vl = kl + kAttnBN * kHD * 2;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       dma16(rk, kv_lane, (uint32_t)((kb + 32 * i) * kHD * 2), kl + (32 * i + wave * 8) * kHD * 2);
       dma16(rv, vv_lane, (uint32_t)(((int64_t)32 * i * Np + kb) * 2), vl + (32 * i + wave * 8) * kAttnBN * 2);
     }
   };
+  // Fragment reads; with a compile-time stage every address is a per-lane base plus an immediate.
+  auto k_frag = [&](int stage, int b, int ks) {
+    return *reinterpret_cast<const bf16x8*>(&smem[stage * kStage + k_off(b * 32 + l32, ks * 2 + hh)]);
+  };
+  auto v_frag = [&](int stage, int db, int g) {
+    return *reinterpret_cast<const bf16x8*>(&smem[stage * kStage + kAttnBN * kHD + v_off(db * 32 + l32, 2 * g + hh)]);
+  };
 
   f32x16 oacc[2] = {f32x16{}, f32x16{}};
-  // The running max m is kept bf16-representable and enters S^T as a fifth MFMA k-step: K gets
-  // a constant dimension 1 (kx, dims 64..79 = [1, 0, ...]) and Q the dimension -m (qx), so the
-  // MFMAs produce s - m directly, with no C operand to refill per block.
-  float m_run = 0.f, l_run = 0.f;
-  const bf16x8 kx = __builtin_bit_cast(bf16x8, u32x4{hh ? 0u : 0x3F80u, 0u, 0u, 0u});
-  uint32_t qx0 = 0;
-  auto set_m = [&](float m) {   // m rounded up to bf16 (so s - m <= the exact shift)
-    uint32_t u = __float_as_uint(m);
-    u = m >= 0.f ? (u + 0xFFFFu) & 0xFFFF0000u : u & 0xFFFF0000u;
-    m_run = __uint_as_float(u);
-    qx0 = hh ? 0u : ((u ^ 0x80000000u) >> 16);
-  };
+  float l_run = 0.f;   // this lane's fp32 row-sum share (its 8 keys of every 16)
+  float m_run = 0.f;   // the shift of the scores: 0 on the main path, the exact row max on the exact path
 
   // Key tiles of 64 from the segment start rounded down to 64; a part of a split item takes its
   // share [t0, t1) of them.
@@ -108,194 +110,140 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
   const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
   const int n_kt = t1 - t0;
+
+  auto mask_block = [&](f32x16& s, int kb, int b) {   // keys outside [seg_s, seg_e) -> -inf
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+      if (key < seg_s || key >= seg_e) s[r] = -INFINITY;
+    }
+  };
+  // p = exp2(s - sh) as bf16 pairs, fp32 row-sum share
+  auto exp_pack = [&](const f32x16& s, float sh, uint32_t (&pk)[8]) {
+    float ta = 0.f, tb = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e0 = __builtin_amdgcn_exp2f(s[2 * j] - sh), e1 = __builtin_amdgcn_exp2f(s[2 * j + 1] - sh);
+      pk[j] = pack_bf16x2(e0, e1);
+      ta = j ? ta + e0 : e0;
+      tb = j ? tb + e1 : e1;
+    }
+    l_run += ta + tb;
+  };
+  // O^T[d][q] += V^T[d][keys] P^T[keys][q]: B operand = 8 P values per lane.
+  auto pv = [&](const bf16x8 (&vf)[4], const uint32_t (&pk)[8]) {
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2) {
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * e2], pk[4 * e2 + 1], pk[4 * e2 + 2], pk[4 * e2 + 3]});
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * e2 + db], pf, oacc[db], 0, 0, 0);
+    }
+  };
+
+  // One key tile in LDS stage ST; EDGE masks keys outside the segment (first and last tiles).
+  auto step = [&](auto edge_tag, auto stage_tag, int it) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    constexpr int ST = decltype(stage_tag)::value;
+    const int kb = k_begin + it * kAttnBN;
+    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, ST ^ 1);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      bf16x8 kf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kf[ks] = k_frag(ST, b, ks);
+      f32x16 s = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+      if constexpr (EDGE) mask_block(s, kb, b);
+      bf16x8 vf[4];
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) vf[2 * e2 + db] = v_frag(ST, db, 2 * b + e2);
+      uint32_t pk[8];
+      exp_pack(s, 0.f, pk);
+      pv(vf, pk);
+    }
+    wait_dma();
+    __syncthreads();
+  };
+
   dma_tile(k_begin, 0);
   wait_dma();
   __syncthreads();
+  // Tile it sits in stage it % 2: tile 0 (masked), then odd/even pairs so each stage is a constant.
+  step(std::true_type{}, int_c<0>{}, 0);
+  int it = 1;
+  for (; it + 2 < n_kt; it += 2) {
+    step(std::false_type{}, int_c<1>{}, it);
+    step(std::false_type{}, int_c<0>{}, it + 1);
+  }
+  if (it == n_kt - 2) {
+    step(std::false_type{}, int_c<1>{}, it);
+    step(std::true_type{}, int_c<0>{}, it + 1);
+  } else if (it == n_kt - 1) {
+    step(std::true_type{}, int_c<1>{}, it);
+  }
 
-  // One key tile. EDGE: the first or last tile (mask keys outside [seg_s, seg_e); the first tile
-  // sets the running max exactly).
-  auto step = [&](auto edge_tag, int it) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    const int cur = it & 1;
-    const int kb = k_begin + it * kAttnBN;
-    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
-    const bf16* sK = smem + cur * (2 * kAttnBN * kHD);
-    const bf16* sV = sK + kAttnBN * kHD;
-    const bool first = EDGE && it == 0;
-
-    // S^T blocks: keys [32b, 32b+32) of this tile, accumulated onto C = -m.
-    f32x16 s[2];
+  float l_tot = l_run + __shfl_xor(l_run, 32);
+  float omax = 0.f;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      s[b] = f32x16{};
+  for (int r = 0; r < 16; ++r) omax = fmaxf(omax, fmaxf(fabsf(oacc[0][r]), fabsf(oacc[1][r])));
+  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !(omax <= 0x1p120f)) != 0) {
+    // Some row's sum of 2^s left [2^-64, 2^96] (or O grew past 2^120, or anything overflowed):
+    // recompute this wave's rows shifted by the exact row max, reading K and V^T from global
+    // memory (the other waves may be done).
+    const __amdgpu_buffer_rsrc_t rkg = make_rsrc(K + head * head_elems, (uint32_t)(head_elems * 2));
+    const __amdgpu_buffer_rsrc_t rvg = make_rsrc(Vt + head * head_elems, (uint32_t)(head_elems * 2));
+    bf16x8 qg[4];   // reloaded: the loop's fragments are not kept live past it
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qg[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * kHD + ks * 16 + hh * 8) * 2)));
+    auto scores = [&](int kb, int b) {
+      f32x16 s = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k_off(b * 32 + l32, ks * 2 + hh)]);
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
+        const bf16x8 kf = __builtin_bit_cast(
+            bf16x8, buf_load16(rkg, (uint32_t)(((int64_t)(kb + 32 * b + l32) * kHD + ks * 16 + hh * 8) * 2)));
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qg[ks], s, 0, 0, 0);
       }
-      if (!first) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx, __builtin_bit_cast(bf16x8, u32x4{qx0, 0u, 0u, 0u}), s[b], 0, 0, 0);
-    }
-    if constexpr (EDGE) {
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
-        }
-    }
-    float shift = 0.f;
-    if (first) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      set_m(fmaxf(mx, __shfl_xor(mx, 32)));
-      shift = m_run;
-    }
-    // p = exp2(s - shift) as bf16 pairs; partial row sum over the rounded values.
-    uint32_t pk[2][8];
-    float ts = 0.f, ts2 = 0.f;
-    auto exp_pack = [&](float sh) {
-      ts = 0.f; ts2 = 0.f;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j] - sh), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1] - sh);
-          pk[b][j] = pack_bf16x2(e0, e1);
-          ts += e0;
-          ts2 += e1;
-        }
-      ts += ts2;
+      mask_block(s, kb, b);
+      return s;
     };
-    exp_pack(shift);
-    if (!first && __builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
-      // Some row of this tile outgrew the stale max: raise it (s holds score - m).
-      float mx = -INFINITY;
+    float mx = -INFINITY;
+    for (int t = 0; t < n_kt; ++t)
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < 2; ++b) {
+        const f32x16 s = scores(k_begin + t * kAttnBN, b);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-      const float m_old = m_run;
-      set_m(m_old + fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f));
-      const float d = m_run - m_old;
-      exp_pack(d);
-      const float alpha = __builtin_amdgcn_exp2f(-d);
-      l_run *= alpha;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
-    }
-    l_run += ts;
-
-    // O^T[d][q] += V^T[d][keys] P^T[keys][q]: B operand = 8 P values per lane.
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[b][4 * e2], pk[b][4 * e2 + 1], pk[b][4 * e2 + 2],
-                                                           pk[b][4 * e2 + 3]});
-        const int g = 2 * b + e2;   // 16-key group within the tile
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * g + hh)]);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
-        }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
       }
-    wait_dma();
-    __syncthreads();
-  };
-
-  // Every tile after the first, one 32-key block at a time: block 0's softmax is independent of
-  // block 1's S MFMAs and block 1's softmax of block 0's PV MFMAs, so each wave has VALU work to
-  // issue beside its own MFMAs. Each block checks its own partial row sum; a raise rescales O and
-  // l, which already hold block 0's PV when block 1 raises (exact), and shifts the blocks not yet
-  // exponentiated by the same amount.
-  auto step_blocks = [&](auto edge_tag, int it) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    const int cur = it & 1;
-    const int kb = k_begin + it * kAttnBN;
-    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
-    const bf16* sK = smem + cur * (2 * kAttnBN * kHD);
-    const bf16* sV = sK + kAttnBN * kHD;
-    f32x16 s[2];
-    const bf16x8 qx = __builtin_bit_cast(bf16x8, u32x4{qx0, 0u, 0u, 0u});
+    m_run = fmaxf(mx, __shfl_xor(mx, 32));
+    oacc[0] = f32x16{};
+    oacc[1] = f32x16{};
+    l_run = 0.f;
+    for (int t = 0; t < n_kt; ++t) {
+      const int kb = k_begin + t * kAttnBN;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx, qx, f32x16{}, 0, 0, 0);
+      for (int b = 0; b < 2; ++b) {
+        uint32_t pk[8];
+        exp_pack(scores(kb, b), m_run, pk);
+        bf16x8 vf[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k_off(b * 32 + l32, ks * 2 + hh)]);
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
+        for (int e2 = 0; e2 < 2; ++e2)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+            vf[2 * e2 + db] = __builtin_bit_cast(
+                bf16x8, buf_load16(rvg, (uint32_t)(((int64_t)(db * 32 + l32) * Np + kb + (2 * (2 * b + e2) + hh) * 8) * 2)));
+        pv(vf, pk);
       }
     }
-    if constexpr (EDGE) {
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      uint32_t pk[8];
-      float ts;
-      auto exp_block = [&]() {
-        float ta = 0.f, tb = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j]), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1]);
-          pk[j] = pack_bf16x2(e0, e1);
-          ta += e0;
-          tb += e1;
-        }
-        ts = ta + tb;
-      };
-      exp_block();
-      if (__builtin_amdgcn_ballot_w64(!(ts <= 0x1p64f)) != 0) {
-        // Some row of this block outgrew the stale max: raise it by the block's max.
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-        const float m_old = m_run;
-        set_m(m_old + fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f));
-        const float d = m_run - m_old;
-#pragma unroll
-        for (int bb = b; bb < 2; ++bb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[bb][r] -= d;
-        exp_block();
-        const float alpha = __builtin_amdgcn_exp2f(-d);
-        l_run *= alpha;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
-      }
-      l_run += ts;
-#pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * e2], pk[4 * e2 + 1], pk[4 * e2 + 2], pk[4 * e2 + 3]});
-        const int g = 2 * b + e2;   // 16-key group within the tile
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * g + hh)]);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
-        }
-      }
-    }
-    wait_dma();
-    __syncthreads();
-  };
+    l_tot = l_run + __shfl_xor(l_run, 32);
+  }
 
-  step(std::true_type{}, 0);
-  for (int it = 1; it + 1 < n_kt; ++it) step_blocks(std::false_type{}, it);
-  if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (parts) {
-    // Part of a split item: unnormalised O^T, running max and row sum, for the combine kernel.
+    // Part of a split item: unnormalised O^T, m and row sum, for the combine kernel.
     if (qrow < seg_e) {
       float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(kHD);
       const int ql = wave * 32 + l32;
@@ -326,10 +274,10 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
 
 // ---------------------------------------------------------------------------------------------
 // head_dim 72 (the 8B tower): Q/K [H][Np][88] (dims 72..87 zero; the QK MFMAs use dims 0..79),
-// V^T [H][72][Np] (keys at vt_pos). Same work items, softmax pipeline and block-at-a-time steady
-// state as the hd-64 kernel. K tiles arrive by LDS DMA as contiguous 176-byte rows: 11 16-byte
-// chunks, an odd count, so the 16 rows one fragment read touches fall on 16 distinct bank groups
-// without a swizzle. V^T tiles arrive as 128-byte rows with the hd-64 kernel's XOR swizzle; the
+// V^T [H][72][Np] (keys at vt_pos). Same work items, unshifted softmax with the exact fallback,
+// and block-at-a-time steady state as the hd-64 kernel. K tiles arrive by LDS DMA as contiguous
+// 176-byte rows: 11 16-byte chunks, an odd count, so the 16 rows one fragment read touches fall on
+// 16 distinct bank groups without a swizzle. V^T tiles arrive as 128-byte rows with the hd-64 kernel's XOR swizzle; the
 // third 32-row PV block reads LDS rows 72..95, which the DMA never writes: row 72 holds ones, so
 // output row 72 accumulates the softmax row sums (no VALU adds for them); rows 73..95 only feed
 // output rows that are not stored (an MFMA output row depends on its own A row only).
@@ -396,16 +344,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   };
 
   f32x16 oacc[kNDB72] = {f32x16{}, f32x16{}, f32x16{}};
-  // Running max: bf16-representable, applied by an MFMA k-step as in attn_fwd_hd64_kernel.
-  float m_run = 0.f;
-  const bf16x8 kx = __builtin_bit_cast(bf16x8, u32x4{hh ? 0u : 0x3F80u, 0u, 0u, 0u});
-  uint32_t qx0 = 0;
-  auto set_m = [&](float m) {   // m rounded up to bf16
-    uint32_t u = __float_as_uint(m);
-    u = m >= 0.f ? (u + 0xFFFFu) & 0xFFFF0000u : u & 0xFFFF0000u;
-    m_run = __uint_as_float(u);
-    qx0 = hh ? 0u : ((u ^ 0x80000000u) >> 16);
-  };
+  float m_run = 0.f;   // the shift of the scores: 0 on the main path, the exact row max on the exact path
 
   const int n_all = (seg_e - (seg_s & ~(kAttnBN - 1)) + kAttnBN - 1) / kAttnBN;
   const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
@@ -413,144 +352,139 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   const int n_kt = t1 - t0;
   dma_tile(k_begin, 0);
   // Row 72 of both V^T stages holds ones (the DMA fills rows 0..71 only): the third PV block then
-  // accumulates each query's row sum of the bf16 P in O^T row 72, with the rescales of O.
+  // accumulates each query's row sum of the bf16 P in O^T row 72.
   if (tid < 16)
     *reinterpret_cast<u32x4*>(smem + (tid >> 3) * (kKTile72 + kVTile72) + kKTile72 + kVR72 * kAttnBN + (tid & 7) * 8) =
         u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   wait_dma();
   __syncthreads();
 
-  auto s_blocks = [&](const bf16* sK, f32x16 (&s)[2], bool first) {
+  auto mask_block = [&](f32x16& s, int kb, int b) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      s[b] = first ? f32x16{}
-                   : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx, __builtin_bit_cast(bf16x8, u32x4{qx0, 0u, 0u, 0u}),
-                                                             f32x16{}, 0, 0, 0);
-#pragma unroll
-      for (int ks = 0; ks < kKS72; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k72_off(b * 32 + l32, ks * 2 + hh)]);
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+      if (key < seg_s || key >= seg_e) s[r] = -INFINITY;
     }
   };
-  auto mask_edge = [&](f32x16 (&s)[2], int kb) {
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (key < seg_s || key >= seg_e) s[b][r] = -INFINITY;
-      }
-  };
-  auto pv_block = [&](const bf16* sV, int b, const uint32_t (&pk)[8]) {
+  auto pv_frags = [&](const bf16x8 (&vf)[2][kNDB72], const uint32_t (&pk)[8]) {
 #pragma unroll
     for (int e2 = 0; e2 < 2; ++e2) {
       const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * e2], pk[4 * e2 + 1], pk[4 * e2 + 2], pk[4 * e2 + 3]});
-      const int g = 2 * b + e2;   // 16-key group within the tile
 #pragma unroll
-      for (int db = 0; db < kNDB72; ++db) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * g + hh)]);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[db], 0, 0, 0);
-      }
+      for (int db = 0; db < kNDB72; ++db)
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[e2][db], pf, oacc[db], 0, 0, 0);
     }
   };
-  // Raise m by at least sh; returns the exact raise d and rescales O (row sums included) by 2^-d.
-  auto raise_m = [&](float sh) {
-    const float m_old = m_run;
-    set_m(m_old + sh);
-    const float d = m_run - m_old;
-    const float alpha = __builtin_amdgcn_exp2f(-d);
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-#pragma unroll
-      for (int db = 0; db < kNDB72; ++db) oacc[db][r] *= alpha;
-    return d;
-  };
-
-  // First tile: the running max is set exactly from both blocks.
-  auto step_first = [&]() {
-    const int kb = k_begin;
-    if (n_kt > 1) dma_tile(kb + kAttnBN, 1);
-    const bf16* sK = smem;
-    const bf16* sV = sK + kKTile72;
-    f32x16 s[2];
-    s_blocks(sK, s, true);
-    mask_edge(s, kb);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-    set_m(fmaxf(mx, __shfl_xor(mx, 32)));
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      uint32_t pk[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float e0 = __builtin_amdgcn_exp2f(s[b][2 * j] - m_run), e1 = __builtin_amdgcn_exp2f(s[b][2 * j + 1] - m_run);
-        pk[j] = pack_bf16x2(e0, e1);
-      }
-      pv_block(sV, b, pk);
-    }
-    wait_dma();
-    __syncthreads();
-  };
-
-  // Later tiles, one 32-key block at a time (see attn_fwd_hd64_kernel's step_blocks).
-  auto step_blocks = [&](auto edge_tag, int it) {
+  // One key tile in LDS stage ST, one 32-key block at a time; EDGE masks keys outside the segment.
+  auto step = [&](auto edge_tag, auto stage_tag, int it) {
     constexpr bool EDGE = decltype(edge_tag)::value;
-    const int cur = it & 1;
+    constexpr int ST = decltype(stage_tag)::value;
     const int kb = k_begin + it * kAttnBN;
-    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, cur ^ 1);
-    const bf16* sK = smem + cur * (kKTile72 + kVTile72);
+    if (it + 1 < n_kt) dma_tile(kb + kAttnBN, ST ^ 1);
+    const bf16* sK = smem + ST * (kKTile72 + kVTile72);
     const bf16* sV = sK + kKTile72;
-    f32x16 s[2];
-    s_blocks(sK, s, false);
-    if constexpr (EDGE) mask_edge(s, kb);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      // p = exp2(s) as bf16 pairs and the block's largest p (the row sums come from the ones row)
-      uint32_t pk[8];
-      float pmax;
-      auto exp_block = [&]() {
-        float e[16];
+      f32x16 s = f32x16{};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          e[2 * j] = __builtin_amdgcn_exp2f(s[b][2 * j]);
-          e[2 * j + 1] = __builtin_amdgcn_exp2f(s[b][2 * j + 1]);
-          pk[j] = pack_bf16x2(e[2 * j], e[2 * j + 1]);
-        }
-        float m0 = fmaxf(fmaxf(e[0], e[1]), e[2]), m1 = fmaxf(fmaxf(e[3], e[4]), e[5]);
-        float m2 = fmaxf(fmaxf(e[6], e[7]), e[8]), m3 = fmaxf(fmaxf(e[9], e[10]), e[11]);
-        float m4 = fmaxf(fmaxf(e[12], e[13]), e[14]);
-        pmax = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), e[15]));
-      };
-      exp_block();
-      // Some row of this block outgrew the stale max by 2^64 (or overflowed): raise it.
-      if (__builtin_amdgcn_ballot_w64(!(pmax <= 0x1p64f)) != 0) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-        const float d = raise_m(fmaxf(fmaxf(mx, __shfl_xor(mx, 32)), 0.f));
-#pragma unroll
-        for (int bb = b; bb < 2; ++bb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[bb][r] -= d;
-        exp_block();
+      for (int ks = 0; ks < kKS72; ++ks) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[k72_off(b * 32 + l32, ks * 2 + hh)]);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s, 0, 0, 0);
       }
-      pv_block(sV, b, pk);
+      if constexpr (EDGE) mask_block(s, kb, b);
+      bf16x8 vf[2][kNDB72];
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2)
+#pragma unroll
+        for (int db = 0; db < kNDB72; ++db)
+          vf[e2][db] = *reinterpret_cast<const bf16x8*>(&sV[v_off(db * 32 + l32, 2 * (2 * b + e2) + hh)]);
+      uint32_t pk[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pk[j] = pack_bf16x2(__builtin_amdgcn_exp2f(s[2 * j]), __builtin_amdgcn_exp2f(s[2 * j + 1]));
+      pv_frags(vf, pk);
     }
     wait_dma();
     __syncthreads();
   };
-
-  step_first();
-  for (int it = 1; it + 1 < n_kt; ++it) step_blocks(std::false_type{}, it);
-  if (n_kt > 1) step_blocks(std::true_type{}, n_kt - 1);
+  step(std::true_type{}, int_c<0>{}, 0);
+  int it = 1;
+  for (; it + 2 < n_kt; it += 2) {
+    step(std::false_type{}, int_c<1>{}, it);
+    step(std::false_type{}, int_c<0>{}, it + 1);
+  }
+  if (it == n_kt - 2) {
+    step(std::false_type{}, int_c<1>{}, it);
+    step(std::true_type{}, int_c<0>{}, it + 1);
+  } else if (it == n_kt - 1) {
+    step(std::true_type{}, int_c<1>{}, it);
+  }
 
   // O^T row 72 (block 2, register 4 of the lanes with hh = 0) is the row sum of query l32
   const float l_row = oacc[2][4], l_swap = __shfl_xor(l_row, 32);
-  const float l_tot = hh ? l_swap : l_row;
+  float l_tot = hh ? l_swap : l_row;
+  // |O| over the stored rows: block 2 holds output rows 64..71 in registers 0..3; its other
+  // registers are the row sum (row 72) and rows 73..95, products of LDS rows the DMA never writes
+  float omax = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) omax = fmaxf(omax, fmaxf(fabsf(oacc[0][r]), fabsf(oacc[1][r])));
+#pragma unroll
+  for (int r = 0; r < 4; ++r) omax = fmaxf(omax, fabsf(oacc[2][r]));
+  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !(omax <= 0x1p120f)) != 0) {
+    // As in attn_fwd_hd64_kernel: recompute this wave's rows shifted by the exact row max, from
+    // global memory; the row sum by fp32 adds (V^T rows past 71 read as zero: one head's range).
+    const __amdgpu_buffer_rsrc_t rkg = make_rsrc(K + head * qk_head, (uint32_t)(qk_head * 2));
+    const __amdgpu_buffer_rsrc_t rvg = make_rsrc(Vt + head * v_head, (uint32_t)(v_head * 2));
+    bf16x8 qg[kKS72];
+#pragma unroll
+    for (int ks = 0; ks < kKS72; ++ks)
+      qg[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * kQK72 + ks * 16 + hh * 8) * 2)));
+    auto scores = [&](int kb, int b) {
+      f32x16 s = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < kKS72; ++ks) {
+        const bf16x8 kf = __builtin_bit_cast(
+            bf16x8, buf_load16(rkg, (uint32_t)(((int64_t)(kb + 32 * b + l32) * kQK72 + ks * 16 + hh * 8) * 2)));
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qg[ks], s, 0, 0, 0);
+      }
+      mask_block(s, kb, b);
+      return s;
+    };
+    float mx = -INFINITY;
+    for (int t = 0; t < n_kt; ++t)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const f32x16 s = scores(k_begin + t * kAttnBN, b);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      }
+    m_run = fmaxf(mx, __shfl_xor(mx, 32));
+#pragma unroll
+    for (int db = 0; db < kNDB72; ++db) oacc[db] = f32x16{};
+    float lsum = 0.f;
+    for (int t = 0; t < n_kt; ++t) {
+      const int kb = k_begin + t * kAttnBN;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const f32x16 s = scores(kb, b);
+        uint32_t pk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(s[2 * j] - m_run), e1 = __builtin_amdgcn_exp2f(s[2 * j + 1] - m_run);
+          pk[j] = pack_bf16x2(e0, e1);
+          lsum += e0 + e1;
+        }
+        bf16x8 vf[2][kNDB72];
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2)
+#pragma unroll
+          for (int db = 0; db < kNDB72; ++db)
+            vf[e2][db] = __builtin_bit_cast(
+                bf16x8, buf_load16(rvg, (uint32_t)(((int64_t)(db * 32 + l32) * Np + kb + (2 * (2 * b + e2) + hh) * 8) * 2)));
+        pv_frags(vf, pk);
+      }
+    }
+    l_tot = lsum + __shfl_xor(lsum, 32);
+  }
   if (parts) {
     if (qrow < seg_e) {
       float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(kHD72);

@@ -309,6 +309,72 @@ def test_attention_split_items_match_whole(pkg, lib, hd, cu, H, n_cus):
             assert rel_l2(parts[s:e], ref[s:e]) <= 1e-2, (s, e)
 
 
+@pytest.mark.parametrize("hd", [64, 72])
+@pytest.mark.parametrize("spike", [40.0, 100.0])
+def test_attention_late_score_spike(pkg, lib, hd, spike):
+    """Scores far above the first key tile's maximum: the kernels hold the first tile's max m and
+    carry p = 2^(s - m) > 1 in fp32; a row sum past 2^64 (spike 100, in log2 units) sends the wave
+    to its exact recompute. Keys in a middle tile and in the segment's last (masked) tile spike for
+    some query rows of every head, on the whole and the split work lists: rel-L2 <= 1e-2 against
+    an fp32 reference per segment, every row finite."""
+    cp = pkg.capi
+    H = 4
+    cu = np.array([0, 100, 2600, 2700, 7000], np.int32)
+    N = int(cu[-1])
+    q, k, vt, _ = _headmajor_operands(H, hd, cu, seed=11 + hd)
+    q, k, vt = q.cpu(), k.cpu(), vt.cpu()
+    # rows r of segment [s, e) get q[r, 0] = 8 and spiking keys j get k[j, 0] = (spike + 8) / 8 * 8 / 8;
+    # the other keys' dimension 0 is cleared so the spike stands out by ~spike
+    rows_keys = [(range(110, 400, 7), 1000), (range(2620, 2700, 3), 2690), (range(4000, 7000, 11), 6990),
+                 (range(2610, 2640), 2650), (range(3000, 3010), 6500)]
+    kval = spike / 8.0
+    for rows, key in rows_keys:
+        for r in rows:
+            q[:, r, 0] = 8.0
+        k[:, key, 0] = kval
+    for h in range(H):
+        for s, e in zip(cu[:-1], cu[1:]):
+            others = [j for j in range(s, e) if j not in {key for _, key in rows_keys}]
+            k[h, others, 0] = 0.0
+    ref = torch.zeros((N, H * hd))
+    vt_keys = torch.empty_like(vt)
+    n = np.arange(vt.shape[2])
+    quad = (n >> 2) & 3
+    pos = (n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3)
+    vt_keys[:, :, :] = vt[:, :, torch.from_numpy(pos)]
+    for s, e in zip(cu[:-1], cu[1:]):
+        sc = torch.einsum("hqd,hkd->hqk", q[:, s:e, :hd].float(), k[:, s:e, :hd].float())
+        p = torch.softmax(sc * 0.6931471805599453, dim=-1)
+        ref[s:e] = torch.einsum("hqk,hdk->hqd", p, vt_keys[:, :, s:e].float()).permute(1, 0, 2).reshape(e - s, H * hd)
+    ref = ref.numpy()
+    q, k, vt = q.to(DEV), k.to(DEV), vt.to(DEV)
+    lists = [(pkg.vision._worklist(lib, cu, H), None)]
+    split, n_whole = pkg.attention_worklist_split(cu, H, hd, 40)
+    if len(split) > n_whole:
+        lists.append((split, n_whole))
+    for items, nw in lists:
+        t = torch.from_numpy(np.ascontiguousarray(items)).to(DEV)
+        out = torch.full((N, H * hd), float("nan"), dtype=torch.bfloat16, device=DEV)
+        if nw is None:
+            cp.check(lib.qvl_attention_headmajor(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(), vt.data_ptr(),
+                                                 t.data_ptr(), len(items), N, H, hd, out.data_ptr(), H * hd))
+        else:
+            nb = C.c_size_t()
+            cp.check(lib.qvl_attention_split_workspace_size(hd, len(items), nw, C.byref(nb)))
+            ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=DEV)
+            cp.check(lib.qvl_attention_headmajor_split(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(),
+                                                       vt.data_ptr(), t.data_ptr(), len(items), nw, N, H, hd,
+                                                       out.data_ptr(), H * hd, ws.data_ptr(), nb.value))
+        torch.cuda.synchronize()
+        got = to_np(out)
+        assert np.isfinite(got).all(), nw
+        for s, e in zip(cu[:-1], cu[1:]):
+            assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (nw, s, e, rel_l2(got[s:e], ref[s:e]))
+        for rows, key in rows_keys:             # the spiking rows follow their key's value row
+            r = np.array(list(rows))
+            assert rel_l2(got[r], ref[r]) <= 1e-2, (nw, key)
+
+
 _TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4}
 
 
