@@ -202,6 +202,43 @@ int qvl_dense_qkv_rotary_pos(void* stream, int32_t dtype, const void* d_x, int64
                              int32_t n_positions, void* d_q, void* d_k, void* d_vt, int64_t n_tokens,
                              int64_t hidden, int32_t num_heads, void* d_workspace, size_t workspace_bytes);
 
+/* LayerNorm folded into the Dense that consumes it (LayerNorm model.py:375-388, feeding the qkv
+ * Dense at 570 via norm1 (628), linear_fc1 at 611 via norm2 (629), and a deepstack merger's
+ * linear_fc1 at 651-655 via its post-shuffle norm). With xn = (x - mean) * rstd * gamma + beta:
+ *   xn . W[n] = rstd * (x . W'[n]) - rstd * mean * c[n] + d[n],
+ *   W'[n][k] = bf16(gamma[k] * W[n][k]),  c[n] = sum_k W'[n][k],  d[n] = sum_k beta[k] * W[n][k],
+ * so the Dense runs on the un-normalised rows x with the folded kernel W', and the per-row
+ * (mean, rstd) and per-feature (c, d) are applied to the fp32 accumulator before the bias and the
+ * rest of the epilogue (the bf16 rounding of the product then happens where the reference rounds
+ * its Dense output; the reference's rounding of xn to bf16 is replaced by the rounding of W').
+ * bf16 only. */
+
+/* (mean, rsqrt(var + eps)) of each row of x [rows, cols] (bf16, row stride ldx), two-pass fp32 as in
+ * qvl_layer_norm: d_stats [rows][2] fp32. (model.py:384-386) */
+int qvl_row_stats(void* stream, int32_t dtype, const void* d_x, int64_t ldx, int64_t rows, int64_t cols,
+                  float eps, float* d_stats);
+
+/* W' and (c, d) from a qvl_pack_dense_weight kernel: d_w and d_out_w packed [round_up(n_out, 64), k_in]
+ * (k_in a multiple of 64), d_out_cd [round_up(n_out, 64)][2] fp32; padding rows give zeros.
+ * d_gamma / d_beta: the LayerNorm's [k_in] affine (bf16-representable fp32 values). */
+int qvl_fold_ln_weight(void* stream, int32_t dtype, const void* d_w, int64_t k_in, int64_t n_out,
+                       const float* d_gamma, const float* d_beta, void* d_out_w, float* d_out_cd);
+
+/* qvl_dense_ws on the un-normalised rows with a folded LayerNorm (QVL_EPI_BIAS or
+ * QVL_EPI_BIAS_GELU): d_w = W', d_cd = (c, d) of qvl_fold_ln_weight, d_stats = qvl_row_stats of x. */
+int qvl_dense_ln_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, int64_t lda,
+                    const void* d_w, const float* d_cd, const float* d_stats, const float* d_bias,
+                    void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                    void* d_workspace, size_t workspace_bytes);
+
+/* qvl_dense_qkv_rotary (d_cos_sin != NULL, d_pos_hw / d_table NULL) or qvl_dense_qkv_rotary_pos
+ * (d_cos_sin NULL) with norm1 folded in: x un-normalised, d_w = W', d_cd, d_stats as above. */
+int qvl_dense_qkv_rotary_ln(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
+                            const float* d_cd, const float* d_stats, const float* d_bias,
+                            const void* d_cos_sin, const int32_t* d_pos_hw, const uint32_t* d_table,
+                            int32_t n_positions, void* d_q, void* d_k, void* d_vt, int64_t n_tokens,
+                            int64_t hidden, int32_t num_heads, void* d_workspace, size_t workspace_bytes);
+
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
  * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][88] (dims 72..87 zero) and
@@ -261,6 +298,12 @@ typedef struct qvl_vision_config {
                                        cu_seqlens (depth <= 64)                          */
 } qvl_vision_config;
 
+/* A LayerNorm folded into the Dense after it (qvl_fold_ln_weight); w == NULL: not folded. */
+typedef struct qvl_ln_fold {
+  const void* w;                             /* packed W' [n_out_pad, k_in] bf16     */
+  const float* cd;                           /* [n_out_pad][2] (c, d) fp32           */
+} qvl_ln_fold;
+
 typedef struct qvl_block_weights {           /* blocks_{i} (model.py:617-630)          */
   const float* norm1_w; const float* norm1_b;
   const float* norm2_w; const float* norm2_b;
@@ -268,12 +311,18 @@ typedef struct qvl_block_weights {           /* blocks_{i} (model.py:617-630)   
   const void* proj_w; const float* proj_b;   /* packed [D, D]                         */
   const void* fc1_w;  const float* fc1_b;    /* packed [I_pad, D]                     */
   const void* fc2_w;  const float* fc2_b;    /* packed [D, I_pad]                     */
+  /* bf16 towers: norm1 folded into qkv and norm2 into fc1. When both are set the tower runs
+   * qvl_row_stats + the folded GEMMs instead of the two qvl_layer_norm launches. */
+  qvl_ln_fold qkv_ln, fc1_ln;
 } qvl_block_weights;
 
 typedef struct qvl_merger_weights {          /* merger / deepstack_mergers_{j} (633-656) */
   const float* norm_w; const float* norm_b;  /* [D] (main) or [4D] (deepstack)         */
   const void* fc1_w; const float* fc1_b;     /* packed [4D, 4D]                        */
   const void* fc2_w; const float* fc2_b;     /* packed [Dout_pad, 4D]                  */
+  /* deepstack mergers in bf16: the post-shuffle norm folded into fc1 (the main merger's norm
+   * acts per token on a row of 4 tokens, which one accumulator cannot take: never folded) */
+  qvl_ln_fold fc1_ln;
 } qvl_merger_weights;
 
 typedef struct qvl_vision_weights {

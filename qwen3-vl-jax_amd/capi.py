@@ -35,14 +35,20 @@ class VisionConfig(C.Structure):
                 ("fullatt_mask", C.c_uint64)]
 
 
+class LnFold(C.Structure):
+    _fields_ = [("w", _p), ("cd", _p)]
+
+
 class BlockWeights(C.Structure):
     _fields_ = [("norm1_w", _p), ("norm1_b", _p), ("norm2_w", _p), ("norm2_b", _p),
                 ("qkv_w", _p), ("qkv_b", _p), ("proj_w", _p), ("proj_b", _p),
-                ("fc1_w", _p), ("fc1_b", _p), ("fc2_w", _p), ("fc2_b", _p)]
+                ("fc1_w", _p), ("fc1_b", _p), ("fc2_w", _p), ("fc2_b", _p),
+                ("qkv_ln", LnFold), ("fc1_ln", LnFold)]
 
 
 class MergerWeights(C.Structure):
-    _fields_ = [("norm_w", _p), ("norm_b", _p), ("fc1_w", _p), ("fc1_b", _p), ("fc2_w", _p), ("fc2_b", _p)]
+    _fields_ = [("norm_w", _p), ("norm_b", _p), ("fc1_w", _p), ("fc1_b", _p), ("fc2_w", _p), ("fc2_b", _p),
+                ("fc1_ln", LnFold)]
 
 
 class VisionWeights(C.Structure):
@@ -75,6 +81,11 @@ SIGNATURES = {
     "qvl_dense_workspace_size": (C.c_int, [C.POINTER(_sz)]),
     "qvl_dense_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _sz]),
     "qvl_layer_norm": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _f32]),
+    "qvl_row_stats": (C.c_int, [_p, _i32, _p, _i64, _i64, _i64, _f32, _p]),
+    "qvl_fold_ln_weight": (C.c_int, [_p, _i32, _p, _i64, _i64, _p, _p, _p, _p]),
+    "qvl_dense_ln_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz]),
+    "qvl_dense_qkv_rotary_ln": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64,
+                                          _i64, _i32, _p, _sz]),
     "qvl_pos_embed": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64]),
     "qvl_rotary_table": (C.c_int, [_p, _i32, _p, _i64, _i32, _f32, _p]),
     "qvl_vision_attention_workspace_size": (C.c_int, [_i32, _i64, _i32, _i32, C.POINTER(_sz)]),

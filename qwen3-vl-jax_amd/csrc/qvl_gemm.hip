@@ -128,6 +128,50 @@ __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int 
                                             const f32x4& bhi, const float (&lo_acc)[4], const float (&hi_acc)[4],
                                             const f32x4& c01, const f32x4& c23, u32x2& o1, u32x2& o2);
 
+// Folded LayerNorm (p.ln_stats): the 4 accumulators of features n..n+3 of token m become
+// rstd * acc - rstd * mean * c + d, i.e. LN(x) . W (model.py:387 into 556), before any rounding.
+__device__ __forceinline__ void ln_fold_quad(const GemmParams& p, int m, int n, float (&a)[4]) {
+  const f32x2 st = m < p.M ? p.ln_stats[m] : f32x2{0.f, 0.f};
+  const f32x4 cd01 = *reinterpret_cast<const f32x4*>(p.ln_cd + n), cd23 = *reinterpret_cast<const f32x4*>(p.ln_cd + n + 2);
+  const float nm = -st.x * st.y;
+  a[0] = fmaf(a[0], st.y, fmaf(nm, cd01[0], cd01[1]));
+  a[1] = fmaf(a[1], st.y, fmaf(nm, cd01[2], cd01[3]));
+  a[2] = fmaf(a[2], st.y, fmaf(nm, cd23[0], cd23[1]));
+  a[3] = fmaf(a[3], st.y, fmaf(nm, cd23[2], cd23[3]));
+}
+
+// The fold on a workgroup's accumulators, applied where each epilogue reads them (acc[a][b][4 g + e]
+// is token m0 + wm TM + 32 b + l32, feature n0 + wn TN + 32 a + 8 g + 4 hh + e): the rows'
+// (rstd, -mean * rstd) are loaded once, then each 4-feature group takes its (c, d) from the LDS
+// copy as it is staged.
+template <int MB>
+struct LnRows {
+  float r[MB], nm[MB];
+};
+
+// lrs: the tile's rows' (rstd, -mean * rstd) in LDS (row m0 + i at lrs[i]), r_first: the lane's first row.
+template <int MB>
+__device__ __forceinline__ LnRows<MB> ln_rows(const f32x2* lrs, int r_first) {
+  LnRows<MB> L;
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const f32x2 v = lrs[r_first + 32 * b];
+    L.r[b] = v.x;
+    L.nm[b] = v.y;
+  }
+  return L;
+}
+
+// lcd: the tile's (c, d) pairs in LDS (column n0 + i at lcd[i], zeros past N), copied at kernel start.
+__device__ __forceinline__ void ln_fold_group(const f32x2* lcd, float r, float nm, int col, float (&v)[4]) {
+  const f32x4 cd01 = *reinterpret_cast<const f32x4*>(lcd + col), cd23 = *reinterpret_cast<const f32x4*>(lcd + col + 2);
+  v[0] = fmaf(v[0], r, fmaf(nm, cd01[0], cd01[1]));
+  v[1] = fmaf(v[1], r, fmaf(nm, cd01[2], cd01[3]));
+  v[2] = fmaf(v[2], r, fmaf(nm, cd23[0], cd23[1]));
+  v[3] = fmaf(v[3], r, fmaf(nm, cd23[2], cd23[3]));
+}
+
+
 // (cos, sin) of the 4 dims d..d+3 (< head_dim/2) of token m as (c_d, s_d, c_d+1, s_d+1) |
 // (c_d+2, s_d+2, c_d+3, s_d+3): from the per-token table p.cs, or from the per-position table
 // p.rtab (global memory) at the token's (h, w) ids. Tokens past M get anything (their outputs are
@@ -204,13 +248,16 @@ __device__ __forceinline__ void epi_rope_pair(const GemmParams& p, int m, int n,
 // so the 32 rows one ds_write_b64 touches land on distinct chunks; then the workgroup walks the
 // tile row by row, 16 bytes (8 features) per lane, and applies bias / GELU / residual with whole
 // rows per load and store instead of 8-byte pieces of 32 rows.
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
                                                   f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
-                                                  int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem) {
+                                                  int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem,
+                                                  const f32x2* lcd) {
   using S = GemmShape<BM, BN, WM, WN>;
   constexpr int CH = BN / 8;
   const int l32 = lane & 31, hh = lane >> 5;
+  LnRows<S::MB> L;
+  if constexpr (LN) L = ln_rows<S::MB>(lcd + BN, wm * S::TM + l32);
 #pragma unroll
   for (int a = 0; a < S::NB; ++a)
 #pragma unroll
@@ -219,8 +266,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
       for (int g = 0; g < 4; ++g) {
         const int r = wm * S::TM + b * 32 + l32;
         const int c = (wn * S::TN + a * 32) / 8 + g;
-        const u32x2 v = {pack_bf16x2(acc[a][b][4 * g], acc[a][b][4 * g + 1]),
-                         pack_bf16x2(acc[a][b][4 * g + 2], acc[a][b][4 * g + 3])};
+        float f[4] = {acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+        if constexpr (LN) ln_fold_group(lcd, L.r[b], L.nm[b], c * 8 + 4 * hh, f);
+        const u32x2 v = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])};
         *reinterpret_cast<u32x2*>(smem + r * BN + ((c ^ (r % CH)) << 3) + hh * 4) = v;
       }
   __syncthreads();
@@ -301,11 +349,11 @@ __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int 
 // bytes of [H][Np][64] (16 bytes per lane), and v goes out transposed to [H][64][Np] as 16-byte
 // runs of 8 key positions (gathered from the block with the vt_pos quad swap), instead of
 // 8-byte pieces of 32 rows (q, k) and 2-byte scattered stores (v).
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool LN>
 __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
                                                        f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
                                                        int m0, int n0, int wm, int wn, int lane, int wave, bf16* smem,
-                                                       const uint32_t* ltab) {
+                                                       const uint32_t* ltab, const f32x2* lcd) {
   using S = GemmShape<BM, BN, WM, WN>;
   constexpr int TM = S::TM, TN = S::TN, CPR = TN / 8, HPW = TN / 64;
   static_assert(TN % 64 == 0 && TM % 16 == 0, "the rotary epilogue needs whole heads and 16-token groups");
@@ -324,37 +372,66 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
 #pragma unroll
     for (int b = 0; b < S::MB; ++b) token_pos(p, base + b * 32 + l32, ph[b], pw[b]);
   }
+  LnRows<S::MB> L;
+  if constexpr (LN) L = ln_rows<S::MB>(lcd + BN, wm * S::TM + l32);
+  // one (head, 4 dims, token block) unit: bias, the folded LayerNorm (LN), rotary, into LDS
+  auto unit = [&](int h2, int g, int b, const f32x4& blo, const f32x4& bhi) {
+    const int d = 8 * g + 4 * hh, n = nw + h2 * 64 + d;
+    const int t = b * 32 + l32;
+    float lo[4], hi[4];
 #pragma unroll
-  for (int h2 = 0; h2 < HPW; ++h2)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 8 * g + 4 * hh, n = nw + h2 * 64 + d;
-      const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);      // once per (head, dims)
-      const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
-#pragma unroll
-      for (int b = 0; b < S::MB; ++b) {
-        const int t = b * 32 + l32;
-        float lo[4], hi[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
-        f32x4 c01 = {}, c23 = {};
-        if (which < 2) {
-          if (ltab) {
-            // dims d..d+3 lie in one half (d % 4 == 0, head_dim / 4 = 16): one 16-byte LDS read
-            uint32_t w[4];
-            const u32x4 q = *reinterpret_cast<const u32x4*>(ltab + (d < 16 ? ph[b] : pw[b]) * 16 + (d & 15));
-            w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
-            unpack_cs4(w, c01, c23);
-          } else {
-            rope_cs_global(p, base + t, d, c01, c23);
-          }
-        }
-        u32x2 o1, o2;
-        rope_values(p, which, base + t, d, blo, bhi, lo, hi, c01, c23, o1, o2);
-        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + g) + 4 * hh) = o1;
-        *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + 4 + g) + 4 * hh) = o2;
+    for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
+    if constexpr (LN) {
+      ln_fold_group(lcd, L.r[b], L.nm[b], n - n0, lo);
+      ln_fold_group(lcd, L.r[b], L.nm[b], n - n0 + 32, hi);
+    }
+    f32x4 c01 = {}, c23 = {};
+    if (which < 2) {
+      if (ltab) {
+        // dims d..d+3 lie in one half (d % 4 == 0, head_dim / 4 = 16): one 16-byte LDS read
+        uint32_t w[4];
+        const u32x4 q = *reinterpret_cast<const u32x4*>(ltab + (d < 16 ? ph[b] : pw[b]) * 16 + (d & 15));
+        w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+        unpack_cs4(w, c01, c23);
+      } else {
+        rope_cs_global(p, base + t, d, c01, c23);
       }
     }
+    u32x2 o1, o2;
+    rope_values(p, which, base + t, d, blo, bhi, lo, hi, c01, c23, o1, o2);
+    *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + g) + 4 * hh) = o1;
+    *reinterpret_cast<u32x2*>(reg + off(t, h2 * 8 + 4 + g) + 4 * hh) = o2;
+  };
+  auto bias_of = [&](int h2, int g, f32x4& blo, f32x4& bhi) {
+    const int n = nw + h2 * 64 + 8 * g + 4 * hh;
+    blo = *reinterpret_cast<const f32x4*>(p.bias + n);
+    bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 32);
+  };
+  if constexpr (LN) {
+    // token blocks outermost: a unit's (c, d) and bias are used once, so none stay live across
+    // units beside the accumulators
+#pragma unroll
+    for (int b = 0; b < S::MB; ++b)
+#pragma unroll
+      for (int h2 = 0; h2 < HPW; ++h2)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f32x4 blo, bhi;
+          bias_of(h2, g, blo, bhi);
+          unit(h2, g, b, blo, bhi);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+  } else {
+#pragma unroll
+    for (int h2 = 0; h2 < HPW; ++h2)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 blo, bhi;
+        bias_of(h2, g, blo, bhi);                 // once per (head, dims)
+#pragma unroll
+        for (int b = 0; b < S::MB; ++b) unit(h2, g, b, blo, bhi);
+      }
+  }
   // (a wave reads back only its own region; its LDS operations complete in order)
   if (which < 2) {
     bf16* dst = which == 0 ? p.q : p.k;
@@ -414,14 +491,16 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
 // at the vt_pos positions. Tokens in [M, Np) get zeros.
 constexpr int kR72 = 296;   // LDS row stride (elements) of the staged tile: 592 bytes, 16-byte multiple
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool LN>
 __device__ __forceinline__ void gemm_epilogue_rope72_lds(const GemmParams& p,
                                                          f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
                                                          int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem,
-                                                         const uint32_t* ltab) {
+                                                         const uint32_t* ltab, const f32x2* lcd) {
   using S = GemmShape<BM, BN, WM, WN>;
   static_assert(BN == 4 * 72 && BM % 8 == 0, "four 72-dim heads per tile");
   const int l32 = lane & 31, hh = lane >> 5;
+  LnRows<S::MB> L;
+  if constexpr (LN) L = ln_rows<S::MB>(lcd + BN, wm * S::TM + l32);
 #pragma unroll
   for (int a = 0; a < S::NB; ++a)
 #pragma unroll
@@ -430,8 +509,9 @@ __device__ __forceinline__ void gemm_epilogue_rope72_lds(const GemmParams& p,
       for (int g = 0; g < 4; ++g) {
         const int r = wm * S::TM + b * 32 + l32;
         const int c = wn * S::TN + a * 32 + 8 * g + 4 * hh;
-        *reinterpret_cast<u32x2*>(smem + r * kR72 + c) = u32x2{pack_bf16x2(acc[a][b][4 * g], acc[a][b][4 * g + 1]),
-                                                                 pack_bf16x2(acc[a][b][4 * g + 2], acc[a][b][4 * g + 3])};
+        float f[4] = {acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+        if constexpr (LN) ln_fold_group(lcd, L.r[b], L.nm[b], c, f);
+        *reinterpret_cast<u32x2*>(smem + r * kR72 + c) = u32x2{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])};
       }
   __syncthreads();
   const int which = n0 / p.D;                    // tiles never straddle q | k | v (D % 288 == 0)
@@ -519,10 +599,16 @@ __host__ __device__ constexpr int gemm_lds_elems() {
              ? 2 * GemmShape<BM, BN, WM, WN>::LDS_ELEMS
              : (EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN);
 }
+// Above the ring / staging area: for a folded LayerNorm (LN kernels) the tile's BN columns' (c, d)
+// then its BM rows' (rstd, -mean * rstd), 8 bytes each; then the rotary epilogues' per-position table.
 template <int BM, int BN, int WM, int WN, int EPI>
-__host__ __device__ constexpr int rope_tab_offset() { return (gemm_lds_elems<BM, BN, WM, WN, EPI>() + 7) / 8 * 8; }
+__host__ __device__ constexpr int ln_cd_offset() { return (gemm_lds_elems<BM, BN, WM, WN, EPI>() + 7) / 8 * 8; }
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
+__host__ __device__ constexpr int rope_tab_offset() {
+  return ln_cd_offset<BM, BN, WM, WN, EPI>() + (LN ? (BN + BM) * 4 : 0);
+}
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
   using S = GemmShape<BM, BN, WM, WN>;
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];   // [2][BM+BN][64]
@@ -582,10 +668,30 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   const uint32_t* ltab = nullptr;
   if constexpr (EPI == kEpiQkvRope || EPI == kEpiQkvRope72) {
     if (p.rtab && unit < 0) {
-      uint32_t* t = reinterpret_cast<uint32_t*>(smem + rope_tab_offset<BM, BN, WM, WN, EPI>());
+      uint32_t* t = reinterpret_cast<uint32_t*>(smem + rope_tab_offset<BM, BN, WM, WN, EPI, LN>());
       const int words = p.rtab_pos * (p.cs_half / 2);
       for (int i = tid; i < words; i += S::THREADS) t[i] = p.rtab[i];
       ltab = t;
+    }
+  }
+
+  // The folded LayerNorm's (c, d) of the tile's columns and (rstd, -mean * rstd) of its rows, copied
+  // once into LDS (published by the first barrier below, read by the epilogue); tail units write
+  // raw partials and skip it.
+  const f32x2* lcd = nullptr;
+  if constexpr (LN) {
+    if (unit < 0) {
+      f32x2* t = reinterpret_cast<f32x2*>(smem + ln_cd_offset<BM, BN, WM, WN, EPI>());
+      for (int i = tid; i < BN + BM; i += S::THREADS) {
+        if (i < BN) {
+          t[i] = n0 + i < p.N ? p.ln_cd[n0 + i] : f32x2{0.f, 0.f};
+        } else {
+          const int m = m0 + i - BN;
+          const f32x2 st = m < p.M ? p.ln_stats[m] : f32x2{0.f, 0.f};
+          t[i] = f32x2{st.y, -st.x * st.y};
+        }
+      }
+      lcd = t;
     }
   }
 
@@ -663,11 +769,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   }
   if constexpr (EPI == kEpiQkvRope) {
     __syncthreads();                    // every wave is done with the last stage
-    gemm_epilogue_rope_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, wave, smem, ltab);
+    gemm_epilogue_rope_lds<BM, BN, WM, WN, LN>(p, acc, m0, n0, wm, wn, lane, wave, smem, ltab, lcd);
   } else if constexpr (EPI == kEpiQkvRope72) {
-    gemm_epilogue_rope72_lds<BM, BN, WM, WN>(p, acc, m0, n0, wm, wn, lane, tid, smem, ltab);
+    gemm_epilogue_rope72_lds<BM, BN, WM, WN, LN>(p, acc, m0, n0, wm, wn, lane, tid, smem, ltab, lcd);
   } else {
-    gemm_epilogue_lds<BM, BN, WM, WN, EPI>(p, acc, m0, n0, wm, wn, lane, tid, smem);
+    gemm_epilogue_lds<BM, BN, WM, WN, EPI, LN>(p, acc, m0, n0, wm, wn, lane, tid, smem, lcd);
   }
 }
 
@@ -699,6 +805,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
 #pragma unroll
       for (int e = 0; e < 4; ++e) hi[e] += b[e];
     }
+  }
+  if (p.ln_stats && n < p.N) {
+    ln_fold_quad(p, m, n, lo);
+    if constexpr (EPI == kEpiQkvRope) ln_fold_quad(p, m, n + 32, hi);
   }
   if constexpr (EPI == kEpiQkvRope) epi_rope_pair(p, m, n, lo, hi);
   else epi_store_quad<EPI>(p, m, n, lo);
@@ -770,24 +880,25 @@ static int gemm_group_n(int tiles_n) {
   return std::max(1, std::min(g, tiles_n));
 }
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   using S = GemmShape<BM, BN, WM, WN>;
   constexpr bool kRope = EPI == kEpiQkvRope || EPI == kEpiQkvRope72;
   // rotary epilogues: room for the largest position table (rope_table_lds_bytes) after the ring
-  constexpr size_t lds_max = (size_t)rope_tab_offset<BM, BN, WM, WN, EPI>() * sizeof(bf16) +
-                             (kRope ? (EPI == kEpiQkvRope ? 16384 : 12288) : 0);
+  // (and the folded LayerNorm's (c, d))
+  constexpr size_t lds_max = (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16) +
+                             (kRope ? rope_table_lds_bytes(EPI == kEpiQkvRope ? 64 : 72, LN) : 0);
   static_assert(lds_max <= 163840, "LDS budget");
-  const size_t lds = p.rtab ? lds_max : (size_t)gemm_lds_elems<BM, BN, WM, WN, EPI>() * sizeof(bf16);
+  const size_t lds = p.rtab ? lds_max : (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16);
   // once per instantiation (a C++ function-local static: initialised exactly once, thread-safe)
-  static const hipError_t attr_rc = hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI>,
+  static const hipError_t attr_rc = hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI, LN>,
                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
   if (attr_rc != hipSuccess) return set_error(QVL_ERR_LAUNCH, "gemm_bf16: cannot reserve %zu bytes of LDS", lds_max);
   p.full_tiles = g.full;
   p.split = g.split;
   p.group_n = gemm_group_n((p.N + BN - 1) / BN);
   const int grid = g.full + g.tail * g.split;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI>), dim3(grid), dim3(S::THREADS), lds, stream, p);
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI, LN>), dim3(grid), dim3(S::THREADS), lds, stream, p);
   int rc = check_launch("gemm_bf16");
   if (rc || g.tail == 0) return rc;
   const int64_t items = (int64_t)g.tail * BM * ((EPI == kEpiQkvRope) ? BN / 8 : BN / 4);
@@ -806,7 +917,7 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.36e6,
                  kRate288x128 = 1.36e6;   // MACs/us/CU
 
-template <int EPI>
+template <int EPI, bool LN>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const int cus = gemm_device_cus();
   const ForcedPlan f = t_plan;
@@ -823,13 +934,13 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
     for (int i = 1; i < 4; ++i)
       if (cost[i] < cost[pick - 1]) pick = i + 1;
   }
-  if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI>(p, a, stream);
+  if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI, LN>(p, a, stream);
   if constexpr (EPI == kEpiQkvRope) {
-    return launch_gemm<256, 256, 4, 2, EPI>(p, b, stream);
+    return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
   } else {
-    if (pick == 2) return launch_gemm<256, 256, 4, 2, EPI>(p, b, stream);
-    if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI>(p, c, stream);
-    return launch_gemm<288, 128, 3, 4, EPI>(p, d, stream);
+    if (pick == 2) return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
+    if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
+    return launch_gemm<288, 128, 3, 4, EPI, LN>(p, d, stream);
   }
 }
 
@@ -847,16 +958,25 @@ constexpr double kRate256x288 = 1.50e6;
 
 static int dispatch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
   const GemmPlan g = plan_gemm<256, 288>(p, gemm_device_cus(), kRate256x288, -1);
-  return launch_gemm<256, 288, 4, 3, kEpiQkvRope72>(p, g, stream);
+  if (p.ln_stats) return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, true>(p, g, stream);
+  return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, false>(p, g, stream);
 }
 
+// A folded LayerNorm (p.ln_stats) selects the kernels instantiated with the fold (bias, GELU and
+// rotary epilogues: the Dense layers that follow a LayerNorm); the others carry no trace of it.
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream) {
+  const bool ln = p.ln_stats != nullptr;
+  if (ln && !p.ln_cd) return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: folded LayerNorm without (c, d)");
   switch (epi) {
     case kEpiQkvRope72: return dispatch_qkv_rope72(p, stream);
-    case kEpiBias: return dispatch_gemm<kEpiBias>(p, stream);
-    case kEpiBiasGelu: return dispatch_gemm<kEpiBiasGelu>(p, stream);
-    case kEpiBiasResidual: return dispatch_gemm<kEpiBiasResidual>(p, stream);
-    case kEpiQkvRope: return dispatch_gemm<kEpiQkvRope>(p, stream);
+    case kEpiBias: return ln ? dispatch_gemm<kEpiBias, true>(p, stream) : dispatch_gemm<kEpiBias, false>(p, stream);
+    case kEpiBiasGelu:
+      return ln ? dispatch_gemm<kEpiBiasGelu, true>(p, stream) : dispatch_gemm<kEpiBiasGelu, false>(p, stream);
+    case kEpiBiasResidual:
+      if (ln) return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: no folded LayerNorm with the residual epilogue");
+      return dispatch_gemm<kEpiBiasResidual, false>(p, stream);
+    case kEpiQkvRope:
+      return ln ? dispatch_gemm<kEpiQkvRope, true>(p, stream) : dispatch_gemm<kEpiQkvRope, false>(p, stream);
   }
   return set_error(QVL_ERR_INVALID_ARG, "unknown epilogue %d", epi);
 }

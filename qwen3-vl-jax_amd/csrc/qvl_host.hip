@@ -46,7 +46,8 @@ int qvl_cast(void* stream, int32_t dtype, const float* x, void* y, int64_t n) {
 
 static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
                       const float* bias, const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n,
-                      int64_t k, void* ws, size_t ws_bytes) {
+                      int64_t k, void* ws, size_t ws_bytes, const float* ln_cd = nullptr,
+                      const float* ln_stats = nullptr) {
   if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_UNSUPPORTED, "dense: dtype %d", dtype);
   if (epi < QVL_EPI_BIAS || epi > QVL_EPI_BIAS_RESIDUAL) return set_error(QVL_ERR_INVALID_ARG, "dense: epilogue %d", epi);
   if (m < 0 || n <= 0 || k <= 0) return set_error(QVL_ERR_INVALID_ARG, "dense: m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
@@ -80,6 +81,8 @@ static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, i
   p.res = (const bf16*)res; p.ldr = ldr; p.y = (bf16*)y; p.ldc = ldc;
   p.M = (int)m; p.N = (int)n; p.K = (int)k;
   p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
+  p.ln_stats = (const f32x2*)ln_stats;
+  p.ln_cd = (const f32x2*)ln_cd;
   return gemm_bf16(p, epi, (hipStream_t)stream);
 }
 
@@ -102,6 +105,41 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epi, const void* x, int64_
                  const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n, int64_t k, void* ws,
                  size_t ws_bytes) {
   return dense_impl(stream, dtype, epi, x, lda, w, bias, res, ldr, y, ldc, m, n, k, ws, ws_bytes);
+}
+
+int qvl_row_stats(void* stream, int32_t dtype, const void* x, int64_t ldx, int64_t rows, int64_t cols, float eps,
+                  float* stats) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "row_stats: dtype %d (bf16 only)", dtype);
+  if (rows < 0 || cols <= 0 || cols % 8 || cols > 8192 || ldx < cols || rows > INT32_MAX)
+    return set_error(QVL_ERR_INVALID_ARG, "row_stats: rows=%lld cols=%lld", (long long)rows, (long long)cols);
+  if (rows == 0) return QVL_OK;
+  if (!x || !stats) return set_error(QVL_ERR_INVALID_ARG, "row_stats: NULL operand");
+  if (!aligned16(x) || ldx % 8 || ((uintptr_t)stats & 7)) return set_error(QVL_ERR_MISALIGNED, "row_stats: alignment");
+  return row_stats_bf16((const bf16*)x, ldx, (int)rows, (int)cols, eps, (f32x2*)stats, (hipStream_t)stream);
+}
+
+int qvl_fold_ln_weight(void* stream, int32_t dtype, const void* w, int64_t k_in, int64_t n_out, const float* gamma,
+                       const float* beta, void* out_w, float* out_cd) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "fold_ln_weight: dtype %d (bf16 only)", dtype);
+  if (k_in <= 0 || k_in % 64 || n_out <= 0 || k_in > INT32_MAX || round_up(n_out, 64) > INT32_MAX)
+    return set_error(QVL_ERR_INVALID_ARG, "fold_ln_weight: k_in=%lld (a multiple of 64) n_out=%lld", (long long)k_in,
+                     (long long)n_out);
+  if (!w || !gamma || !beta || !out_w || !out_cd) return set_error(QVL_ERR_INVALID_ARG, "fold_ln_weight: NULL operand");
+  if (!aligned16(w) || !aligned16(gamma) || !aligned16(beta) || !aligned16(out_w) || !aligned16(out_cd))
+    return set_error(QVL_ERR_MISALIGNED, "fold_ln_weight: operands must be 16-byte aligned");
+  return fold_ln_weight_bf16((const bf16*)w, k_in, round_up(n_out, 64), gamma, beta, (bf16*)out_w, (f32x2*)out_cd,
+                             (hipStream_t)stream);
+}
+
+int qvl_dense_ln_ws(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
+                    const float* cd, const float* stats, const float* bias, void* y, int64_t ldc, int64_t m, int64_t n,
+                    int64_t k, void* ws, size_t ws_bytes) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense_ln: dtype %d (bf16 only)", dtype);
+  if (epi != QVL_EPI_BIAS && epi != QVL_EPI_BIAS_GELU)
+    return set_error(QVL_ERR_INVALID_ARG, "dense_ln: epilogue %d (bias or bias+GELU)", epi);
+  if (m > 0 && (!cd || !stats)) return set_error(QVL_ERR_INVALID_ARG, "dense_ln: NULL folded LayerNorm operand");
+  if (((uintptr_t)cd & 15) || ((uintptr_t)stats & 7)) return set_error(QVL_ERR_MISALIGNED, "dense_ln: alignment");
+  return dense_impl(stream, dtype, epi, x, lda, w, bias, nullptr, 0, y, ldc, m, n, k, ws, ws_bytes, cd, stats);
 }
 
 int qvl_layer_norm(void* stream, int32_t dtype, const void* x, int64_t ldx, const float* g, const float* b, void* y,
@@ -218,7 +256,8 @@ int qvl_rotary_pos_table(void* stream, int32_t head_dim, float theta, int32_t n_
 
 static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
                            const void* cs, const int32_t* pos_hw, const uint32_t* rtab, int32_t n_pos, void* q,
-                           void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H, void* ws, size_t ws_bytes) {
+                           void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H, void* ws, size_t ws_bytes,
+                           const float* ln_cd = nullptr, const float* ln_stats = nullptr) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: dtype %d", dtype);
   if (H <= 0 || (hidden != (int64_t)H * 64 && hidden != (int64_t)H * 72))
     return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64 or 72");
@@ -229,9 +268,9 @@ static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t l
   if (n_tokens == 0) return QVL_OK;
   if (!x || !w || !bias || !q || !k || !vt || (!cs && (!pos_hw || !rtab)))
     return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
-  if (rtab && (n_pos <= 0 || (int64_t)n_pos * (hd / 4) * 4 > rope_table_lds_bytes(hd)))
+  if (rtab && (n_pos <= 0 || (int64_t)n_pos * (hd / 4) * 4 > rope_table_lds_bytes(hd, ln_stats != nullptr)))
     return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: %d rotary positions exceed the %d-byte table of head_dim %d",
-                     n_pos, rope_table_lds_bytes(hd), hd);
+                     n_pos, rope_table_lds_bytes(hd, ln_stats != nullptr), hd);
   if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(q) || !aligned16(k) || !aligned16(vt) ||
       (cs && !aligned16(cs)) || (rtab && !aligned16(rtab)))
     return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: alignment");
@@ -249,6 +288,8 @@ static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t l
   p.qscale = (1.0f / sqrtf((float)hd)) * kLog2e;
   if (ws && !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: workspace alignment");
   p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
+  p.ln_stats = (const f32x2*)ln_stats;
+  p.ln_cd = (const f32x2*)ln_cd;
   return gemm_bf16(p, hd == 64 ? kEpiQkvRope : kEpiQkvRope72, (hipStream_t)stream);
 }
 
@@ -266,6 +307,18 @@ int qvl_dense_qkv_rotary_pos(void* stream, int32_t dtype, const void* x, int64_t
   if (n_tokens > 0 && (!pos_hw || !table)) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary_pos: NULL positions/table");
   return qkv_rotary_impl(stream, dtype, x, lda, w, bias, nullptr, pos_hw, table, n_positions, q, k, vt, n_tokens,
                          hidden, H, ws, ws_bytes);
+}
+
+int qvl_dense_qkv_rotary_ln(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* cd,
+                            const float* stats, const float* bias, const void* cs, const int32_t* pos_hw,
+                            const uint32_t* table, int32_t n_positions, void* q, void* k, void* vt, int64_t n_tokens,
+                            int64_t hidden, int32_t H, void* ws, size_t ws_bytes) {
+  if (n_tokens > 0 && (!cd || !stats)) return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary_ln: NULL folded LayerNorm operand");
+  if (((uintptr_t)cd & 15) || ((uintptr_t)stats & 7)) return set_error(QVL_ERR_MISALIGNED, "qkv_rotary_ln: alignment");
+  if (n_tokens > 0 && (cs ? (pos_hw || table) : (!pos_hw || !table)))
+    return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary_ln: give either the per-token cos/sin table or positions + table");
+  return qkv_rotary_impl(stream, dtype, x, lda, w, bias, cs, cs ? nullptr : pos_hw, cs ? nullptr : table,
+                         cs ? 0 : n_positions, q, k, vt, n_tokens, hidden, H, ws, ws_bytes, cd, stats);
 }
 
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
@@ -329,7 +382,7 @@ struct TowerLayout {
   size_t esz;
   int64_t N, Np, D, I_pad, PV, hd, H;
   int hdp, vrows;
-  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, off_apart, apart_bytes, total;
+  size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, off_apart, off_stats, apart_bytes, total;
 };
 
 // Upper bound on the parts of split attention items one work list holds (qvl_attention_
@@ -381,6 +434,8 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   // partial outputs of split attention items: at most one per workgroup slot (4 per CU)
   L->apart_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)attn_split_slots_bound() * attn_partial_floats((int)hd) * 4 : 0;
   L->off_apart = take(L->apart_bytes);
+  // (mean, rstd) per row of the LayerNorms folded into the following Dense (bf16)
+  L->off_stats = c->dtype == QVL_DTYPE_BF16 ? take((size_t)N * 8) : 0;
   L->total = o;
   return QVL_OK;
 }
@@ -397,16 +452,24 @@ int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tok
 
 // VisionPatchMerger.__call__ (model.py:648-656): main (LN over D then view [N/4, 4D]) or
 // deepstack (view [N/4, 4D] then LN over 4D); fc1 + GELU-tanh; fc2.
+// A deepstack merger in bf16 with its norm folded into fc1 runs qvl_row_stats + qvl_dense_ln_ws instead of
+// the LayerNorm launch.
 static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLayout& L, const qvl_merger_weights& mw,
-                      bool postshuffle, const void* x, void* xn, void* h, void* out, void* part) {
+                      bool postshuffle, const void* x, void* xn, void* h, void* out, void* part, float* stats) {
   const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
   const int dt = L.dtype;
-  if (postshuffle)
-    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
-  else
-    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
-  QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4,
-                          part, L.part_bytes));
+  if (postshuffle && dt == QVL_DTYPE_BF16 && mw.fc1_ln.w && mw.fc1_ln.cd && stats) {
+    QVL_TRY_RC(qvl_row_stats(st, dt, x, D4, N / 4, D4, c->ln_eps, stats));
+    QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS_GELU, x, D4, mw.fc1_ln.w, mw.fc1_ln.cd, stats, mw.fc1_b, h, D4,
+                               N / 4, D4, D4, part, L.part_bytes));
+  } else {
+    if (postshuffle)
+      QVL_TRY_RC(qvl_layer_norm(st, dt, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
+    else
+      QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, mw.norm_w, mw.norm_b, xn, D, N, D, c->ln_eps));
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D4, mw.fc1_w, mw.fc1_b, nullptr, 0, h, D4, N / 4, D4, D4,
+                            part, L.part_bytes));
+  }
   QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, h, D4, mw.fc2_w, mw.fc2_b, nullptr, 0, out, c->out_hidden_size, N / 4,
                           c->out_hidden_size, D4, part, L.part_bytes));
   return QVL_OK;
@@ -435,6 +498,7 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   char* h = base + L.off_h;
   f32x2* cs = (f32x2*)(base + L.off_cs);
   void* part = L.part_bytes ? base + L.off_part : nullptr;
+  float* stats = f32 ? nullptr : (float*)(base + L.off_stats);
   const size_t PB = L.part_bytes;
   const int64_t N = L.N, D = L.D, I = L.I_pad;
   const size_t e = L.esz;
@@ -467,8 +531,11 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   // LDS table (measured on MI355X at config 2: 126.6 vs 127.9 us per qkv launch; at head_dim 72
   // the table's 4-byte LDS reads were slower than the per-token loads, 89.3 vs 86.5 us)
   const bool fused_qkv = fused_qkv_rotary(dt, (int)L.hd, (int)L.H);
+  // (the folded-LayerNorm kernels leave the table 2 KB less; sized for the tower's first block)
+  const bool fold0 = !f32 && c->depth > 0 && W->blocks[0].qkv_ln.w && W->blocks[0].qkv_ln.cd &&
+                     W->blocks[0].fc1_ln.w && W->blocks[0].fc1_ln.cd;
   const bool pos_tab = fused_qkv && L.hd == 64 && meta->n_positions > 0 &&
-                       meta->n_positions * (L.hd / 4) * 4 <= rope_table_lds_bytes((int)L.hd);
+                       meta->n_positions * (L.hd / 4) * 4 <= rope_table_lds_bytes((int)L.hd, fold0);
   if (pos_tab)
     QVL_TRY_RC(qvl_rotary_pos_table(st, (int)L.hd, c->rope_theta, (int)meta->n_positions, (uint32_t*)cs));
   else
@@ -485,9 +552,19 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   int ds_next = 0;
   for (int i = 0; i < c->depth; ++i) {
     const qvl_block_weights& B = W->blocks[i];
+    // bf16: norm1 / norm2 folded into the qkv / fc1 GEMMs (the Dense reads x itself; only the row
+    // statistics run before it)
+    const bool fold = !f32 && B.qkv_ln.w && B.qkv_ln.cd && B.fc1_ln.w && B.fc1_ln.cd;
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
-    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
-    if (fused_qkv) {
+    if (fold)
+      QVL_TRY_RC(qvl_row_stats(st, dt, x, D, N, D, c->ln_eps, stats));
+    else
+      QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
+    if (fused_qkv && fold) {
+      QVL_TRY_RC(qvl_dense_qkv_rotary_ln(st, dt, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, B.qkv_b, pos_tab ? nullptr : cs,
+                                         pos_tab ? meta->pos_hw : nullptr, pos_tab ? (const uint32_t*)cs : nullptr,
+                                         pos_tab ? (int)meta->n_positions : 0, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
+    } else if (fused_qkv) {
       // qkv Dense with rotary + head-major relayout fused into its epilogue.
       if (pos_tab)
         QVL_TRY_RC(qvl_dense_qkv_rotary_pos(st, dt, xn, D, B.qkv_w, B.qkv_b, meta->pos_hw, (const uint32_t*)cs,
@@ -496,8 +573,12 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
         QVL_TRY_RC(qvl_dense_qkv_rotary(st, dt, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
     } else {
       // qkv Dense into h, then rotary + head-major relayout.
-      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D, D, part,
-                              PB));
+      if (fold)
+        QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, B.qkv_b, h, 3 * D, N,
+                                   3 * D, D, part, PB));
+      else
+        QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, xn, D, B.qkv_w, B.qkv_b, nullptr, 0, h, 3 * D, N, 3 * D, D, part,
+                                PB));
       if (f32)
         QVL_TRY_RC(attention_relayout_f32((const float*)h, (const float*)h + D, (const float*)h + 2 * D, 3 * D, cs,
                                           (int)N, (int)L.Np, (int)L.H, (int)L.hd, L.vrows, qscale, (float*)Qb,
@@ -520,21 +601,27 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     }
     QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, part, PB));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
-    QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
-    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D, part, PB));
+    if (fold) {
+      QVL_TRY_RC(qvl_row_stats(st, dt, x, D, N, D, c->ln_eps, stats));
+      QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS_GELU, x, D, B.fc1_ln.w, B.fc1_ln.cd, stats, B.fc1_b, h, I, N, I,
+                                 D, part, PB));
+    } else {
+      QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
+      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D, part, PB));
+    }
     QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I, part, PB));
     // deepstack tap (model.py:841-843)
     for (int j = 0; j < c->n_deepstack; ++j)
       if (c->deepstack_indexes[j] == i) {
         void* out = win ? (void*)Qb : deepstack[ds_next];
-        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, out, part));
+        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, out, part, stats));
         if (win)   // unshuffle (model.py:845-848)
           QVL_TRY_RC(qvl_gather_rows(st, dt, Qb, Dout, dt, deepstack[ds_next], Dout, meta->window_reverse, N / 4, 1, Dout));
         ++ds_next;
       }
   }
   (void)e;
-  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, win ? (void*)Qb : tokens, part));
+  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, win ? (void*)Qb : tokens, part, stats));
   if (win) QVL_TRY_RC(qvl_gather_rows(st, dt, Qb, Dout, dt, tokens, Dout, meta->window_reverse, N / 4, 1, Dout));
   return QVL_OK;
 }

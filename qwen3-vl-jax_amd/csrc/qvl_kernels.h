@@ -35,6 +35,11 @@ struct GemmParams {
   int64_t part_elems;
   int full_tiles, split;
   int group_n;                   // tile order: panels of group_n column tiles (set by the launcher)
+  // LayerNorm folded into this Dense (ln_stats != NULL): x holds the un-normalised rows, w the
+  // folded kernel W' = bf16(gamma W), ln_stats[m] = (mean, rstd) of row m and ln_cd[n] = (c, d);
+  // the accumulator becomes rstd * acc - rstd * mean * c + d before the epilogue.
+  const f32x2* ln_stats;
+  const f32x2* ln_cd;
 };
 
 // fp32 GEMM (qvl_f32.hip): w packed [n_rows_w][ldw] fp32 (ldw = k padded to 64), Kp = ldw.
@@ -65,8 +70,11 @@ __host__ __device__ __forceinline__ int vt_pos(int m) {
 }
 
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream);
-// LDS bytes the qkv rotary epilogue can give to a per-position rotary table (head_dim 64 / 72).
-inline int rope_table_lds_bytes(int hd) { return hd == 64 ? 16384 : 12288; }
+// LDS bytes the qkv rotary epilogue can give to a per-position rotary table (head_dim 64 / 72),
+// with a folded LayerNorm (ln: its (c, d) and row statistics take 4.3 KB of the 160 KB) or without.
+__host__ __device__ constexpr int rope_table_lds_bytes(int hd, bool ln = false) {
+  return hd == 64 ? (ln ? 12032 : 16384) : (ln ? 7936 : 12288);
+}
 int rotary_pos_table(int n_pos, int head_dim, const float* inv_freq, uint32_t* table, hipStream_t stream);
 int gemm_set_plan(int tile, int split_mode, int group_n);
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
@@ -83,6 +91,9 @@ int layer_norm_bf16(const bf16* x, int64_t ldx, const float* g, const float* b, 
                     int cols, float eps, hipStream_t stream);
 int pos_embed_bf16(const bf16* table, const int* idx, const float* wts, bf16* y, int n_tok, int dim,
                    hipStream_t stream);
+int row_stats_bf16(const bf16* x, int64_t ldx, int rows, int cols, float eps, f32x2* stats, hipStream_t stream);
+int fold_ln_weight_bf16(const bf16* w, int64_t k, int64_t n_pad, const float* gamma, const float* beta, bf16* out,
+                        f32x2* cd, hipStream_t stream);
 int rotary_table(const int* pos_hw, int n_tok, int head_dim, const float* inv_freq, int round16, f32x2* cs,
                  hipStream_t stream);
 int cast_f32_bf16(const float* x, bf16* y, int64_t n, hipStream_t stream);

@@ -136,6 +136,129 @@ int layer_norm_bf16(const bf16* x, int64_t ldx, const float* g, const float* b, 
 }
 
 // ---------------------------------------------------------------------------------------------
+// LayerNorm statistics alone (model.py:384-386) for a LayerNorm folded into the Dense that consumes
+// it: stats[row] = (mean, rsqrt(var + eps)) with the same exact two-pass fp32 arithmetic as
+// layernorm_bf16_kernel, one wave per row walking rows with the next row's loads in flight. It
+// reads the rows once and writes 8 bytes per row (LayerNorm itself also writes the normalised rows).
+// ---------------------------------------------------------------------------------------------
+template <int CH>
+__global__ __launch_bounds__(256) void rowstats_bf16_kernel(const bf16* __restrict__ x, int64_t ldx, int rows,
+                                                            int cols, float eps, f32x2* __restrict__ stats) {
+  const int lane = threadIdx.x & 63;
+  const int stride = gridDim.x * 4;
+  const int nch = cols >> 3;
+  const float inv_n = 1.0f / (float)cols;
+  auto load_row = [&](int r, u32x4* dst) {
+    const bf16* xr = x + (int64_t)r * ldx;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = lane + 64 * i;
+      dst[i] = (c < nch) ? *reinterpret_cast<const u32x4*>(xr + c * 8) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  u32x4 nxt[CH];
+  if (row < rows) load_row(row, nxt);
+  for (; row < rows; row += stride) {
+    float v[CH][8];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const u32x4 w = nxt[i];
+      v[i][0] = bf16_lo(w.x); v[i][1] = bf16_hi(w.x); v[i][2] = bf16_lo(w.y); v[i][3] = bf16_hi(w.y);
+      v[i][4] = bf16_lo(w.z); v[i][5] = bf16_hi(w.z); v[i][6] = bf16_lo(w.w); v[i][7] = bf16_hi(w.w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[i][e];      // chunks past the row end hold zeros
+    }
+    if (row + stride < rows) load_row(row + stride, nxt);
+    const float mean = wave_sum(s) * inv_n;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
+      }
+    }
+    const float var = wave_sum(q) * inv_n;
+    if (lane == 0) stats[row] = f32x2{mean, rsqrtf(var + eps)};
+  }
+}
+
+template <int CH>
+static int launch_rowstats(const bf16* x, int64_t ldx, int rows, int cols, float eps, f32x2* stats,
+                           hipStream_t stream) {
+  const int grid = std::min((rows + 3) / 4, 4 * gemm_device_cus());
+  hipLaunchKernelGGL(rowstats_bf16_kernel<CH>, dim3(grid), dim3(256), 0, stream, x, ldx, rows, cols, eps, stats);
+  return check_launch("rowstats_bf16");
+}
+
+int row_stats_bf16(const bf16* x, int64_t ldx, int rows, int cols, float eps, f32x2* stats, hipStream_t stream) {
+  if (rows == 0) return QVL_OK;
+  switch ((cols / 8 + 63) / 64) {
+    case 1: return launch_rowstats<1>(x, ldx, rows, cols, eps, stats, stream);
+    case 2: return launch_rowstats<2>(x, ldx, rows, cols, eps, stats, stream);
+    case 3: return launch_rowstats<3>(x, ldx, rows, cols, eps, stats, stream);
+    case 4: return launch_rowstats<4>(x, ldx, rows, cols, eps, stats, stream);
+    case 5: case 6: return launch_rowstats<6>(x, ldx, rows, cols, eps, stats, stream);
+    case 7: case 8: return launch_rowstats<8>(x, ldx, rows, cols, eps, stats, stream);
+    case 9: return launch_rowstats<9>(x, ldx, rows, cols, eps, stats, stream);
+    case 10: case 11: case 12: return launch_rowstats<12>(x, ldx, rows, cols, eps, stats, stream);
+    case 13: case 14: case 15: case 16: return launch_rowstats<16>(x, ldx, rows, cols, eps, stats, stream);
+  }
+  return set_error(QVL_ERR_UNSUPPORTED, "row_stats: cols=%d unsupported (max 8192)", cols);
+}
+
+// ---------------------------------------------------------------------------------------------
+// LayerNorm folded into the next Dense: with xn = (x - mean) r gamma + beta (model.py:387),
+//   xn . W[n] = r (x . W'[n]) - r mean c[n] + d[n],  W'[n][k] = bf16(gamma[k] W[n][k]),
+//   c[n] = sum_k W'[n][k],  d[n] = sum_k beta[k] W[n][k].
+// From the packed kernel w [n_pad][k] (bf16, K contiguous): out [n_pad][k] = W', cd[n] = (c, d);
+// padding rows give zeros. One wave per output feature, fp32 sums.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fold_ln_weight_kernel(const bf16* __restrict__ w, int k, int n_pad,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, bf16* __restrict__ out,
+                                                             f32x2* __restrict__ cd) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= n_pad) return;
+  const bf16* wr = w + (int64_t)n * k;
+  bf16* orow = out + (int64_t)n * k;
+  float c = 0.f, d = 0.f;
+  for (int j = lane * 8; j < k; j += 512) {
+    const u32x4 u = *reinterpret_cast<const u32x4*>(wr + j);
+    const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + j), g1 = *reinterpret_cast<const f32x4*>(gamma + j + 4);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + j), b1 = *reinterpret_cast<const f32x4*>(beta + j + 4);
+    const float wv[8] = {bf16_lo(u.x), bf16_hi(u.x), bf16_lo(u.y), bf16_hi(u.y),
+                         bf16_lo(u.z), bf16_hi(u.z), bf16_lo(u.w), bf16_hi(u.w)};
+    const float gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    const float bv[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      f[e] = round_bf16(gv[e] * wv[e]);
+      c += f[e];
+      d = fmaf(bv[e], wv[e], d);
+    }
+    *reinterpret_cast<u32x4*>(orow + j) = u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                                                pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
+  }
+  c = wave_sum(c);
+  d = wave_sum(d);
+  if (lane == 0) cd[n] = f32x2{c, d};
+}
+
+int fold_ln_weight_bf16(const bf16* w, int64_t k, int64_t n_pad, const float* gamma, const float* beta, bf16* out,
+                        f32x2* cd, hipStream_t stream) {
+  if (n_pad == 0) return QVL_OK;
+  hipLaunchKernelGGL(fold_ln_weight_kernel, dim3((unsigned)((n_pad + 3) / 4)), dim3(256), 0, stream, w, (int)k,
+                     (int)n_pad, gamma, beta, out, cd);
+  return check_launch("fold_ln_weight");
+}
+
+// ---------------------------------------------------------------------------------------------
 // Pos-embed bilinear gather (model.py:751-764): one wave per token, 4 table rows weighted, in
 // the reference's bf16 arithmetic: each tap product rounded to bf16, the sum taken left to right
 // ((t0 + t1) + t2) + t3 with each partial sum rounded (eager jnp ops, model.py:751-752). Taps

@@ -321,7 +321,7 @@ class Qwen3VisionTransformer:
     META_CACHE_SIZE = 16   # grids whose device metadata stays cached (LRU)
 
     def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0",
-                 split_attention: bool = True):
+                 split_attention: bool = True, ln_fold: bool = False):
         if dtype not in ("bfloat16", "float32"):
             raise NotImplementedError(f"dtype {dtype!r}: the tower runs in bfloat16 or float32")
         if spec.spatial_merge_size != 2:
@@ -333,6 +333,13 @@ class Qwen3VisionTransformer:
         # bf16 full attention runs a qvl_attention_worklist_split list (the last round's items split
         # along keys) when true
         self.split_attention = split_attention
+        # ln_fold (bf16): each block's norm1 / norm2 and the deepstack mergers' post-shuffle norms
+        # are folded into the Dense after them (qvl_fold_ln_weight at bind time; qvl_row_stats + the
+        # folded GEMM at run time instead of a LayerNorm launch). Off by default: on MI355X the
+        # fold's epilogue work costs more than the LayerNorm launches it removes (same-box A/B at
+        # config 2: 17.83 vs 17.76 ms per forward).
+        self.ln_fold = bool(ln_fold) and self.qdtype == capi.QVL_DTYPE_BF16
+        self._folds: Dict[str, tuple] = {}
         self._lib = capi.load()
         self._w = None
         self._keep = []
@@ -392,6 +399,17 @@ class Qwen3VisionTransformer:
         b = np.zeros(npad, np.float32)
         b[:nout] = np.asarray(p["bias"], np.float32)
         return out, self._round(torch.from_numpy(b).to(self.device))
+
+    def _fold(self, w, gamma, beta):
+        """(W', cd) of a LayerNorm (gamma, beta) folded into the packed Dense kernel w [n_pad, k]:
+        W' = bf16(gamma * W) and (c, d) per output feature (qvl_fold_ln_weight)."""
+        torch = _torch()
+        n_pad, k = w.shape
+        out = torch.empty_like(w)
+        cd = torch.empty((n_pad, 2), dtype=torch.float32, device=self.device)
+        capi.check(self._lib.qvl_fold_ln_weight(self._stream(), self.qdtype, w.data_ptr(), k, n_pad, gamma.data_ptr(),
+                                                beta.data_ptr(), out.data_ptr(), cd.data_ptr()), "qvl_fold_ln_weight")
+        return out, cd
 
     def _vec(self, v):
         torch = _torch()
@@ -496,12 +514,25 @@ class Qwen3VisionTransformer:
                 setattr(bw, name + "_w", p(f"blocks.{i}.{name}.w"))
                 setattr(bw, name + "_b", p(f"blocks.{i}.{name}.b"))
         W.blocks = blocks
+        folds: Dict[str, tuple] = {}
+        if self.ln_fold:
+            for i in range(s.depth):
+                for name, norm in (("qkv", "norm1"), ("fc1", "norm2")):
+                    f = self._fold(st[f"blocks.{i}.{name}.w"], st[f"blocks.{i}.{norm}.w"], st[f"blocks.{i}.{norm}.b"])
+                    folds[f"blocks.{i}.{name}"] = f
+                    fl = getattr(blocks[i], name + "_ln")
+                    fl.w, fl.cd = f[0].data_ptr(), f[1].data_ptr()
+            for j in range(len(s.deepstack_visual_indexes)):
+                folds[f"deepstack.{j}.fc1"] = self._fold(st[f"deepstack.{j}.fc1.w"], st[f"deepstack.{j}.norm.w"],
+                                                         st[f"deepstack.{j}.norm.b"])
 
         def merger(name):
             mw = capi.MergerWeights()
             mw.norm_w, mw.norm_b = p(name + ".norm.w"), p(name + ".norm.b")
             mw.fc1_w, mw.fc1_b, mw.fc2_w, mw.fc2_b = p(name + ".fc1.w"), p(name + ".fc1.b"), p(name + ".fc2.w"), p(
                 name + ".fc2.b")
+            if name + ".fc1" in folds:
+                mw.fc1_ln.w, mw.fc1_ln.cd = folds[name + ".fc1"][0].data_ptr(), folds[name + ".fc1"][1].data_ptr()
             return mw
 
         W.merger = merger("merger")
@@ -511,7 +542,8 @@ class Qwen3VisionTransformer:
             ds[j] = merger(f"deepstack.{j}")
         W.deepstack = ds
         self._state = st
-        self._keep = list(st.values())
+        self._folds = folds
+        self._keep = list(st.values()) + [t for f in folds.values() for t in f]
         self._blocks_arr, self._ds_arr = blocks, ds
         self._w = W
         return self
@@ -671,6 +703,7 @@ class Qwen3VisionTransformer:
                                                                     C.byref(ab)), "attention split ws")
         ctx["apart"] = torch.empty(max(ab.value, 256), dtype=torch.uint8, **dev)
         ctx["apart_bytes"] = ab.value
+        ctx["stats"] = torch.empty((N, 2), dtype=torch.float32, **dev)     # folded LayerNorms' (mean, rstd)
         # (cos, sin) per rotary position, as the tower looks them up when the grid's positions fit
         n_pos = ctx["m"].n_positions
         cap = 16384 if hd == 64 else 12288
@@ -686,7 +719,9 @@ class Qwen3VisionTransformer:
         rotary (qvl_dense_qkv_rotary, head-major Q/K/V^T), attention on the tower's work list
         (qvl_attention_headmajor_split when the tower builds a split list, else
         qvl_attention_headmajor), proj + residual, LayerNorm, fc1 + GELU, fc2 + residual, the
-        GEMMs with the tower's split-K workspace."""
+        GEMMs with the tower's split-K workspace. With ln_fold each LayerNorm is qvl_row_stats and
+        the Dense after it the folded entry (qvl_dense_qkv_rotary_ln, qvl_dense_ln_ws), as in the
+        tower."""
         ctx = self._fused_ctx(ctx)
         lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
         N, D, H, hd, I = ctx["N"], ctx["D"], ctx["H"], ctx["hd"], ctx["I"]
@@ -695,14 +730,26 @@ class Qwen3VisionTransformer:
         gws, gwn = ctx["gws"].data_ptr(), ctx["gws_bytes"]
         md = ctx["md"]
         B = self._blocks_arr[i]
-        ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
-        if "rtab" in ctx:
-            ck(lib.qvl_dense_qkv_rotary_pos(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["tens"]["pos_hw"].data_ptr(),
-                                            ctx["rtab"].data_ptr(), ctx["rtab"].shape[0], qb, kb, vb, N, D, H, gws,
-                                            gwn), "qkv_rotary_pos")
+        fold = self.ln_fold
+        if fold:
+            stats = ctx["stats"].data_ptr()
+            fq, ff = self._folds[f"blocks.{i}.qkv"], self._folds[f"blocks.{i}.fc1"]
+            ck(lib.qvl_row_stats(st, dt, x.data_ptr(), D, N, D, 1e-6, stats), "ln1 stats")
+            rt = "rtab" in ctx
+            ck(lib.qvl_dense_qkv_rotary_ln(st, dt, x.data_ptr(), D, fq[0].data_ptr(), fq[1].data_ptr(), stats, B.qkv_b,
+                                           None if rt else ctx["cs"].data_ptr(),
+                                           ctx["tens"]["pos_hw"].data_ptr() if rt else None,
+                                           ctx["rtab"].data_ptr() if rt else None, ctx["rtab"].shape[0] if rt else 0,
+                                           qb, kb, vb, N, D, H, gws, gwn), "qkv_rotary_ln")
         else:
-            ck(lib.qvl_dense_qkv_rotary(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb, N,
-                                        D, H, gws, gwn), "qkv_rotary")
+            ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
+            if "rtab" in ctx:
+                ck(lib.qvl_dense_qkv_rotary_pos(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b,
+                                                ctx["tens"]["pos_hw"].data_ptr(), ctx["rtab"].data_ptr(),
+                                                ctx["rtab"].shape[0], qb, kb, vb, N, D, H, gws, gwn), "qkv_rotary_pos")
+            else:
+                ck(lib.qvl_dense_qkv_rotary(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb,
+                                            N, D, H, gws, gwn), "qkv_rotary")
         if md.split_tiles:
             ck(lib.qvl_attention_headmajor_split(st, dt, qb, kb, vb, md.split_tiles, md.n_split_tiles,
                                                  md.n_split_whole, N, H, hd, o.data_ptr(), D,
@@ -712,11 +759,42 @@ class Qwen3VisionTransformer:
                "attention")
         ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D,
                             x.data_ptr(), D, N, D, D, gws, gwn), "proj")
-        ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm2_w, B.norm2_b, xn.data_ptr(), D, N, D, 1e-6), "ln2")
-        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_GELU, xn.data_ptr(), D, B.fc1_w, B.fc1_b, None, 0, h.data_ptr(),
-                            I, N, I, D, gws, gwn), "fc1")
+        if fold:
+            ck(lib.qvl_row_stats(st, dt, x.data_ptr(), D, N, D, 1e-6, stats), "ln2 stats")
+            ck(lib.qvl_dense_ln_ws(st, dt, capi.QVL_EPI_BIAS_GELU, x.data_ptr(), D, ff[0].data_ptr(), ff[1].data_ptr(),
+                                   stats, B.fc1_b, h.data_ptr(), I, N, I, D, gws, gwn), "fc1 (folded ln2)")
+        else:
+            ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm2_w, B.norm2_b, xn.data_ptr(), D, N, D, 1e-6), "ln2")
+            ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_GELU, xn.data_ptr(), D, B.fc1_w, B.fc1_b, None, 0,
+                                h.data_ptr(), I, N, I, D, gws, gwn), "fc1")
         ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D,
                             x.data_ptr(), D, N, D, I, gws, gwn), "fc2")
+
+    def merger_fused(self, x, ctx, which: int = -1):
+        """The merger as the whole-tower call runs it: a deepstack merger of a tower with ln_fold takes
+        qvl_row_stats of the [N/4, 4D] rows and the folded fc1 (qvl_dense_ln_ws); every other merger
+        is merger_staged."""
+        if which < 0 or not self.ln_fold:
+            return self.merger_staged(x, ctx, which)
+        torch = _torch()
+        ctx = self._fused_ctx(ctx)
+        lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
+        N, D, s = ctx["N"], ctx["D"], self.spec
+        D4 = 4 * D
+        mw = self._ds_arr[which]
+        f = self._folds[f"deepstack.{which}.fc1"]
+        dev = dict(device=self.device)
+        stats = ctx["stats"].data_ptr()
+        ck(lib.qvl_row_stats(st, dt, x.data_ptr(), D4, N // 4, D4, 1e-6, stats), "merger ln stats")
+        hm = torch.empty((N // 4, D4), dtype=self._tdtype(), **dev)
+        ck(lib.qvl_dense_ln_ws(st, dt, capi.QVL_EPI_BIAS_GELU, x.data_ptr(), D4, f[0].data_ptr(), f[1].data_ptr(), stats,
+                               mw.fc1_b, hm.data_ptr(), D4, N // 4, D4, D4, ctx["gws"].data_ptr(), ctx["gws_bytes"]),
+           "merger fc1 (folded ln)")
+        out = torch.empty((N // 4, s.out_hidden_size), dtype=self._tdtype(), **dev)
+        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS, hm.data_ptr(), D4, mw.fc2_w, mw.fc2_b, None, 0, out.data_ptr(),
+                            s.out_hidden_size, N // 4, s.out_hidden_size, D4, ctx["gws"].data_ptr(), ctx["gws_bytes"]),
+           "merger fc2")
+        return out
 
     def merger_staged(self, x, ctx, which: int = -1):
         """VisionPatchMerger (model.py:648-656) on the residual stream x: main merger (which=-1) or

@@ -1,0 +1,252 @@
+"""LayerNorm folded into the Dense after it (qvl_row_stats, qvl_fold_ln_weight, qvl_dense_ln_ws,
+qvl_dense_qkv_rotary_ln), through the C ABI, against fp64 / torch fp32 references of the
+reference's LayerNorm + Dense (model.py:375-388 feeding 556 / 570-582 / 611 / 651-655).
+
+The fold computes LN(x) . W as rstd * (x . W') - rstd * mean * c + d with W' = bf16(gamma W): the
+reference's rounding of the LayerNorm output to bf16 is replaced by the rounding of W'. The bar:
+within rel-L2 6e-3 of the reference's bf16 arithmetic (LN output rounded, then the bf16 Dense), and
+at least as close to the exact fp64 result as that bf16 arithmetic is (x1.25 + 5e-4)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import vision_tower as vt
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+EPS = 1e-6
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def to_np(t):
+    return t.float().cpu().numpy()
+
+
+def pack(lib, cp, kernel):
+    kin, nout = kernel.shape
+    src = torch.from_numpy(np.ascontiguousarray(kernel, np.float32)).to(DEV)
+    out = torch.empty((-(-nout // 64) * 64, -(-kin // 64) * 64), dtype=torch.bfloat16, device=DEV)
+    cp.check(lib.qvl_pack_dense_weight(stream(), cp.QVL_DTYPE_BF16, src.data_ptr(), kin, nout, out.data_ptr()))
+    return out
+
+
+def rows(rng, m, k):
+    """bf16 rows with per-row offsets and scales (some rows far off zero)."""
+    off = rng.standard_normal((m, 1)) * 2 + np.where(rng.random((m, 1)) < 0.1, 40.0, 0.0)
+    return vt.bf16_round((rng.standard_normal((m, k)) * rng.uniform(0.3, 3.0, (m, 1)) + off).astype(np.float32))
+
+
+def ln_params(rng, k):
+    return (vt.bf16_round((1 + 0.2 * rng.standard_normal(k)).astype(np.float32)),
+            vt.bf16_round((0.1 * rng.standard_normal(k)).astype(np.float32)))
+
+
+def ln64(x, g, b):
+    x = x.astype(np.float64)
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + EPS) * g + b
+
+
+def gelu64(y):
+    return 0.5 * y * (1 + np.tanh(np.sqrt(2 / np.pi) * (y + 0.044715 * y ** 3)))
+
+
+def fold(lib, cp, w, g, b):
+    n_pad, k = w.shape
+    out = torch.empty_like(w)
+    cd = torch.empty((n_pad, 2), dtype=torch.float32, device=DEV)
+    gt, bt = torch.from_numpy(g).to(DEV), torch.from_numpy(b).to(DEV)
+    cp.check(lib.qvl_fold_ln_weight(stream(), cp.QVL_DTYPE_BF16, w.data_ptr(), k, n_pad, gt.data_ptr(), bt.data_ptr(),
+                                    out.data_ptr(), cd.data_ptr()))
+    return out, cd
+
+
+def stats(lib, cp, x, cols):
+    m = x.shape[0]
+    st = torch.empty((m, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_row_stats(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), x.shape[1], m, cols, EPS, st.data_ptr()))
+    return st
+
+
+@pytest.mark.parametrize("cols", [1024, 1152, 4096])
+def test_row_stats_vs_fp64(pkg, lib, cols):
+    """(mean, rstd) per row: within 1e-6 (mean, relative to |mean| + std) and 2e-6 (rstd, relative)
+    of a two-pass fp64 computation, rows with offsets up to 40 standard deviations included."""
+    cp = pkg.capi
+    rng = np.random.default_rng(cols)
+    x = rows(rng, 517, cols)
+    st = to_np(stats(lib, cp, torch.from_numpy(x).to(DEV).to(torch.bfloat16), cols))
+    x64 = x.astype(np.float64)
+    mu = x64.mean(-1)
+    sd = np.sqrt(((x64 - mu[:, None]) ** 2).mean(-1))
+    assert np.all(np.abs(st[:, 0] - mu) <= 1e-6 * (np.abs(mu) + sd))
+    assert np.all(np.abs(st[:, 1] * np.sqrt(sd ** 2 + EPS) - 1) <= 2e-6)
+
+
+def test_fold_ln_weight_exact(pkg, lib):
+    """W' = bf16(gamma W) bit for bit (a bf16 x bf16 product is exact in fp32, so one rounding),
+    c = sum_k W' and d = sum_k beta W within fp32 summation error of fp64, padding rows zero."""
+    cp = pkg.capi
+    rng = np.random.default_rng(3)
+    k, n = 1152, 4304                                   # the 8B fc1: 4304 outputs packed to 4352
+    w = pack(lib, cp, (rng.standard_normal((k, n)) * 0.03).astype(np.float32))
+    g, b = ln_params(rng, k)
+    wf, cd = fold(lib, cp, w, g, b)
+    torch.cuda.synchronize()
+    w_h, wf_h, cd_h = to_np(w), to_np(wf), cd.cpu().numpy()
+    np.testing.assert_array_equal(wf_h, vt.bf16_round(w_h * g[None, :]))
+    c64 = wf_h.astype(np.float64).sum(1)
+    d64 = (w_h.astype(np.float64) * b[None, :].astype(np.float64)).sum(1)
+    assert np.all(np.abs(cd_h[:, 0] - c64) <= 1e-5 * np.abs(wf_h).sum(1) + 1e-30)
+    assert np.all(np.abs(cd_h[:, 1] - d64) <= 1e-5 * np.abs(w_h * b[None, :]).sum(1) + 1e-30)
+    assert not wf_h[n:].any() and not cd_h[n:].any()
+
+
+def ref_bf16_dense(xn, w_h, b_h, epi):
+    """The reference's arithmetic after a bf16 LayerNorm output xn: bf16(bf16(xn.W) + b), GELU."""
+    r = vt.bf16_round
+    y = r(r(xn.astype(np.float32) @ r(w_h)) + b_h)
+    return r(gelu64(y.astype(np.float64)).astype(np.float32)) if epi == 1 else y
+
+
+@pytest.mark.parametrize("epi,m,n,k,plan", [(0, 1000, 3072, 1024, 0), (1, 700, 4096, 1024, 0),
+                                            (1, 300, 4096, 4096, 0), (1, 257, 4304, 1152, 0),
+                                            (1, 700, 4096, 1024, 1), (0, 1000, 3072, 1024, 1)])
+def test_dense_ln_vs_reference(pkg, lib, epi, m, n, k, plan):
+    """qvl_row_stats + qvl_fold_ln_weight + qvl_dense_ln_ws (bias / bias+GELU) against the
+    reference's LayerNorm (bf16 output) + bf16 Dense, and against exact fp64; plan 1 forces the
+    288x256 tiles with a tail split (the split-K reduce applies the fold)."""
+    cp = pkg.capi
+    rng = np.random.default_rng(m + n + k + epi)
+    x = rows(rng, m, k)
+    g, b = ln_params(rng, k)
+    w_h = (rng.standard_normal((k, n)) * 0.03).astype(np.float32)
+    b_h = vt.bf16_round((rng.standard_normal(n) * 0.1).astype(np.float32))
+    w = pack(lib, cp, w_h)
+    wf, cd = fold(lib, cp, w, g, b)
+    xt = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    st = stats(lib, cp, xt, k)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    bias = torch.zeros(-(-n // 64) * 64, dtype=torch.float32, device=DEV)
+    bias[:n] = torch.from_numpy(b_h).to(DEV)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    try:
+        if plan:
+            cp.check(lib.qvl_set_gemm_plan(1, 1, 0))
+        cp.check(lib.qvl_dense_ln_ws(stream(), cp.QVL_DTYPE_BF16, epi, xt.data_ptr(), k, wf.data_ptr(), cd.data_ptr(),
+                                     st.data_ptr(), bias.data_ptr(), y.data_ptr(), n, m, n, k, ws.data_ptr(), nb.value))
+    finally:
+        cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
+    torch.cuda.synchronize()
+    got = to_np(y)
+    xn64 = ln64(x, g, b)
+    exact = xn64 @ vt.bf16_round(w_h).astype(np.float64) + b_h
+    if epi == 1:
+        exact = gelu64(exact)
+    ref = ref_bf16_dense(vt.bf16_round(xn64.astype(np.float32)), w_h, b_h, epi)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) <= 6e-3
+    assert rel_l2(got, exact) <= 1.25 * rel_l2(ref, exact) + 5e-4
+
+
+def vt_positions(n):
+    n = np.asarray(n)
+    quad = (n >> 2) & 3
+    return (n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3)
+
+
+@pytest.mark.parametrize("hd,grids,plan", [(64, [(1, 48, 48)], 0), (64, [(1, 16, 16), (2, 10, 14)], 1),
+                                           (72, [(1, 32, 40)], 0)])
+def test_qkv_rotary_ln_vs_reference(pkg, lib, hd, grids, plan):
+    """qvl_dense_qkv_rotary_ln (norm1 folded into the fused qkv + rotary GEMM, the tower's path)
+    against (a) the unfolded entries (qvl_layer_norm + qvl_dense_qkv_rotary) and (b) exact fp64
+    LayerNorm + Dense + rotary + pre-scale, layouts undone; the per-position-table form equals the
+    per-token form bit for bit. plan 1 forces a tail split (head_dim 64)."""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    H = 16
+    N, D = m.n_tokens, H * hd
+    Np, hdp, half, q4 = -(-N // 64) * 64, (64 if hd == 64 else 88), hd // 2, hd // 4
+    rng = np.random.default_rng(N + hd)
+    x = rows(rng, N, D)
+    g, b = ln_params(rng, D)
+    w_h = (rng.standard_normal((D, 3 * D)) * 0.03).astype(np.float32)
+    b_h = vt.bf16_round((rng.standard_normal(3 * D) * 0.1).astype(np.float32))
+    w = pack(lib, cp, w_h)
+    wf, cd = fold(lib, cp, w, g, b)
+    xt = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    st = stats(lib, cp, xt, D)
+    gt, bt = torch.from_numpy(g).to(DEV), torch.from_numpy(b).to(DEV)
+    xn = torch.empty_like(xt)
+    cp.check(lib.qvl_layer_norm(stream(), cp.QVL_DTYPE_BF16, xt.data_ptr(), D, gt.data_ptr(), bt.data_ptr(),
+                                xn.data_ptr(), D, N, D, EPS))
+    bias = torch.from_numpy(b_h).to(DEV)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    cs = torch.empty((N, half, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
+    P = m.n_positions
+    tab = torch.empty((P, q4), dtype=torch.int32, device=DEV)
+    cp.check(lib.qvl_rotary_pos_table(stream(), hd, 10000.0, P, tab.data_ptr()))
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    outs = {}
+    try:
+        if plan:
+            cp.check(lib.qvl_set_gemm_plan(1, 1, 0))
+        for mode in ("unfolded", "folded", "folded_tab"):
+            if mode == "folded_tab" and hd != 64:
+                continue
+            q = torch.full((H, Np, hdp), 5.0, dtype=torch.bfloat16, device=DEV)
+            k = q.clone()
+            vtm = torch.full((H, hd, Np), 5.0, dtype=torch.bfloat16, device=DEV)
+            if mode == "unfolded":
+                cp.check(lib.qvl_dense_qkv_rotary(stream(), cp.QVL_DTYPE_BF16, xn.data_ptr(), D, w.data_ptr(),
+                                                  bias.data_ptr(), cs.data_ptr(), q.data_ptr(), k.data_ptr(),
+                                                  vtm.data_ptr(), N, D, H, ws.data_ptr(), nb.value))
+            else:
+                tb = mode == "folded_tab"
+                cp.check(lib.qvl_dense_qkv_rotary_ln(stream(), cp.QVL_DTYPE_BF16, xt.data_ptr(), D, wf.data_ptr(),
+                                                     cd.data_ptr(), st.data_ptr(), bias.data_ptr(),
+                                                     None if tb else cs.data_ptr(), pos.data_ptr() if tb else None,
+                                                     tab.data_ptr() if tb else None, P if tb else 0, q.data_ptr(),
+                                                     k.data_ptr(), vtm.data_ptr(), N, D, H, ws.data_ptr(), nb.value))
+            torch.cuda.synchronize()
+            outs[mode] = (to_np(q), to_np(k), to_np(vtm))
+    finally:
+        cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
+    if "folded_tab" in outs:
+        for a, c in zip(outs["folded"], outs["folded_tab"]):
+            np.testing.assert_array_equal(a, c)
+    # exact fp64: LN, Dense on the bf16 kernel, rotary with the table's (bf16) cos / sin, pre-scale
+    qkv = ln64(x, g, b) @ vt.bf16_round(w_h).astype(np.float64) + b_h
+    c_h = cs.cpu().numpy().astype(np.float64)
+    cos = np.concatenate([c_h[..., 0], c_h[..., 0]], axis=1)[:, None, :]
+    sin = np.concatenate([c_h[..., 1], c_h[..., 1]], axis=1)[:, None, :]
+    rot = lambda t: t * cos + np.concatenate([-t[..., half:], t[..., :half]], axis=-1) * sin
+    qscale = 1.4426950408889634 / np.sqrt(hd)
+    exact = (rot(qkv[:, :D].reshape(N, H, hd)).transpose(1, 0, 2) * qscale,
+             rot(qkv[:, D:2 * D].reshape(N, H, hd)).transpose(1, 0, 2),
+             qkv[:, 2 * D:].reshape(N, H, hd).transpose(1, 2, 0))
+    cols = vt_positions(np.arange(N))
+    view = lambda o: (o[0][:, :N, :hd], o[1][:, :N, :hd], o[2][:, :, cols])
+    for name, got, unf, ex in zip("qkv", view(outs["folded"]), view(outs["unfolded"]), exact):
+        assert np.isfinite(got).all(), name
+        assert rel_l2(got, unf) <= 6e-3, name
+        assert rel_l2(got, ex) <= 1.25 * rel_l2(unf, ex) + 5e-4, name
+    q, k, _ = outs["folded"]
+    assert not q[:, N:].any() and not k[:, N:].any() and not q[:, :, hd:].any()

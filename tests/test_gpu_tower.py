@@ -58,9 +58,10 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
     two images (352 tokens).
 
     Per layer: each GPU block, fed the oracle's input to that block, matches the oracle's block
-    output within rel-L2 1e-2, both through the staged entries and through the entries the
-    whole-tower call runs (fused qkv + rotary epilogue, the tower's attention work list); each
-    deepstack merger and the final merger likewise.
+    output within rel-L2 1e-2, through the staged entries, through the entries the whole-tower
+    call runs (fused qkv + rotary epilogue, the tower's attention work list) and through those
+    entries with the LayerNorms folded into the GEMMs (ln_fold); each deepstack merger (also
+    folded) and the final merger likewise.
     End to end: the reference's own bf16 mode drifts ~1.4e-2 from its fp32 mode by block 24
     (bf16 rounding noise the 24 residual blocks accumulate), so no bf16 implementation that is
     not bit-identical to it can sit within 1e-2 of it there. The end-to-end bar is therefore: the
@@ -77,9 +78,11 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
     ref = vt.encode_vision(params, px, grids, ospec, "bf16", keep_layers=True)
     f32 = vt.encode_vision(params, px, grids, ospec, "fp32")
     tower = pkg.Qwen3VisionTransformer(spec).bind(params)
+    towerf = pkg.Qwen3VisionTransformer(spec, ln_fold=True).bind(params)
     g = np.array(grids, np.int32)
     # per layer, in isolation
     ctx = tower._staged_ctx(g)
+    ctxf = towerf._staged_ctx(g)
     x0 = tower.embed_staged(px, ctx)
     assert rel_l2(to_np(x0), ref.embed) <= TOL
     for i in range(spec.depth):
@@ -90,16 +93,22 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
         x = torch.from_numpy(np.ascontiguousarray(xin)).to("cuda:0").to(torch.bfloat16)
         tower.block_fused(i, x, ctx)
         assert rel_l2(to_np(x), ref.layers[i]) <= TOL, f"fused block {i}"
+        x = torch.from_numpy(np.ascontiguousarray(xin)).to("cuda:0").to(torch.bfloat16)
+        towerf.block_fused(i, x, ctxf)
+        assert rel_l2(to_np(x), ref.layers[i]) <= TOL, f"fused block {i}, LayerNorms folded"
     xl = torch.from_numpy(np.ascontiguousarray(ref.layers[-1])).to("cuda:0").to(torch.bfloat16)
     assert rel_l2(to_np(tower.merger_staged(xl, ctx)), vt.patch_merger(ref.layers[-1], params["visual"]["merger"],
                                                                       ospec, False, vt._P("bf16"))) <= TOL
     for j, li in enumerate(spec.deepstack_visual_indexes):
         xl = torch.from_numpy(np.ascontiguousarray(ref.layers[li])).to("cuda:0").to(torch.bfloat16)
         assert rel_l2(to_np(tower.merger_staged(xl, ctx, j)), ref.deepstack[j]) <= TOL, f"deepstack {j}"
+        # with the post-shuffle norm folded into fc1
+        assert rel_l2(to_np(towerf.merger_fused(xl, ctxf, j)), ref.deepstack[j]) <= TOL, f"folded deepstack {j}"
     # end to end, fused whole-tower entry and staged entries
     tok, ds = tower(px, g)
     tok2, ds2, _ = tower.forward_staged(px, g)
-    for got_tok, got_ds in ((tok, ds), (tok2, ds2)):
+    tok3, ds3 = towerf(px, g)
+    for got_tok, got_ds in ((tok, ds), (tok2, ds2), (tok3, ds3)):
         pairs = [(to_np(got_tok), ref.tokens, f32.tokens)] + [(to_np(a), b, c) for a, b, c in
                                                               zip(got_ds, ref.deepstack, f32.deepstack)]
         assert len(pairs) == 4
@@ -108,14 +117,17 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
             assert rel_l2(got, rb) <= 2e-2
 
 
-def test_config2_image_reduced_depth(pkg, params2b):
+@pytest.mark.parametrize("ln_fold", [True, False])
+def test_config2_image_reduced_depth(pkg, params2b, ln_fold):
     """One full 768x768 image of config 2 (grid 1x48x48 = 2304 patches), first 6 blocks + the
-    deepstack tap after block 5 + the merger: rel-L2 <= 1e-2 (fused and staged, per layer)."""
+    deepstack tap after block 5 + the merger: rel-L2 <= 1e-2 (whole-tower entry with the LayerNorms
+    folded into the GEMMs and with LayerNorm launches; staged, per layer)."""
     spec, ospec = specs(pkg, depth=6, ds=(5,))
     grids = [(1, 48, 48)]
     px = pixels(grids, 2)
     ref = vt.encode_vision(params2b, px, grids, ospec, "bf16", keep_layers=True)
-    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tower = pkg.Qwen3VisionTransformer(spec, ln_fold=ln_fold).bind(params2b)
+    assert tower.ln_fold == ln_fold
     tok, ds = tower(px, np.array(grids, np.int32))
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
@@ -148,6 +160,11 @@ def test_config2_image_full_depth_fused_path(pkg, params2b):
         r = rel_l2(to_np(x), ref.layers[i])
         worst = max(worst, r)
         assert r <= TOL, f"fused block {i}: {r:.3e}"
+    for j, li in enumerate(spec.deepstack_visual_indexes):
+        xl = torch.from_numpy(np.ascontiguousarray(ref.layers[li])).to("cuda:0").to(torch.bfloat16)
+        r = rel_l2(to_np(tower.merger_fused(xl, ctx, j)), ref.deepstack[j])
+        worst = max(worst, r)
+        assert r <= TOL, f"fused deepstack merger {j}: {r:.3e}"
     tok, ds = tower(px, g)
     names = ["tokens"] + [f"deepstack{j}" for j in range(len(ds))]
     rows = []
@@ -157,7 +174,8 @@ def test_config2_image_full_depth_fused_path(pkg, params2b):
         rows.append(f"{name}: vs bf16 oracle {e_b:.3e}, vs fp32 oracle {e_f:.3e} (oracle bf16 vs fp32 {e_ref:.3e})")
         assert e_f <= 1.1 * e_ref, name
         assert e_b <= 2e-2, name
-    print(f"\n[config2 image, 24 blocks] worst fused block in isolation {worst:.3e}; " + "; ".join(rows), flush=True)
+    print(f"\n[config2 image, 24 blocks] worst fused block / deepstack merger in isolation {worst:.3e}; "
+          + "; ".join(rows), flush=True)
 
 
 def test_config3_video_reduced_depth(pkg, params2b):
