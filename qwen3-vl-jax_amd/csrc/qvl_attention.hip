@@ -152,6 +152,9 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
       bf16x8 kf[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kf[ks] = k_frag(ST, b, ks);
+      // a wave issuing MFMAs takes issue priority over the SIMD's other waves, which are then in
+      // their softmax VALU work (same-box A/B: -1.5 % at config 2)
+      __builtin_amdgcn_s_setprio(1);
       f32x16 s = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
@@ -161,9 +164,12 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
       for (int e2 = 0; e2 < 2; ++e2)
 #pragma unroll
         for (int db = 0; db < 2; ++db) vf[2 * e2 + db] = v_frag(ST, db, 2 * b + e2);
+      __builtin_amdgcn_s_setprio(0);
       uint32_t pk[8];
       exp_pack(s, 0.f, pk);
+      __builtin_amdgcn_s_setprio(1);
       pv(vf, pk);
+      __builtin_amdgcn_s_setprio(0);
     }
     wait_dma();
     __syncthreads();
