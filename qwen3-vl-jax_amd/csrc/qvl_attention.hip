@@ -111,12 +111,14 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
   const int n_kt = t1 - t0;
 
-  auto mask_block = [&](f32x16& s, int kb, int b) {   // keys outside [seg_s, seg_e) -> -inf
+  // keys outside [seg_s, seg_e) -> -inf. Element r of a lane is key kb + 32 b + 4 hh + 8 (r / 4) + r % 4:
+  // one unsigned range test against the lane's bounds per element (the offsets are constants).
+  auto mask_block = [&](f32x16& s, int kb, int b) {
+    const int lo = seg_s - (kb + 32 * b + 4 * hh);
+    const uint32_t span = (uint32_t)(seg_e - seg_s);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kb + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-      if (key < seg_s || key >= seg_e) s[r] = -INFINITY;
-    }
+    for (int r = 0; r < 16; ++r)
+      if ((uint32_t)(8 * (r >> 2) + (r & 3) - lo) >= span) s[r] = -INFINITY;
   };
   // p = exp2(s - sh) as bf16 pairs, fp32 row-sum share
   auto exp_pack = [&](const f32x16& s, float sh, uint32_t (&pk)[8]) {
@@ -158,15 +160,21 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
       f32x16 s = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
-      if constexpr (EDGE) mask_block(s, kb, b);
       bf16x8 vf[4];
+      auto read_v = [&]() {
 #pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2)
+        for (int e2 = 0; e2 < 2; ++e2)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) vf[2 * e2 + db] = v_frag(ST, db, 2 * b + e2);
+          for (int db = 0; db < 2; ++db) vf[2 * e2 + db] = v_frag(ST, db, 2 * b + e2);
+      };
+      // steady state: the V^T reads are in flight during the softmax; the (once per item) edge
+      // tiles issue them after it, which keeps the mask's temporaries within the register budget
+      if constexpr (EDGE) mask_block(s, kb, b);
+      else read_v();
       __builtin_amdgcn_s_setprio(0);
       uint32_t pk[8];
       exp_pack(s, 0.f, pk);
+      if constexpr (EDGE) read_v();
       __builtin_amdgcn_s_setprio(1);
       pv(vf, pk);
       __builtin_amdgcn_s_setprio(0);
