@@ -15,16 +15,20 @@
 //
 // S^T = K Q^T via v_mfma_f32_32x32x16_bf16: a lane holds one query and 16 keys of a 32-key block.
 // Softmax is shift invariant, and with the tower's scores (log2 units) far inside fp32 range the
-// kernel applies no shift at all: p = exp2(s) is one instruction per score, the fp32 row sum one
-// add, and P goes to bf16 pairs for the PV MFMA (its B operand, straight from registers); there is
-// no running max, no rescale and no per-block check in the loop. After the loop each wave checks
-// its rows: a row sum outside [2^-64, 2^96] or an accumulator above 2^120 (inf / NaN included)
-// means the unshifted sum under- or overflowed, and that wave recomputes its rows shifted by the
-// exact row max (global loads: a max pass, then the sum pass), which holds for any finite scores.
-// The reference normalises by the fp32 sum of the fp32 weights (model.py:594-595) and so does the
-// kernel. V^T's quad-swapped key layout makes each lane's 8 PV keys one 16-byte LDS chunk.
-// Steady-state tiles run one 32-key block at a time (S, softmax, PV), so a block's four K and four
-// V^T fragment reads are issued ahead of its MFMAs within the 128-register budget of 4 waves/SIMD.
+// kernel applies no shift at all: p = exp2(s) is one instruction per score and P goes to bf16 pairs
+// for the PV MFMA (its B operand, straight from registers); there is no running max, no rescale and
+// no per-block check in the loop. The row sums come from the matrix cores: per 16-key group one
+// v_mfma_f32_16x16x32_bf16 multiplies the same B operand by a selector fragment (rowsum_selector)
+// whose rows 0 and 1 sum the bf16 P of the wave's queries 0..15 and 16..31, so the output is the
+// convex combination of V rows with the weights the PV MFMA used (the reference normalises by the
+// sum of its fp32 weights, model.py:594-595; the difference is bf16 rounding of P, as in the PV
+// product itself). After the loop each wave checks its rows: a row sum outside [2^-64, 2^96] or an
+// accumulator above 2^120 (inf / NaN included) means the unshifted sum under- or overflowed, and
+// that wave recomputes its rows shifted by the exact row max (global loads: a max pass, then the
+// sum pass with fp32 sums), which holds for any finite scores. V^T's quad-swapped key layout makes
+// each lane's 8 PV keys one 16-byte LDS chunk. Steady-state tiles run one 32-key block at a time
+// (S, softmax, PV), so a block's four K and four V^T fragment reads are issued ahead of its MFMAs
+// within the 128-register budget of 4 waves/SIMD.
 #include <math.h>
 #include <type_traits>
 #include "qvl_kernels.h"
@@ -43,6 +47,16 @@ template <int V> using int_c = std::integral_constant<int, V>;
 // rows' worth), and the 16 rows one such read touches land in 16 distinct bank groups.
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * kHD + ((chunk ^ ((row >> 1) & 7)) << 3); }
 __device__ __forceinline__ int v_off(int d, int chunk) { return d * kAttnBN + ((chunk ^ ((d >> 1) & 7)) << 3); }
+
+// A operand of v_mfma_f32_16x16x32_bf16 (lane l: row l % 16, k-slots 8 (l / 16) .. +8) with row 0
+// one on k-slot groups 0 and 2 and row 1 on groups 1 and 3. The PV B operand read as a 16x16x32 B
+// operand (lane l: column l % 16, k-slot group l / 16) holds in groups 0 / 2 the P of queries 0..15
+// and in groups 1 / 3 those of queries 16..31 (the same 16 keys), so output rows 0 and 1 of lane n
+// accumulate the row sums of queries n and 16 + n.
+__device__ __forceinline__ bf16x8 rowsum_selector(int lane) {
+  const uint32_t w = ((lane & 15) == ((lane >> 4) & 1)) ? 0x3F803F80u : 0u;
+  return __builtin_bit_cast(bf16x8, u32x4{w, w, w, w});
+}
 
 __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
@@ -101,7 +115,9 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   };
 
   f32x16 oacc[2] = {f32x16{}, f32x16{}};
-  float l_run = 0.f;   // this lane's fp32 row-sum share (its 8 keys of every 16)
+  f32x4 lacc = {0.f, 0.f, 0.f, 0.f};   // row sums: lane n holds queries n (element 0) and 16 + n (1)
+  const bf16x8 ones = rowsum_selector(lane);
+  float l_run = 0.f;   // the exact path's fp32 row-sum share (this lane's 8 keys of every 16)
   float m_run = 0.f;   // the shift of the scores: 0 on the main path, the exact row max on the exact path
 
   // Key tiles of 64 from the segment start rounded down to 64; a part of a split item takes its
@@ -132,7 +148,7 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     }
     l_run += ta + tb;
   };
-  // O^T[d][q] += V^T[d][keys] P^T[keys][q]: B operand = 8 P values per lane.
+  // O^T[d][q] += V^T[d][keys] P^T[keys][q]: B operand = 8 P values per lane; the row sums beside.
   auto pv = [&](const bf16x8 (&vf)[4], const uint32_t (&pk)[8]) {
 #pragma unroll
     for (int e2 = 0; e2 < 2; ++e2) {
@@ -140,7 +156,12 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
 #pragma unroll
       for (int db = 0; db < 2; ++db)
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * e2 + db], pf, oacc[db], 0, 0, 0);
+      lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, lacc, 0, 0, 0);
     }
+  };
+  auto exp_only = [&](const f32x16& s, uint32_t (&pk)[8]) {   // p = exp2(s) as bf16 pairs
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pk[j] = pack_bf16x2(__builtin_amdgcn_exp2f(s[2 * j]), __builtin_amdgcn_exp2f(s[2 * j + 1]));
   };
 
   // One key tile in LDS stage ST; EDGE masks keys outside the segment (first and last tiles).
@@ -149,35 +170,52 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     constexpr int ST = decltype(stage_tag)::value;
     const int kb = k_begin + it * kAttnBN;
     if (it + 1 < n_kt) dma_tile(kb + kAttnBN, ST ^ 1);
+    // A wave issuing MFMAs takes issue priority (s_setprio) over the SIMD's other waves, which are
+    // then in their softmax VALU work (same-box A/B: -1.5 % at config 2).
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      bf16x8 kf[4];
+      if constexpr (EDGE) {
+        // first / last tile (once per item): fragments are read next to their MFMAs, so the mask's
+        // temporaries fit the register budget without spills
+        __builtin_amdgcn_s_setprio(1);
+        f32x16 s = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[ks] = k_frag(ST, b, ks);
-      // a wave issuing MFMAs takes issue priority over the SIMD's other waves, which are then in
-      // their softmax VALU work (same-box A/B: -1.5 % at config 2)
-      __builtin_amdgcn_s_setprio(1);
-      f32x16 s = f32x16{};
+        for (int ks = 0; ks < 4; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(ST, b, ks), qf[ks], s, 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+        mask_block(s, kb, b);
+        uint32_t pk[8];
+        exp_only(s, pk);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
-      bf16x8 vf[4];
-      auto read_v = [&]() {
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * e2], pk[4 * e2 + 1], pk[4 * e2 + 2], pk[4 * e2 + 3]});
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+            oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(ST, db, 2 * b + e2), pf, oacc[db], 0, 0, 0);
+          lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, lacc, 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+      } else {
+        // steady state: the block's K and V^T fragment reads are in flight ahead of its MFMAs
+        bf16x8 kf[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kf[ks] = k_frag(ST, b, ks);
+        __builtin_amdgcn_s_setprio(1);
+        f32x16 s = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+        bf16x8 vf[4];
 #pragma unroll
         for (int e2 = 0; e2 < 2; ++e2)
 #pragma unroll
           for (int db = 0; db < 2; ++db) vf[2 * e2 + db] = v_frag(ST, db, 2 * b + e2);
-      };
-      // steady state: the V^T reads are in flight during the softmax; the (once per item) edge
-      // tiles issue them after it, which keeps the mask's temporaries within the register budget
-      if constexpr (EDGE) mask_block(s, kb, b);
-      else read_v();
-      __builtin_amdgcn_s_setprio(0);
-      uint32_t pk[8];
-      exp_pack(s, 0.f, pk);
-      if constexpr (EDGE) read_v();
-      __builtin_amdgcn_s_setprio(1);
-      pv(vf, pk);
-      __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_setprio(0);
+        uint32_t pk[8];
+        exp_only(s, pk);
+        __builtin_amdgcn_s_setprio(1);
+        pv(vf, pk);
+        __builtin_amdgcn_s_setprio(0);
+      }
     }
     wait_dma();
     __syncthreads();
@@ -200,7 +238,8 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     step(std::true_type{}, int_c<1>{}, it);
   }
 
-  float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float la = __shfl(lacc[0], lane & 15), lb = __shfl(lacc[1], lane & 15);
+  float l_tot = (l32 & 16) ? lb : la;   // lanes q and q + 32 both hold query q's sum
   float omax = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) omax = fmaxf(omax, fmaxf(fabsf(oacc[0][r]), fabsf(oacc[1][r])));
