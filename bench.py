@@ -147,6 +147,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cpu-compiled", action="store_true", help="skip the torch.compile CPU variant (~35 s)")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--block-forwards", type=int, default=2,
+                    help="timed forwards through the per-block entries for the per-block kernel classes")
     ap.add_argument("--only", default=None,
                     help="launch only this kernel class (name prefix, or 'copy') --kernel-reps times; for rocprofv3 runs")
     args = ap.parse_args()
@@ -242,6 +244,51 @@ def main():
                                            tens["tiles"].data_ptr(), md.n_tiles, N, H, hd, yk.data_ptr(), D)
     ln_g = torch.ones(D, device=dev)
     ln_b = torch.zeros(D, device=dev)
+    # The tower folds norm1 / norm2 into qkv / fc1 (its default, ln_fold): proj and fc2 write the row
+    # partials of x that the folded qkv and fc1 read, and no LayerNorm runs inside a block. The
+    # classes below time those launches; parts_x holds the partials of xk (plumbing: torch ops),
+    # parts_y receives the producers' partials of yk.
+    fold = bool(tower.ln_fold) and D % 128 == 0
+    G = D // 128
+    if fold:
+        fq, ff = tower._folds["blocks.0.qkv"], tower._folds["blocks.0.fc1"]
+        xg = xk.float().view(N, G, 128)
+        gs = xg.sum(-1)
+        parts_x = torch.stack([gs, ((xg - gs[..., None] / 128) ** 2).sum(-1)], -1).contiguous()
+        parts_y = torch.empty_like(parts_x)
+    # the per-position rotary table the tower's head_dim-64 qkv epilogue reads (when it fits)
+    use_tab = hd == 64 and m.n_positions * (hd // 4) * 4 <= (12032 if fold else 16384)
+    if use_tab:
+        rtab = torch.empty((m.n_positions, hd // 4), dtype=torch.int32, device=dev)
+        cp.check(lib.qvl_rotary_pos_table(s_, hd, 10000.0, m.n_positions, rtab.data_ptr()), "rotary table")
+
+    def qkv_launch():
+        tab = (tens["pos_hw"].data_ptr(), rtab.data_ptr(), m.n_positions) if use_tab else (None, None, 0)
+        if fold:
+            return lib.qvl_dense_qkv_rotary_ln_parts(s_, BF, xk.data_ptr(), D, fq[0].data_ptr(), fq[1].data_ptr(),
+                                                     parts_x.data_ptr(), G, 1e-6, blk.qkv_b,
+                                                     None if use_tab else cs.data_ptr(), *tab, qb.data_ptr(),
+                                                     kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn)
+        if use_tab:
+            return lib.qvl_dense_qkv_rotary_pos(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, *tab, qb.data_ptr(),
+                                                kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn)
+        return lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(), qb.data_ptr(),
+                                        kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn)
+
+    def fc1_launch():
+        if fold:
+            return lib.qvl_dense_ln_parts_ws(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, ff[0].data_ptr(),
+                                             ff[1].data_ptr(), parts_x.data_ptr(), G, 1e-6, blk.fc1_b,
+                                             hout.data_ptr(), Ip, N, Ip, D, pp, pn)
+        return lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
+                                hout.data_ptr(), Ip, N, Ip, D, pp, pn)
+
+    def residual_launch(src, ld, w, b, k):
+        if fold:
+            return lib.qvl_dense_rowstats_ws(s_, BF, src.data_ptr(), ld, w, b, yk.data_ptr(), D, yk.data_ptr(), D, N,
+                                             D, k, parts_y.data_ptr(), pp, pn)
+        return lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, src.data_ptr(), ld, w, b, yk.data_ptr(), D,
+                                yk.data_ptr(), D, N, D, k, pp, pn)
     # The two pixel-sized HBM kernels write (and the cast reads) 113-170 MB per launch at config 2;
     # launched back to back on one buffer their data stays in the 256 MB Infinity Cache and the rate
     # reads above the HBM peak. They rotate over 3 buffers instead (340 MB / 510 MB at config 2), as a
@@ -266,31 +313,24 @@ def main():
     cp.check(lib.qvl_vision_positions(s_, tok_txt.data_ptr(), 1, S_txt, 1, V, vpos.data_ptr(), vcnt.data_ptr()),
              "positions")
     segs = f"{len(seg)} x {seg[0]}" if len(set(seg)) == 1 else "+".join(map(str, seg))
+    ln_tag = ", LayerNorm folded" if fold else ""
+    rs_tag = ", + row partials" if fold else ""
     PV = spec.patch_volume
     kernels = {
         # name: (callable, "mfma" FLOPs or "hbm" bytes per launch, bound, launches per step)
-        f"fc1 (gemm, bias+GELU) {N}x{I}x{D}": (
-            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_GELU, xk.data_ptr(), D, blk.fc1_w, blk.fc1_b, None, 0,
-                                     hout.data_ptr(), Ip, N, Ip, D, pp, pn), 2.0 * N * D * I, "mfma", depth),
-        f"fc2 (gemm, bias+residual) {N}x{D}x{I}": (
-            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, hk.data_ptr(), Ip, blk.fc2_w, blk.fc2_b,
-                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, Ip, pp, pn), 2.0 * N * I * D, "mfma",
-            depth),
-        f"proj (gemm, bias+residual) {N}x{D}x{D}": (
-            lambda: lib.qvl_dense_ws(s_, BF, cp.QVL_EPI_BIAS_RESIDUAL, xk.data_ptr(), D, blk.proj_w, blk.proj_b,
-                                     yk.data_ptr(), D, yk.data_ptr(), D, N, D, D, pp, pn), 2.0 * N * D * D, "mfma",
-            depth),
-        f"qkv+rotary (gemm) {N}x{3 * D}x{D}": (
-            lambda: lib.qvl_dense_qkv_rotary(s_, BF, xk.data_ptr(), D, blk.qkv_w, blk.qkv_b, cs.data_ptr(),
-                                             qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), N, D, H, pp, pn),
-            2.0 * N * D * 3 * D, "mfma", depth),
+        f"fc1 (gemm, bias+GELU{ln_tag}) {N}x{I}x{D}": (fc1_launch, 2.0 * N * D * I, "mfma", depth),
+        f"fc2 (gemm, bias+residual{rs_tag}) {N}x{D}x{I}": (
+            lambda: residual_launch(hk, Ip, blk.fc2_w, blk.fc2_b, Ip), 2.0 * N * I * D, "mfma", depth),
+        f"proj (gemm, bias+residual{rs_tag}) {N}x{D}x{D}": (
+            lambda: residual_launch(xk, D, blk.proj_w, blk.proj_b, D), 2.0 * N * D * D, "mfma", depth),
+        f"qkv+rotary (gemm{ln_tag}) {N}x{3 * D}x{D}": (qkv_launch, 2.0 * N * D * 3 * D, "mfma", depth),
         f"attention (varlen, {segs} tokens, {H}x{hd})": (
             attention_launch,
             float(sum(4 * L * L * D for L in seg)), "mfma", depth),
         # memory-bound kernels: algorithmic bytes = every operand read once + every output written once
         f"layer_norm ({N}x{D} bf16)": (
             lambda: lib.qvl_layer_norm(s_, BF, xk.data_ptr(), D, ln_g.data_ptr(), ln_b.data_ptr(), yk.data_ptr(), D,
-                                       N, D, 1e-6), 2.0 * N * D * 2 + 2 * D * 4, "hbm", 2 * depth + 1 + nds),
+                                       N, D, 1e-6), 2.0 * N * D * 2 + 2 * D * 4, "hbm", 1 if fold else 2 * depth + 1 + nds),
         f"pos_embed ({N}x{D}, 4 bilinear taps)": (
             lambda: lib.qvl_pos_embed(s_, BF, tower._w.pos_table, tens["tap_idx"].data_ptr(),
                                       tens["tap_w"].data_ptr(), yk.data_ptr(), N, D),
@@ -326,31 +366,30 @@ def main():
         torch.cuda.synchronize()
         print(f"bench.py --only {args.only}: {args.kernel_reps} launches", flush=True)
         return
-    # The per-block kernels are timed inside a replay of one block's launch sequence (the order
-    # the tower runs them): the GPU's clock under a sustained single-kernel loop drops well below
-    # its level in the tower (power), so an isolated loop would misstate each kernel's share of
-    # the step. Each kernel launches GROUP times back to back between one pair of HIP events on
-    # the launch stream, which spreads the events' own cost (a few us) over the group. The rest
-    # run in back-to-back loops of their own.
-    GROUP = 4
+    # The per-block kernels are timed inside forwards of the tower through the per-block entries
+    # (block_fused: the tower's kernels, in the tower's order, on the tower's activations — the
+    # embed output fed through all blocks, each block's norm1 reading the row partials the
+    # previous block's fc2 wrote), each launch between its own pair of HIP events on the launch
+    # stream. Synthetic N(0,1) operands or a kernel repeated back to back run hotter than the tower
+    # (the GPU is power-limited): replays of one block on such operands measured these kernels 5-14 %
+    # slower than the rocprofv3 trace of the tower's own launches. The rest run in back-to-back loops
+    # of their own.
     name_of = {k.split(" ")[0]: k for k in kernels}
-    block_seq = [name_of[k] for k in ("layer_norm", "qkv+rotary", "attention", "proj", "layer_norm", "fc1", "fc2")]
+    cls_key = {"qkv": name_of["qkv+rotary"], "attention": name_of["attention"], "proj": name_of["proj"],
+               "fc1": name_of["fc1"], "fc2": name_of["fc2"]}
+    block_seq = list(cls_key.values())
     times = {k: [] for k in kernels}
-    for _ in range(2):
-        for name in block_seq:
-            cp.check(kernels[name][0](), name)
-    evs = []
-    for _ in range(args.kernel_reps):
-        for name in block_seq:
-            a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a_.record(st)
-            for _ in range(GROUP):
-                kernels[name][0]()
-            b_.record(st)
-            evs.append((name, a_, b_))
+    sctx = tower._staged_ctx(grids)
+    x0 = tower.embed_staged(px, sctx)
+    marks = []
+    for rep in range(1 + args.block_forwards):
+        xb = x0.clone()
+        for i in range(depth):
+            tower.block_fused(i, xb, sctx, x_parts=i > 0, marks=marks if rep > 0 else None)
     torch.cuda.synchronize()
-    for name, a_, b_ in evs:
-        times[name].append(a_.elapsed_time(b_) / GROUP)
+    for name, a_, b_ in marks:
+        times[cls_key[name]].append(a_.elapsed_time(b_))
+    del sctx, x0, xb
     for name, (fn, work, bound, per_step) in kernels.items():
         if name in block_seq:
             continue

@@ -239,6 +239,35 @@ int qvl_dense_qkv_rotary_ln(void* stream, int32_t dtype, const void* d_x, int64_
                             int32_t n_positions, void* d_q, void* d_k, void* d_vt, int64_t n_tokens,
                             int64_t hidden, int32_t num_heads, void* d_workspace, size_t workspace_bytes);
 
+/* The row statistics of a folded LayerNorm produced by the Dense that writes its input: the
+ * residual Dense (x + proj / fc2, model.py:628-629; the patch embed + pos-embed, 802-806) also
+ * writes, per output row m and 128-column group g, d_parts[m][g] = (sum_j y, sum_j (y - mean_g)^2)
+ * over the group's bf16 outputs y (n % 128 == 0, ldc and ldr multiples of 8; d_parts
+ * [m][n / 128][2] fp32). The folded Dense entries below combine a row's groups into its mean and
+ * variance (Chan et al.'s pairwise update), which replaces the LayerNorm's statistics pass
+ * (model.py:384-386): no LayerNorm and no statistics launch remain between the two GEMMs. bf16. */
+int qvl_dense_rowstats_ws(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
+                          const float* d_bias, const void* d_residual, int64_t ldr, void* d_y, int64_t ldc,
+                          int64_t m, int64_t n, int64_t k, float* d_parts, void* d_workspace,
+                          size_t workspace_bytes);
+
+/* qvl_dense_ln_ws with the row statistics given as qvl_dense_rowstats_ws partials of x: `groups`
+ * 128-column groups per row (k == 128 * groups; a row of the deepstack mergers' [N/4, 4D] view is 4
+ * token rows, i.e. 4 * D / 128 groups), eps the LayerNorm's (model.py:375-388). */
+int qvl_dense_ln_parts_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, int64_t lda,
+                          const void* d_w, const float* d_cd, const float* d_parts, int32_t groups, float eps,
+                          const float* d_bias, void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                          void* d_workspace, size_t workspace_bytes);
+
+/* qvl_dense_qkv_rotary_ln with the row statistics as qvl_dense_rowstats_ws partials (hidden == 128 *
+ * groups), model.py:628 + 570-582. */
+int qvl_dense_qkv_rotary_ln_parts(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
+                                  const float* d_cd, const float* d_parts, int32_t groups, float eps,
+                                  const float* d_bias, const void* d_cos_sin, const int32_t* d_pos_hw,
+                                  const uint32_t* d_table, int32_t n_positions, void* d_q, void* d_k, void* d_vt,
+                                  int64_t n_tokens, int64_t hidden, int32_t num_heads, void* d_workspace,
+                                  size_t workspace_bytes);
+
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
  * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][88] (dims 72..87 zero) and

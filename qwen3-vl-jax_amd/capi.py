@@ -86,6 +86,12 @@ SIGNATURES = {
     "qvl_dense_ln_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz]),
     "qvl_dense_qkv_rotary_ln": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64,
                                           _i64, _i32, _p, _sz]),
+    "qvl_dense_rowstats_ws": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _p,
+                                        _sz]),
+    "qvl_dense_ln_parts_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _i64, _i64, _i64,
+                                        _i64, _p, _sz]),
+    "qvl_dense_qkv_rotary_ln_parts": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _p, _p, _i32,
+                                                _p, _p, _p, _i64, _i64, _i32, _p, _sz]),
     "qvl_pos_embed": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i64, _i64]),
     "qvl_rotary_table": (C.c_int, [_p, _i32, _p, _i64, _i32, _f32, _p]),
     "qvl_vision_attention_workspace_size": (C.c_int, [_i32, _i64, _i32, _i32, C.POINTER(_sz)]),

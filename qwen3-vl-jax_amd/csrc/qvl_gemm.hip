@@ -87,8 +87,8 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
 // past N): 16-byte loads/stores when the rows are 16-byte aligned. The products are exact bf16
 // values, so only the sum with the bias is rounded (pairwise, one conversion per two values).
 template <int EPI>
-__device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n, u32x4 raw, const f32x4& b0,
-                                              const f32x4& b1, bool full, bool vec16) {
+__device__ __forceinline__ u32x4 epi_store_oct(const GemmParams& p, int m, int n, u32x4 raw, const f32x4& b0,
+                                               const f32x4& b1, bool full, bool vec16) {
   float v[8] = {bf16_lo(raw.x) + b0[0], bf16_hi(raw.x) + b0[1], bf16_lo(raw.y) + b0[2], bf16_hi(raw.y) + b0[3],
                 bf16_lo(raw.z) + b1[0], bf16_hi(raw.z) + b1[1], bf16_lo(raw.w) + b1[2], bf16_hi(raw.w) + b1[3]};
   if constexpr (EPI != kEpiBias) {
@@ -108,11 +108,11 @@ __device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n,
     }
     // Streaming (nt) store: every CU writes its whole tile at once at the end of a round, and
     // the output is not re-read by this kernel; measured ~1.5% faster per tower forward.
-    __builtin_nontemporal_store(u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                      pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])},
-                                reinterpret_cast<u32x4*>(dst));
-    return;
+    const u32x4 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst));
+    return o;
   }
+  u32x4 o = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     if (h == 1 && !full) break;
@@ -120,18 +120,83 @@ __device__ __forceinline__ void epi_store_oct(const GemmParams& p, int m, int n,
       const u32x2 r = *reinterpret_cast<const u32x2*>(p.res + (int64_t)m * p.ldr + n + 4 * h);
       v[4 * h] += bf16_lo(r.x); v[4 * h + 1] += bf16_hi(r.x); v[4 * h + 2] += bf16_lo(r.y); v[4 * h + 3] += bf16_hi(r.y);
     }
-    *reinterpret_cast<u32x2*>(dst + 4 * h) = u32x2{pack_bf16x2(v[4 * h], v[4 * h + 1]), pack_bf16x2(v[4 * h + 2], v[4 * h + 3])};
+    const u32x2 oh = {pack_bf16x2(v[4 * h], v[4 * h + 1]), pack_bf16x2(v[4 * h + 2], v[4 * h + 3])};
+    *reinterpret_cast<u32x2*>(dst + 4 * h) = oh;
+    o[2 * h] = oh.x;
+    o[2 * h + 1] = oh.y;
   }
+  return o;
+}
+
+// Statistics of the LayerNorm that reads this epilogue's output next (p.rs_part): the bf16 values
+// w of 8 consecutive columns n..n+7 of row m, one such octet per lane, 16 lanes (aligned to 16)
+// holding the 16 octets of one 128-column group; the group's sum and its sum of squared deviations
+// from the group mean go to rs_part (two butterfly reductions over the 16 lanes; every lane ends
+// with the same bits, IEEE addition being commutative).
+__device__ __forceinline__ void row_group_stats(const GemmParams& p, int m, int n, u32x4 w) {
+  const float y[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
+                      bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+  float s = ((y[0] + y[1]) + (y[2] + y[3])) + ((y[4] + y[5]) + (y[6] + y[7]));
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o);
+  const float mean = s * (1.0f / 128.0f);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float d = y[e] - mean;
+    q = fmaf(d, d, q);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
+  if ((threadIdx.x & 15) == 0) p.rs_part[(int64_t)m * (p.N / 128) + n / 128] = f32x2{s, q};
+}
+
+// (mean, rstd) of row m for a folded LayerNorm: from p.ln_stats, or combined from the row's
+// 128-column partials (Chan et al.'s pairwise update: M2 = sum_g [Q_g + (S_g - 128 mean)^2 / 128]),
+// var = M2 / K, rstd = 1 / sqrt(var + eps) (model.py:384-386). Rows at or past M give zeros.
+// A row's partials are loaded kLnChunk at a time (an unrolled, guarded loop: every load of a
+// chunk is in flight before the first use) and combined in registers; a row of at most kLnChunk
+// groups (the blocks' LayerNorms: hidden / 128) is loaded once for both passes.
+constexpr int kLnChunk = 16;
+
+__device__ __forceinline__ f32x2 ln_row(const GemmParams& p, int m) {
+  if (m >= p.M) return f32x2{0.f, 0.f};
+  if (!p.ln_part) return p.ln_stats[m];
+  const int G = p.ln_groups;
+  const f32x2* q = p.ln_part + (int64_t)m * G;
+  f32x2 v[kLnChunk];
+  auto load = [&](int base) {
+#pragma unroll
+    for (int g = 0; g < kLnChunk; ++g) v[g] = base + g < G ? q[base + g] : f32x2{0.f, 0.f};
+  };
+  float s = 0.f;
+  for (int base = 0; base < G; base += kLnChunk) {
+    load(base);
+#pragma unroll
+    for (int g = 0; g < kLnChunk; ++g) s += v[g].x;
+  }
+  const float inv_n = 1.0f / (128.0f * (float)G);
+  const float mean = s * inv_n;
+  float m2 = 0.f;
+  for (int base = 0; base < G; base += kLnChunk) {
+    if (G > kLnChunk) load(base);
+#pragma unroll
+    for (int g = 0; g < kLnChunk; ++g) {
+      const float d = v[g].x - 128.0f * mean;
+      if (base + g < G) m2 += v[g].y + d * d * (1.0f / 128.0f);
+    }
+  }
+  return f32x2{mean, rsqrtf(m2 * inv_n + p.ln_eps)};
 }
 
 __device__ __forceinline__ void rope_values(const GemmParams& p, int which, int m, int d, const f32x4& blo,
                                             const f32x4& bhi, const float (&lo_acc)[4], const float (&hi_acc)[4],
                                             const f32x4& c01, const f32x4& c23, u32x2& o1, u32x2& o2);
 
-// Folded LayerNorm (p.ln_stats): the 4 accumulators of features n..n+3 of token m become
+// Folded LayerNorm (p.ln_stats or p.ln_part): the 4 accumulators of features n..n+3 of token m become
 // rstd * acc - rstd * mean * c + d, i.e. LN(x) . W (model.py:387 into 556), before any rounding.
 __device__ __forceinline__ void ln_fold_quad(const GemmParams& p, int m, int n, float (&a)[4]) {
-  const f32x2 st = m < p.M ? p.ln_stats[m] : f32x2{0.f, 0.f};
+  const f32x2 st = ln_row(p, m);
   const f32x4 cd01 = *reinterpret_cast<const f32x4*>(p.ln_cd + n), cd23 = *reinterpret_cast<const f32x4*>(p.ln_cd + n + 2);
   const float nm = -st.x * st.y;
   a[0] = fmaf(a[0], st.y, fmaf(nm, cd01[0], cd01[1]));
@@ -163,12 +228,15 @@ __device__ __forceinline__ LnRows<MB> ln_rows(const f32x2* lrs, int r_first) {
 }
 
 // lcd: the tile's (c, d) pairs in LDS (column n0 + i at lcd[i], zeros past N), copied at kernel start.
-__device__ __forceinline__ void ln_fold_group(const f32x2* lcd, float r, float nm, int col, float (&v)[4]) {
-  const f32x4 cd01 = *reinterpret_cast<const f32x4*>(lcd + col), cd23 = *reinterpret_cast<const f32x4*>(lcd + col + 2);
+__device__ __forceinline__ void ln_fold_cd(const f32x4& cd01, const f32x4& cd23, float r, float nm, float (&v)[4]) {
   v[0] = fmaf(v[0], r, fmaf(nm, cd01[0], cd01[1]));
   v[1] = fmaf(v[1], r, fmaf(nm, cd01[2], cd01[3]));
   v[2] = fmaf(v[2], r, fmaf(nm, cd23[0], cd23[1]));
   v[3] = fmaf(v[3], r, fmaf(nm, cd23[2], cd23[3]));
+}
+
+__device__ __forceinline__ void ln_fold_group(const f32x2* lcd, float r, float nm, int col, float (&v)[4]) {
+  ln_fold_cd(*reinterpret_cast<const f32x4*>(lcd + col), *reinterpret_cast<const f32x4*>(lcd + col + 2), r, nm, v);
 }
 
 
@@ -258,19 +326,27 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
   const int l32 = lane & 31, hh = lane >> 5;
   LnRows<S::MB> L;
   if constexpr (LN) L = ln_rows<S::MB>(lcd + BN, wm * S::TM + l32);
+  // (column groups outermost: a folded LayerNorm's (c, d) of a lane's 4 columns are read once for
+  // all its row blocks)
 #pragma unroll
   for (int a = 0; a < S::NB; ++a)
 #pragma unroll
-    for (int b = 0; b < S::MB; ++b)
+    for (int g = 0; g < 4; ++g) {
+      const int c = (wn * S::TN + a * 32) / 8 + g;
+      f32x4 cd01 = {}, cd23 = {};
+      if constexpr (LN) {
+        cd01 = *reinterpret_cast<const f32x4*>(lcd + c * 8 + 4 * hh);
+        cd23 = *reinterpret_cast<const f32x4*>(lcd + c * 8 + 4 * hh + 2);
+      }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int b = 0; b < S::MB; ++b) {
         const int r = wm * S::TM + b * 32 + l32;
-        const int c = (wn * S::TN + a * 32) / 8 + g;
         float f[4] = {acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
-        if constexpr (LN) ln_fold_group(lcd, L.r[b], L.nm[b], c * 8 + 4 * hh, f);
+        if constexpr (LN) ln_fold_cd(cd01, cd23, L.r[b], L.nm[b], f);
         const u32x2 v = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])};
         *reinterpret_cast<u32x2*>(smem + r * BN + ((c ^ (r % CH)) << 3) + hh * 4) = v;
       }
+    }
   __syncthreads();
   const bool vec16 = ((p.ldc | (EPI == kEpiBiasResidual ? p.ldr : 0)) & 7) == 0;
   // A thread keeps one 8-feature column group for the whole walk (THREADS is a multiple of the
@@ -288,7 +364,12 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
     const int m = m0 + r;
     if (m >= p.M) break;               // rows only grow with i
     const u32x4 raw = *reinterpret_cast<const u32x4*>(smem + r * BN + ((c ^ (r % CH)) << 3));
-    epi_store_oct<EPI>(p, m, n, raw, b0, b1, full, vec16);
+    const u32x4 out = epi_store_oct<EPI>(p, m, n, raw, b0, b1, full, vec16);
+    if constexpr (EPI == kEpiBiasResidual) {
+      // 16 consecutive threads, aligned to 16, hold the 16 octets of one 128-column group of row m
+      static_assert(CH % 16 == 0, "row statistics need 128-column groups within a tile row");
+      if (p.rs_part) row_group_stats(p, m, n, out);
+    }
   }
 }
 
@@ -663,6 +744,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         dma16(rww, wv, (uint32_t)((i * S::ROWS_PER_PASS * p.K + k0) * 2), wa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
   };
 
+  // The first k-step's operands are on their way while the prologue below copies its tables.
+  dma_stage(kt0 * kBK, 0);
+
   // The qkv rotary epilogues' per-position (cos, sin) table, copied once into LDS above the
   // operand ring / staging area (its first barrier below publishes it).
   const uint32_t* ltab = nullptr;
@@ -686,8 +770,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         if (i < BN) {
           t[i] = n0 + i < p.N ? p.ln_cd[n0 + i] : f32x2{0.f, 0.f};
         } else {
-          const int m = m0 + i - BN;
-          const f32x2 st = m < p.M ? p.ln_stats[m] : f32x2{0.f, 0.f};
+          const f32x2 st = ln_row(p, m0 + i - BN);
           t[i] = f32x2{st.y, -st.x * st.y};
         }
       }
@@ -725,7 +808,6 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   };
   constexpr int NMF = S::NB * S::MB;
 
-  dma_stage(kt0 * kBK, 0);
   wait_dma();
   __syncthreads();
   read_frags(smem, 0, 0);
@@ -806,7 +888,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
       for (int e = 0; e < 4; ++e) hi[e] += b[e];
     }
   }
-  if (p.ln_stats && n < p.N) {
+  if ((p.ln_stats || p.ln_part) && n < p.N) {
     ln_fold_quad(p, m, n, lo);
     if constexpr (EPI == kEpiQkvRope) ln_fold_quad(p, m, n + 32, hi);
   }
@@ -920,7 +1002,8 @@ constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.
 template <int EPI, bool LN>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const int cus = gemm_device_cus();
-  const ForcedPlan f = t_plan;
+  ForcedPlan f = t_plan;
+  if (p.rs_part) f.split_mode = -1;   // the split-K reduction writes no row statistics
   const GemmPlan a = plan_gemm<288, 256>(p, cus, kRate288x256, f.split_mode);
   const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
@@ -958,14 +1041,16 @@ constexpr double kRate256x288 = 1.50e6;
 
 static int dispatch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
   const GemmPlan g = plan_gemm<256, 288>(p, gemm_device_cus(), kRate256x288, -1);
-  if (p.ln_stats) return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, true>(p, g, stream);
+  if (p.ln_stats || p.ln_part) return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, true>(p, g, stream);
   return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, false>(p, g, stream);
 }
 
-// A folded LayerNorm (p.ln_stats) selects the kernels instantiated with the fold (bias, GELU and
+// A folded LayerNorm (p.ln_stats or p.ln_part) selects the kernels instantiated with the fold (bias, GELU and
 // rotary epilogues: the Dense layers that follow a LayerNorm); the others carry no trace of it.
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream) {
-  const bool ln = p.ln_stats != nullptr;
+  const bool ln = p.ln_stats != nullptr || p.ln_part != nullptr;
+  if (p.rs_part && (epi != kEpiBiasResidual || p.N % 128))
+    return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: row statistics need the residual epilogue and N %% 128 == 0");
   if (ln && !p.ln_cd) return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: folded LayerNorm without (c, d)");
   switch (epi) {
     case kEpiQkvRope72: return dispatch_qkv_rope72(p, stream);

@@ -47,7 +47,8 @@ int qvl_cast(void* stream, int32_t dtype, const float* x, void* y, int64_t n) {
 static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
                       const float* bias, const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n,
                       int64_t k, void* ws, size_t ws_bytes, const float* ln_cd = nullptr,
-                      const float* ln_stats = nullptr) {
+                      const float* ln_stats = nullptr, const float* ln_part = nullptr, int ln_groups = 0,
+                      float ln_eps = 0.f, float* rs_part = nullptr) {
   if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32) return set_error(QVL_ERR_UNSUPPORTED, "dense: dtype %d", dtype);
   if (epi < QVL_EPI_BIAS || epi > QVL_EPI_BIAS_RESIDUAL) return set_error(QVL_ERR_INVALID_ARG, "dense: epilogue %d", epi);
   if (m < 0 || n <= 0 || k <= 0) return set_error(QVL_ERR_INVALID_ARG, "dense: m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
@@ -83,6 +84,10 @@ static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, i
   p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
   p.ln_stats = (const f32x2*)ln_stats;
   p.ln_cd = (const f32x2*)ln_cd;
+  p.ln_part = (const f32x2*)ln_part;
+  p.ln_groups = ln_groups;
+  p.ln_eps = ln_eps;
+  p.rs_part = (f32x2*)rs_part;
   return gemm_bf16(p, epi, (hipStream_t)stream);
 }
 
@@ -257,8 +262,10 @@ int qvl_rotary_pos_table(void* stream, int32_t head_dim, float theta, int32_t n_
 static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
                            const void* cs, const int32_t* pos_hw, const uint32_t* rtab, int32_t n_pos, void* q,
                            void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H, void* ws, size_t ws_bytes,
-                           const float* ln_cd = nullptr, const float* ln_stats = nullptr) {
+                           const float* ln_cd = nullptr, const float* ln_stats = nullptr,
+                           const float* ln_part = nullptr, int ln_groups = 0, float ln_eps = 0.f) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: dtype %d", dtype);
+  const bool ln = ln_stats || ln_part;
   if (H <= 0 || (hidden != (int64_t)H * 64 && hidden != (int64_t)H * 72))
     return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: head_dim must be 64 or 72");
   const int hd = (int)(hidden / H);
@@ -268,9 +275,9 @@ static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t l
   if (n_tokens == 0) return QVL_OK;
   if (!x || !w || !bias || !q || !k || !vt || (!cs && (!pos_hw || !rtab)))
     return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary: NULL operand");
-  if (rtab && (n_pos <= 0 || (int64_t)n_pos * (hd / 4) * 4 > rope_table_lds_bytes(hd, ln_stats != nullptr)))
+  if (rtab && (n_pos <= 0 || (int64_t)n_pos * (hd / 4) * 4 > rope_table_lds_bytes(hd, ln)))
     return set_error(QVL_ERR_UNSUPPORTED, "qkv_rotary: %d rotary positions exceed the %d-byte table of head_dim %d",
-                     n_pos, rope_table_lds_bytes(hd, ln_stats != nullptr), hd);
+                     n_pos, rope_table_lds_bytes(hd, ln), hd);
   if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(q) || !aligned16(k) || !aligned16(vt) ||
       (cs && !aligned16(cs)) || (rtab && !aligned16(rtab)))
     return set_error(QVL_ERR_MISALIGNED, "qkv_rotary: alignment");
@@ -290,6 +297,9 @@ static int qkv_rotary_impl(void* stream, int32_t dtype, const void* x, int64_t l
   p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
   p.ln_stats = (const f32x2*)ln_stats;
   p.ln_cd = (const f32x2*)ln_cd;
+  p.ln_part = (const f32x2*)ln_part;
+  p.ln_groups = ln_groups;
+  p.ln_eps = ln_eps;
   return gemm_bf16(p, hd == 64 ? kEpiQkvRope : kEpiQkvRope72, (hipStream_t)stream);
 }
 
@@ -319,6 +329,53 @@ int qvl_dense_qkv_rotary_ln(void* stream, int32_t dtype, const void* x, int64_t 
     return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary_ln: give either the per-token cos/sin table or positions + table");
   return qkv_rotary_impl(stream, dtype, x, lda, w, bias, cs, cs ? nullptr : pos_hw, cs ? nullptr : table,
                          cs ? 0 : n_positions, q, k, vt, n_tokens, hidden, H, ws, ws_bytes, cd, stats);
+}
+
+// Row-statistics partials of a LayerNorm's input (128-column groups): shared argument checks.
+static int check_ln_parts(const char* what, int64_t rows, int64_t cols, const float* cd, const float* parts,
+                          int32_t groups, float eps) {
+  if (rows > 0 && (!cd || !parts)) return set_error(QVL_ERR_INVALID_ARG, "%s: NULL folded LayerNorm operand", what);
+  if (groups <= 0 || groups > 64 || (int64_t)groups * 128 != cols)
+    return set_error(QVL_ERR_INVALID_ARG, "%s: %d 128-column groups for rows of %lld", what, groups, (long long)cols);
+  if (!(eps > 0.f)) return set_error(QVL_ERR_INVALID_ARG, "%s: eps must be positive", what);
+  if (((uintptr_t)cd & 15) || ((uintptr_t)parts & 7)) return set_error(QVL_ERR_MISALIGNED, "%s: alignment", what);
+  return QVL_OK;
+}
+
+int qvl_dense_rowstats_ws(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
+                          const void* res, int64_t ldr, void* y, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                          float* parts, void* ws, size_t ws_bytes) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense_rowstats: dtype %d (bf16 only)", dtype);
+  if (n % 128) return set_error(QVL_ERR_UNSUPPORTED, "dense_rowstats: n=%lld not a multiple of 128", (long long)n);
+  if (m > 0 && !parts) return set_error(QVL_ERR_INVALID_ARG, "dense_rowstats: NULL partials");
+  if (((uintptr_t)parts & 7) || ldc % 8 || ldr % 8)
+    return set_error(QVL_ERR_MISALIGNED, "dense_rowstats: partials 8-byte aligned, ldc and ldr multiples of 8");
+  return dense_impl(stream, dtype, QVL_EPI_BIAS_RESIDUAL, x, lda, w, bias, res, ldr, y, ldc, m, n, k, ws, ws_bytes,
+                    nullptr, nullptr, nullptr, 0, 0.f, parts);
+}
+
+int qvl_dense_ln_parts_ws(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
+                          const float* cd, const float* parts, int32_t groups, float eps, const float* bias, void* y,
+                          int64_t ldc, int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes) {
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense_ln_parts: dtype %d (bf16 only)", dtype);
+  if (epi != QVL_EPI_BIAS && epi != QVL_EPI_BIAS_GELU)
+    return set_error(QVL_ERR_INVALID_ARG, "dense_ln_parts: epilogue %d (bias or bias+GELU)", epi);
+  QVL_TRY_RC(check_ln_parts("dense_ln_parts", m, k, cd, parts, groups, eps));
+  return dense_impl(stream, dtype, epi, x, lda, w, bias, nullptr, 0, y, ldc, m, n, k, ws, ws_bytes, cd, nullptr,
+                    parts, groups, eps);
+}
+
+int qvl_dense_qkv_rotary_ln_parts(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w,
+                                  const float* cd, const float* parts, int32_t groups, float eps, const float* bias,
+                                  const void* cs, const int32_t* pos_hw, const uint32_t* table, int32_t n_positions,
+                                  void* q, void* k, void* vt, int64_t n_tokens, int64_t hidden, int32_t H, void* ws,
+                                  size_t ws_bytes) {
+  QVL_TRY_RC(check_ln_parts("qkv_rotary_ln_parts", n_tokens, hidden, cd, parts, groups, eps));
+  if (n_tokens > 0 && (cs ? (pos_hw || table) : (!pos_hw || !table)))
+    return set_error(QVL_ERR_INVALID_ARG, "qkv_rotary_ln_parts: give either the per-token cos/sin table or positions + table");
+  return qkv_rotary_impl(stream, dtype, x, lda, w, bias, cs, cs ? nullptr : pos_hw, cs ? nullptr : table,
+                         cs ? 0 : n_positions, q, k, vt, n_tokens, hidden, H, ws, ws_bytes, cd, nullptr, parts, groups,
+                         eps);
 }
 
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
@@ -383,6 +440,7 @@ struct TowerLayout {
   int64_t N, Np, D, I_pad, PV, hd, H;
   int hdp, vrows;
   size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, off_apart, off_stats, apart_bytes, total;
+  int stat_groups;   // 128-column groups of a row's LayerNorm partials (hidden / 128; 0: hidden % 128 != 0)
 };
 
 // Upper bound on the parts of split attention items one work list holds (qvl_attention_
@@ -434,8 +492,10 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   // partial outputs of split attention items: at most one per workgroup slot (4 per CU)
   L->apart_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)attn_split_slots_bound() * attn_partial_floats((int)hd) * 4 : 0;
   L->off_apart = take(L->apart_bytes);
-  // (mean, rstd) per row of the LayerNorms folded into the following Dense (bf16)
-  L->off_stats = c->dtype == QVL_DTYPE_BF16 ? take((size_t)N * 8) : 0;
+  // row statistics of the LayerNorms folded into the following Dense (bf16): per-128-column partials
+  // (sum, squared deviations) of each row of x, or (mean, rstd) per row when hidden % 128 != 0
+  L->stat_groups = c->hidden_size % 128 == 0 ? (int)(c->hidden_size / 128) : 0;
+  L->off_stats = c->dtype == QVL_DTYPE_BF16 ? take((size_t)N * 8 * std::max(1, L->stat_groups)) : 0;
   L->total = o;
   return QVL_OK;
 }
@@ -452,16 +512,23 @@ int qvl_encode_vision_workspace_size(const qvl_vision_config* cfg, int64_t n_tok
 
 // VisionPatchMerger.__call__ (model.py:648-656): main (LN over D then view [N/4, 4D]) or
 // deepstack (view [N/4, 4D] then LN over 4D); fc1 + GELU-tanh; fc2.
-// A deepstack merger in bf16 with its norm folded into fc1 runs qvl_row_stats + qvl_dense_ln_ws instead of
-// the LayerNorm launch.
+// A deepstack merger in bf16 with its norm folded into fc1 reads the row statistics of x instead of
+// running the LayerNorm: the fc2 epilogue's partials of the merged rows' 4 tokens (parts_groups =
+// 128-column groups per token row, 0: none), or a qvl_row_stats launch.
 static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLayout& L, const qvl_merger_weights& mw,
-                      bool postshuffle, const void* x, void* xn, void* h, void* out, void* part, float* stats) {
+                      bool postshuffle, const void* x, void* xn, void* h, void* out, void* part, float* stats,
+                      int parts_groups) {
   const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
   const int dt = L.dtype;
   if (postshuffle && dt == QVL_DTYPE_BF16 && mw.fc1_ln.w && mw.fc1_ln.cd && stats) {
-    QVL_TRY_RC(qvl_row_stats(st, dt, x, D4, N / 4, D4, c->ln_eps, stats));
-    QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS_GELU, x, D4, mw.fc1_ln.w, mw.fc1_ln.cd, stats, mw.fc1_b, h, D4,
-                               N / 4, D4, D4, part, L.part_bytes));
+    if (parts_groups > 0) {
+      QVL_TRY_RC(qvl_dense_ln_parts_ws(st, dt, QVL_EPI_BIAS_GELU, x, D4, mw.fc1_ln.w, mw.fc1_ln.cd, stats,
+                                       4 * parts_groups, c->ln_eps, mw.fc1_b, h, D4, N / 4, D4, D4, part, L.part_bytes));
+    } else {
+      QVL_TRY_RC(qvl_row_stats(st, dt, x, D4, N / 4, D4, c->ln_eps, stats));
+      QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS_GELU, x, D4, mw.fc1_ln.w, mw.fc1_ln.cd, stats, mw.fc1_b, h, D4,
+                                 N / 4, D4, D4, part, L.part_bytes));
+    }
   } else {
     if (postshuffle)
       QVL_TRY_RC(qvl_layer_norm(st, dt, x, D4, mw.norm_w, mw.norm_b, xn, D4, N / 4, D4, c->ln_eps));
@@ -540,10 +607,26 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     QVL_TRY_RC(qvl_rotary_pos_table(st, (int)L.hd, c->rope_theta, (int)meta->n_positions, (uint32_t*)cs));
   else
     QVL_TRY_RC(qvl_rotary_table(st, dt, meta->pos_hw, N, (int)L.hd, c->rope_theta, cs));
+  // Folded LayerNorms (bf16 blocks / deepstack mergers whose weights carry the folds) read the row
+  // statistics of x as 128-column partials that the residual epilogues writing x (patch embed,
+  // proj, fc2) produce beside it: no LayerNorm or statistics launch. have_parts: `stats` holds
+  // them for the current x; otherwise a folded LayerNorm runs qvl_row_stats first.
+  bool any_fold = false;
+  for (int i = 0; i < c->depth && !f32; ++i)
+    any_fold = any_fold || (W->blocks[i].qkv_ln.w && W->blocks[i].qkv_ln.cd);
+  for (int j = 0; j < c->n_deepstack && !f32; ++j) any_fold = any_fold || W->deepstack[j].fc1_ln.w;
+  const int G = any_fold ? L.stat_groups : 0;
+  bool have_parts = false;
   if (c->num_position_embeddings > 0) {
     QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
-    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
-                            L.PV, part, PB));
+    if (G) {
+      QVL_TRY_RC(qvl_dense_rowstats_ws(st, dt, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV, stats,
+                                       part, PB));
+      have_parts = true;
+    } else {
+      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
+                              L.PV, part, PB));
+    }
   } else {   // no learned pos-embed table (model.py:676-680, 803-806): the patch embed alone
     QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, px_in, L.PV, W->patch_w, W->patch_b, nullptr, 0, x, D, N, D, L.PV,
                             part, PB));
@@ -556,14 +639,22 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     // statistics run before it)
     const bool fold = !f32 && B.qkv_ln.w && B.qkv_ln.cd && B.fc1_ln.w && B.fc1_ln.cd;
     // x += proj(attention(rotary(qkv(LN1 x))))   (model.py:628, 569-601)
-    if (fold)
-      QVL_TRY_RC(qvl_row_stats(st, dt, x, D, N, D, c->ln_eps, stats));
-    else
+    if (fold) {
+      if (!have_parts) QVL_TRY_RC(qvl_row_stats(st, dt, x, D, N, D, c->ln_eps, stats));
+    } else {
       QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm1_w, B.norm1_b, xn, D, N, D, c->ln_eps));
+    }
     if (fused_qkv && fold) {
-      QVL_TRY_RC(qvl_dense_qkv_rotary_ln(st, dt, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, B.qkv_b, pos_tab ? nullptr : cs,
-                                         pos_tab ? meta->pos_hw : nullptr, pos_tab ? (const uint32_t*)cs : nullptr,
-                                         pos_tab ? (int)meta->n_positions : 0, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
+      const void* tcs = pos_tab ? nullptr : (const void*)cs;
+      const int32_t* tpos = pos_tab ? meta->pos_hw : nullptr;
+      const uint32_t* ttab = pos_tab ? (const uint32_t*)cs : nullptr;
+      const int tnp = pos_tab ? (int)meta->n_positions : 0;
+      if (have_parts)
+        QVL_TRY_RC(qvl_dense_qkv_rotary_ln_parts(st, dt, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, G, c->ln_eps, B.qkv_b,
+                                                 tcs, tpos, ttab, tnp, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
+      else
+        QVL_TRY_RC(qvl_dense_qkv_rotary_ln(st, dt, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, B.qkv_b, tcs, tpos, ttab, tnp,
+                                           Qb, Kb, Vb, N, D, (int)L.H, part, PB));
     } else if (fused_qkv) {
       // qkv Dense with rotary + head-major relayout fused into its epilogue.
       if (pos_tab)
@@ -573,7 +664,10 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
         QVL_TRY_RC(qvl_dense_qkv_rotary(st, dt, xn, D, B.qkv_w, B.qkv_b, cs, Qb, Kb, Vb, N, D, (int)L.H, part, PB));
     } else {
       // qkv Dense into h, then rotary + head-major relayout.
-      if (fold)
+      if (fold && have_parts)
+        QVL_TRY_RC(qvl_dense_ln_parts_ws(st, dt, QVL_EPI_BIAS, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, G, c->ln_eps,
+                                         B.qkv_b, h, 3 * D, N, 3 * D, D, part, PB));
+      else if (fold)
         QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS, x, D, B.qkv_ln.w, B.qkv_ln.cd, stats, B.qkv_b, h, 3 * D, N,
                                    3 * D, D, part, PB));
       else
@@ -599,9 +693,16 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
       QVL_TRY_RC(qvl_attention_headmajor(st, dt, Qb, Kb, Vb, full ? meta->tiles : meta->window_tiles,
                                          full ? meta->n_tiles : meta->n_window_tiles, N, (int)L.H, (int)L.hd, xn, D));
     }
-    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, part, PB));
+    have_parts = fold && G;
+    if (have_parts)
+      QVL_TRY_RC(qvl_dense_rowstats_ws(st, dt, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, stats, part, PB));
+    else
+      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, xn, D, B.proj_w, B.proj_b, x, D, x, D, N, D, D, part, PB));
     // x += fc2(gelu(fc1(LN2 x)))   (model.py:629, 610-614)
-    if (fold) {
+    if (fold && have_parts) {
+      QVL_TRY_RC(qvl_dense_ln_parts_ws(st, dt, QVL_EPI_BIAS_GELU, x, D, B.fc1_ln.w, B.fc1_ln.cd, stats, G, c->ln_eps,
+                                       B.fc1_b, h, I, N, I, D, part, PB));
+    } else if (fold) {
       QVL_TRY_RC(qvl_row_stats(st, dt, x, D, N, D, c->ln_eps, stats));
       QVL_TRY_RC(qvl_dense_ln_ws(st, dt, QVL_EPI_BIAS_GELU, x, D, B.fc1_ln.w, B.fc1_ln.cd, stats, B.fc1_b, h, I, N, I,
                                  D, part, PB));
@@ -609,19 +710,25 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
       QVL_TRY_RC(qvl_layer_norm(st, dt, x, D, B.norm2_w, B.norm2_b, xn, D, N, D, c->ln_eps));
       QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_GELU, xn, D, B.fc1_w, B.fc1_b, nullptr, 0, h, I, N, I, D, part, PB));
     }
-    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I, part, PB));
+    // partials of the new x for the next block's folded norm1 or a folded deepstack merger
+    have_parts = G != 0;
+    if (have_parts)
+      QVL_TRY_RC(qvl_dense_rowstats_ws(st, dt, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I, stats, part, PB));
+    else
+      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, h, I, B.fc2_w, B.fc2_b, x, D, x, D, N, D, I, part, PB));
     // deepstack tap (model.py:841-843)
     for (int j = 0; j < c->n_deepstack; ++j)
       if (c->deepstack_indexes[j] == i) {
         void* out = win ? (void*)Qb : deepstack[ds_next];
-        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, out, part, stats));
+        QVL_TRY_RC(run_merger(st, c, L, W->deepstack[ds_next], true, x, xn, h, out, part, stats,
+                              have_parts ? G : 0));
         if (win)   // unshuffle (model.py:845-848)
           QVL_TRY_RC(qvl_gather_rows(st, dt, Qb, Dout, dt, deepstack[ds_next], Dout, meta->window_reverse, N / 4, 1, Dout));
         ++ds_next;
       }
   }
   (void)e;
-  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, win ? (void*)Qb : tokens, part, stats));
+  QVL_TRY_RC(run_merger(st, c, L, W->merger, false, x, xn, h, win ? (void*)Qb : tokens, part, stats, 0));
   if (win) QVL_TRY_RC(qvl_gather_rows(st, dt, Qb, Dout, dt, tokens, Dout, meta->window_reverse, N / 4, 1, Dout));
   return QVL_OK;
 }

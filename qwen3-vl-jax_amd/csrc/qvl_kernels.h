@@ -40,6 +40,15 @@ struct GemmParams {
   // the accumulator becomes rstd * acc - rstd * mean * c + d before the epilogue.
   const f32x2* ln_stats;
   const f32x2* ln_cd;
+  // ... or with the row statistics as per-128-column partials (ln_part != NULL instead of ln_stats):
+  // ln_part[m * ln_groups + g] = (sum, sum of squared deviations from the group mean) of row m's
+  // columns [128 g, 128 g + 128), K = 128 ln_groups, combined per row in the kernel (eps = ln_eps).
+  const f32x2* ln_part;
+  int ln_groups;
+  float ln_eps;
+  // Residual epilogue: also write those partials of the bf16 output rows (rs_part[m * N / 128 + g]),
+  // the statistics of the LayerNorm that reads them next (N % 128 == 0, no split-K tail).
+  f32x2* rs_part;
 };
 
 // fp32 GEMM (qvl_f32.hip): w packed [n_rows_w][ldw] fp32 (ldw = k padded to 64), Kp = ldw.

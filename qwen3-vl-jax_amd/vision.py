@@ -321,7 +321,7 @@ class Qwen3VisionTransformer:
     META_CACHE_SIZE = 16   # grids whose device metadata stays cached (LRU)
 
     def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0",
-                 split_attention: bool = True, ln_fold: bool = False):
+                 split_attention: bool = True, ln_fold: bool = True):
         if dtype not in ("bfloat16", "float32"):
             raise NotImplementedError(f"dtype {dtype!r}: the tower runs in bfloat16 or float32")
         if spec.spatial_merge_size != 2:
@@ -333,11 +333,13 @@ class Qwen3VisionTransformer:
         # bf16 full attention runs a qvl_attention_worklist_split list (the last round's items split
         # along keys) when true
         self.split_attention = split_attention
-        # ln_fold (bf16): each block's norm1 / norm2 and the deepstack mergers' post-shuffle norms
-        # are folded into the Dense after them (qvl_fold_ln_weight at bind time; qvl_row_stats + the
-        # folded GEMM at run time instead of a LayerNorm launch). Off by default: on MI355X the
-        # fold's epilogue work costs more than the LayerNorm launches it removes (same-box A/B at
-        # config 2: 17.83 vs 17.76 ms per forward).
+        # ln_fold (bf16, the default): each block's norm1 / norm2 and the deepstack mergers'
+        # post-shuffle norms are folded into the Dense after them (qvl_fold_ln_weight at bind time);
+        # at run time the residual Dense that writes x also writes its row statistics as 128-column
+        # partials and the folded Dense combines them, so no LayerNorm runs between the GEMMs
+        # (same-box A/Bs at config 2: 16.31 vs 16.47 and 16.06 vs 16.14 ms per forward). The fold
+        # rounds bf16(gamma W) where the reference rounds the LayerNorm output (within the bf16
+        # tolerances). ln_fold=False runs the reference's LayerNorm launches.
         self.ln_fold = bool(ln_fold) and self.qdtype == capi.QVL_DTYPE_BF16
         self._folds: Dict[str, tuple] = {}
         self._lib = capi.load()
@@ -704,24 +706,31 @@ class Qwen3VisionTransformer:
         ctx["apart"] = torch.empty(max(ab.value, 256), dtype=torch.uint8, **dev)
         ctx["apart_bytes"] = ab.value
         ctx["stats"] = torch.empty((N, 2), dtype=torch.float32, **dev)     # folded LayerNorms' (mean, rstd)
+        # per-128-column row partials written by the residual Dense layers (hidden % 128 == 0)
+        ctx["parts"] = torch.empty((N, max(1, self.spec.hidden_size // 128), 2), dtype=torch.float32, **dev)
         # (cos, sin) per rotary position, as the tower looks them up when the grid's positions fit
         n_pos = ctx["m"].n_positions
-        cap = 16384 if hd == 64 else 12288
+        cap = (12032 if self.ln_fold else 16384) if hd == 64 else 12288   # the folded kernels' LDS leaves less
         if hd == 64 and 0 < n_pos and n_pos * (hd // 4) * 4 <= cap:
             ctx["rtab"] = torch.empty((n_pos, hd // 4), dtype=torch.int32, **dev)
             capi.check(self._lib.qvl_rotary_pos_table(self._stream(), hd, 10000.0, n_pos, ctx["rtab"].data_ptr()),
                        "qvl_rotary_pos_table")
         return ctx
 
-    def block_fused(self, i: int, x, ctx) -> None:
+    def block_fused(self, i: int, x, ctx, x_parts: bool = False, marks: Optional[list] = None) -> None:
         """VisionBlock i (model.py:627-630) in place on x [N, D] through exactly the entries the
         whole-tower call runs for a bf16 tower (head_dim 64 or 72): LayerNorm, the fused qkv Dense +
         rotary (qvl_dense_qkv_rotary, head-major Q/K/V^T), attention on the tower's work list
         (qvl_attention_headmajor_split when the tower builds a split list, else
         qvl_attention_headmajor), proj + residual, LayerNorm, fc1 + GELU, fc2 + residual, the
-        GEMMs with the tower's split-K workspace. With ln_fold each LayerNorm is qvl_row_stats and
-        the Dense after it the folded entry (qvl_dense_qkv_rotary_ln, qvl_dense_ln_ws), as in the
-        tower."""
+        GEMMs with the tower's split-K workspace. With ln_fold each LayerNorm is folded into the Dense
+        after it, as in the tower: proj and fc2 write x's row partials (qvl_dense_rowstats_ws) and fc1
+        reads them (qvl_dense_ln_parts_ws); norm1 reads the partials the previous block's fc2 left in
+        ctx when x_parts is true (blocks run in sequence, the tower's exact launches), and otherwise
+        (a block run on its own) takes its statistics from qvl_row_stats (the same mean and rstd up
+        to fp32 rounding) into qvl_dense_qkv_rotary_ln (hidden % 128 != 0: qvl_row_stats for both
+        norms). marks: a list that receives (kernel class, start event, end event) for each of the
+        five GEMM / attention launches, recorded on the launch stream."""
         ctx = self._fused_ctx(ctx)
         lib, st, dt, ck = self._lib, self._stream(), self.qdtype, capi.check
         N, D, H, hd, I = ctx["N"], ctx["D"], ctx["H"], ctx["hd"], ctx["I"]
@@ -731,49 +740,92 @@ class Qwen3VisionTransformer:
         md = ctx["md"]
         B = self._blocks_arr[i]
         fold = self.ln_fold
-        if fold:
+        G = D // 128 if fold and D % 128 == 0 else 0
+        parts = ctx["parts"].data_ptr()
+        torch = _torch()
+        tstream = torch.cuda.current_stream()
+
+        def timed(name, launch):
+            if marks is None:
+                launch()
+                return
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(tstream)
+            launch()
+            b.record(tstream)
+            marks.append((name, a, b))
+        if fold and G and x_parts:
+            fq = self._folds[f"blocks.{i}.qkv"]
+            ff = self._folds[f"blocks.{i}.fc1"]
+            rt = "rtab" in ctx
+            timed("qkv", lambda: ck(lib.qvl_dense_qkv_rotary_ln_parts(
+                st, dt, x.data_ptr(), D, fq[0].data_ptr(), fq[1].data_ptr(), parts, G, 1e-6, B.qkv_b,
+                None if rt else ctx["cs"].data_ptr(), ctx["tens"]["pos_hw"].data_ptr() if rt else None,
+                ctx["rtab"].data_ptr() if rt else None, ctx["rtab"].shape[0] if rt else 0, qb, kb, vb, N, D, H, gws,
+                gwn), "qkv_rotary_ln_parts"))
+        elif fold:
             stats = ctx["stats"].data_ptr()
             fq, ff = self._folds[f"blocks.{i}.qkv"], self._folds[f"blocks.{i}.fc1"]
             ck(lib.qvl_row_stats(st, dt, x.data_ptr(), D, N, D, 1e-6, stats), "ln1 stats")
             rt = "rtab" in ctx
-            ck(lib.qvl_dense_qkv_rotary_ln(st, dt, x.data_ptr(), D, fq[0].data_ptr(), fq[1].data_ptr(), stats, B.qkv_b,
-                                           None if rt else ctx["cs"].data_ptr(),
-                                           ctx["tens"]["pos_hw"].data_ptr() if rt else None,
-                                           ctx["rtab"].data_ptr() if rt else None, ctx["rtab"].shape[0] if rt else 0,
-                                           qb, kb, vb, N, D, H, gws, gwn), "qkv_rotary_ln")
+            timed("qkv", lambda: ck(lib.qvl_dense_qkv_rotary_ln(
+                st, dt, x.data_ptr(), D, fq[0].data_ptr(), fq[1].data_ptr(), stats, B.qkv_b,
+                None if rt else ctx["cs"].data_ptr(), ctx["tens"]["pos_hw"].data_ptr() if rt else None,
+                ctx["rtab"].data_ptr() if rt else None, ctx["rtab"].shape[0] if rt else 0, qb, kb, vb, N, D, H, gws,
+                gwn), "qkv_rotary_ln"))
         else:
             ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm1_w, B.norm1_b, xn.data_ptr(), D, N, D, 1e-6), "ln1")
             if "rtab" in ctx:
-                ck(lib.qvl_dense_qkv_rotary_pos(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b,
-                                                ctx["tens"]["pos_hw"].data_ptr(), ctx["rtab"].data_ptr(),
-                                                ctx["rtab"].shape[0], qb, kb, vb, N, D, H, gws, gwn), "qkv_rotary_pos")
+                timed("qkv", lambda: ck(lib.qvl_dense_qkv_rotary_pos(
+                    st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["tens"]["pos_hw"].data_ptr(),
+                    ctx["rtab"].data_ptr(), ctx["rtab"].shape[0], qb, kb, vb, N, D, H, gws, gwn), "qkv_rotary_pos"))
             else:
-                ck(lib.qvl_dense_qkv_rotary(st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb,
-                                            N, D, H, gws, gwn), "qkv_rotary")
+                timed("qkv", lambda: ck(lib.qvl_dense_qkv_rotary(
+                    st, dt, xn.data_ptr(), D, B.qkv_w, B.qkv_b, ctx["cs"].data_ptr(), qb, kb, vb, N, D, H, gws, gwn),
+                    "qkv_rotary"))
         if md.split_tiles:
-            ck(lib.qvl_attention_headmajor_split(st, dt, qb, kb, vb, md.split_tiles, md.n_split_tiles,
-                                                 md.n_split_whole, N, H, hd, o.data_ptr(), D,
-                                                 ctx["apart"].data_ptr(), ctx["apart_bytes"]), "attention_split")
+            timed("attention", lambda: ck(lib.qvl_attention_headmajor_split(
+                st, dt, qb, kb, vb, md.split_tiles, md.n_split_tiles, md.n_split_whole, N, H, hd, o.data_ptr(), D,
+                ctx["apart"].data_ptr(), ctx["apart_bytes"]), "attention_split"))
         else:
-            ck(lib.qvl_attention_headmajor(st, dt, qb, kb, vb, md.tiles, md.n_tiles, N, H, hd, o.data_ptr(), D),
-               "attention")
-        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D,
-                            x.data_ptr(), D, N, D, D, gws, gwn), "proj")
-        if fold:
+            timed("attention", lambda: ck(lib.qvl_attention_headmajor(
+                st, dt, qb, kb, vb, md.tiles, md.n_tiles, N, H, hd, o.data_ptr(), D), "attention"))
+        if G:
+            timed("proj", lambda: ck(lib.qvl_dense_rowstats_ws(
+                st, dt, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D, x.data_ptr(), D, N, D, D, parts, gws,
+                gwn), "proj (+ row partials)"))
+        else:
+            timed("proj", lambda: ck(lib.qvl_dense_ws(
+                st, dt, capi.QVL_EPI_BIAS_RESIDUAL, o.data_ptr(), D, B.proj_w, B.proj_b, x.data_ptr(), D, x.data_ptr(),
+                D, N, D, D, gws, gwn), "proj"))
+        if G:
+            timed("fc1", lambda: ck(lib.qvl_dense_ln_parts_ws(
+                st, dt, capi.QVL_EPI_BIAS_GELU, x.data_ptr(), D, ff[0].data_ptr(), ff[1].data_ptr(), parts, G, 1e-6,
+                B.fc1_b, h.data_ptr(), I, N, I, D, gws, gwn), "fc1 (folded ln2)"))
+        elif fold:
             ck(lib.qvl_row_stats(st, dt, x.data_ptr(), D, N, D, 1e-6, stats), "ln2 stats")
-            ck(lib.qvl_dense_ln_ws(st, dt, capi.QVL_EPI_BIAS_GELU, x.data_ptr(), D, ff[0].data_ptr(), ff[1].data_ptr(),
-                                   stats, B.fc1_b, h.data_ptr(), I, N, I, D, gws, gwn), "fc1 (folded ln2)")
+            timed("fc1", lambda: ck(lib.qvl_dense_ln_ws(
+                st, dt, capi.QVL_EPI_BIAS_GELU, x.data_ptr(), D, ff[0].data_ptr(), ff[1].data_ptr(), stats, B.fc1_b,
+                h.data_ptr(), I, N, I, D, gws, gwn), "fc1 (folded ln2)"))
         else:
             ck(lib.qvl_layer_norm(st, dt, x.data_ptr(), D, B.norm2_w, B.norm2_b, xn.data_ptr(), D, N, D, 1e-6), "ln2")
-            ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_GELU, xn.data_ptr(), D, B.fc1_w, B.fc1_b, None, 0,
-                                h.data_ptr(), I, N, I, D, gws, gwn), "fc1")
-        ck(lib.qvl_dense_ws(st, dt, capi.QVL_EPI_BIAS_RESIDUAL, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D,
-                            x.data_ptr(), D, N, D, I, gws, gwn), "fc2")
+            timed("fc1", lambda: ck(lib.qvl_dense_ws(
+                st, dt, capi.QVL_EPI_BIAS_GELU, xn.data_ptr(), D, B.fc1_w, B.fc1_b, None, 0, h.data_ptr(), I, N, I, D,
+                gws, gwn), "fc1"))
+        if G:
+            timed("fc2", lambda: ck(lib.qvl_dense_rowstats_ws(
+                st, dt, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D, x.data_ptr(), D, N, D, I, parts, gws, gwn),
+                "fc2 (+ row partials)"))
+        else:
+            timed("fc2", lambda: ck(lib.qvl_dense_ws(
+                st, dt, capi.QVL_EPI_BIAS_RESIDUAL, h.data_ptr(), I, B.fc2_w, B.fc2_b, x.data_ptr(), D, x.data_ptr(), D,
+                N, D, I, gws, gwn), "fc2"))
 
     def merger_fused(self, x, ctx, which: int = -1):
-        """The merger as the whole-tower call runs it: a deepstack merger of a tower with ln_fold takes
-        qvl_row_stats of the [N/4, 4D] rows and the folded fc1 (qvl_dense_ln_ws); every other merger
-        is merger_staged."""
+        """The merger as the whole-tower call runs it: a deepstack merger of a tower with ln_fold folds
+        its post-shuffle norm into fc1 (qvl_dense_ln_ws on the [N/4, 4D] rows; the tower reads the
+        row partials fc2 wrote, here on its own the statistics come from qvl_row_stats); every other
+        merger is merger_staged."""
         if which < 0 or not self.ln_fold:
             return self.merger_staged(x, ctx, which)
         torch = _torch()

@@ -80,6 +80,23 @@ def stats(lib, cp, x, cols):
     return st
 
 
+def host_parts(x):
+    """Per-128-column (sum, sum of squared deviations from the group mean) of bf16-valued rows, fp64."""
+    m, k = x.shape
+    g = np.asarray(x, np.float64).reshape(m, k // 128, 128)
+    s = g.sum(-1)
+    return np.stack([s, ((g - s[..., None] / 128) ** 2).sum(-1)], -1).astype(np.float32)
+
+
+def combine_parts(parts):
+    """(mean, var) of each row from its partials, fp64 (Chan et al.'s pairwise update)."""
+    p = np.asarray(parts, np.float64)
+    n = 128 * p.shape[1]
+    mean = p[..., 0].sum(-1) / n
+    m2 = (p[..., 1] + (p[..., 0] - 128 * mean[:, None]) ** 2 / 128).sum(-1)
+    return mean, m2 / n
+
+
 @pytest.mark.parametrize("cols", [1024, 1152, 4096])
 def test_row_stats_vs_fp64(pkg, lib, cols):
     """(mean, rstd) per row: within 1e-6 (mean, relative to |mean| + std) and 2e-6 (rstd, relative)
@@ -208,7 +225,8 @@ def test_qkv_rotary_ln_vs_reference(pkg, lib, hd, grids, plan):
     try:
         if plan:
             cp.check(lib.qvl_set_gemm_plan(1, 1, 0))
-        for mode in ("unfolded", "folded", "folded_tab"):
+        parts = torch.from_numpy(host_parts(x)).to(DEV)
+        for mode in ("unfolded", "folded", "folded_tab", "folded_parts"):
             if mode == "folded_tab" and hd != 64:
                 continue
             q = torch.full((H, Np, hdp), 5.0, dtype=torch.bfloat16, device=DEV)
@@ -218,6 +236,13 @@ def test_qkv_rotary_ln_vs_reference(pkg, lib, hd, grids, plan):
                 cp.check(lib.qvl_dense_qkv_rotary(stream(), cp.QVL_DTYPE_BF16, xn.data_ptr(), D, w.data_ptr(),
                                                   bias.data_ptr(), cs.data_ptr(), q.data_ptr(), k.data_ptr(),
                                                   vtm.data_ptr(), N, D, H, ws.data_ptr(), nb.value))
+            elif mode == "folded_parts":
+                tb = hd == 64
+                cp.check(lib.qvl_dense_qkv_rotary_ln_parts(
+                    stream(), cp.QVL_DTYPE_BF16, xt.data_ptr(), D, wf.data_ptr(), cd.data_ptr(), parts.data_ptr(),
+                    D // 128, EPS, bias.data_ptr(), None if tb else cs.data_ptr(), pos.data_ptr() if tb else None,
+                    tab.data_ptr() if tb else None, P if tb else 0, q.data_ptr(), k.data_ptr(), vtm.data_ptr(), N, D,
+                    H, ws.data_ptr(), nb.value))
             else:
                 tb = mode == "folded_tab"
                 cp.check(lib.qvl_dense_qkv_rotary_ln(stream(), cp.QVL_DTYPE_BF16, xt.data_ptr(), D, wf.data_ptr(),
@@ -248,5 +273,125 @@ def test_qkv_rotary_ln_vs_reference(pkg, lib, hd, grids, plan):
         assert np.isfinite(got).all(), name
         assert rel_l2(got, unf) <= 6e-3, name
         assert rel_l2(got, ex) <= 1.25 * rel_l2(unf, ex) + 5e-4, name
+    # the statistics as 128-column partials: the same fold up to fp32 rounding of mean and rstd
+    for name, got, st_form, ex in zip("qkv", view(outs["folded_parts"]), view(outs["folded"]), exact):
+        assert rel_l2(got, st_form) <= 2e-3, name
+        assert rel_l2(got, ex) <= 1.25 * rel_l2(st_form, ex) + 5e-4, name
     q, k, _ = outs["folded"]
     assert not q[:, N:].any() and not k[:, N:].any() and not q[:, :, hd:].any()
+
+
+def rowstats_dense(lib, cp, x, w, bias, res, n, k, ws, nb):
+    m = x.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    parts = torch.full((m, n // 128, 2), float("nan"), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_dense_rowstats_ws(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), k, w.data_ptr(), bias.data_ptr(),
+                                       res.data_ptr(), n, y.data_ptr(), n, m, n, k, parts.data_ptr(), ws.data_ptr(), nb))
+    return y, parts
+
+
+@pytest.mark.parametrize("m,n,k,plan", [(1000, 1024, 4096, 0), (517, 1152, 1152, 0), (600, 1024, 1024, 1),
+                                        (300, 1280, 1024, 3)])
+def test_dense_rowstats(pkg, lib, m, n, k, plan):
+    """qvl_dense_rowstats_ws: the residual Dense's output bit for bit as qvl_dense_ws gives it (under a
+    pinned tile plan when plan > 0: 288x256, or 256x128 for plan 3; the split-K tail is never used
+    with row statistics, so the comparison pins the split off too), and per 128-column group of each
+    row the sum and the sum of squared deviations of those bf16 outputs within fp32 summation error
+    of fp64 (rows with offsets up to 40 standard deviations)."""
+    cp = pkg.capi
+    rng = np.random.default_rng(m + n + k)
+    x = torch.from_numpy(rows(rng, m, k)).to(DEV).to(torch.bfloat16)
+    res = torch.from_numpy(rows(rng, m, n)).to(DEV).to(torch.bfloat16)
+    w = pack(lib, cp, (rng.standard_normal((k, n)) * 0.03).astype(np.float32))
+    bias = torch.from_numpy(vt.bf16_round((rng.standard_normal(n) * 0.1).astype(np.float32))).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    y_ws = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    try:
+        cp.check(lib.qvl_set_gemm_plan(plan, -1, 0))
+        y, parts = rowstats_dense(lib, cp, x, w, bias, res, n, k, ws, nb.value)
+        cp.check(lib.qvl_dense_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_RESIDUAL, x.data_ptr(), k, w.data_ptr(),
+                                  bias.data_ptr(), res.data_ptr(), n, y_ws.data_ptr(), n, m, n, k, ws.data_ptr(),
+                                  nb.value))
+    finally:
+        cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
+    torch.cuda.synchronize()
+    yh = to_np(y)
+    np.testing.assert_array_equal(yh, to_np(y_ws))
+    got = parts.cpu().numpy()
+    want = host_parts(yh).astype(np.float64)
+    g = np.abs(yh.astype(np.float64)).reshape(m, n // 128, 128)
+    assert np.isfinite(got).all()
+    assert np.all(np.abs(got[..., 0] - want[..., 0]) <= 1e-6 * g.sum(-1) + 1e-30)
+    assert np.all(np.abs(got[..., 1] - want[..., 1]) <= 1e-5 * want[..., 1] + 1e-11 * g.sum(-1) ** 2)
+    mean, var = combine_parts(got)
+    y64 = yh.astype(np.float64)
+    mu = y64.mean(-1)
+    v64 = ((y64 - mu[:, None]) ** 2).mean(-1)
+    assert np.all(np.abs(mean - mu) <= 1e-6 * (np.abs(mu) + np.sqrt(v64)))
+    assert np.all(np.abs(var / v64 - 1) <= 1e-5)
+
+
+@pytest.mark.parametrize("shape", ["fc1", "merger"])
+def test_rowstats_feed_folded_dense(pkg, lib, shape):
+    """The tower's chain without a LayerNorm launch: a residual Dense writes x and its partials,
+    qvl_dense_ln_parts_ws (bias+GELU) consumes them, as fc1 after proj or a deepstack merger's fc1
+    after fc2 (the [N/4, 4D] view: 4 token rows = 32 groups). Against qvl_row_stats +
+    qvl_dense_ln_ws on the same x (the same fold, statistics by the other route: within 2e-3),
+    against the reference's bf16 LayerNorm + Dense (6e-3) and no further from exact fp64 than it."""
+    cp = pkg.capi
+    D, m = 1024, 1000
+    rng = np.random.default_rng(11 if shape == "fc1" else 12)
+    x0 = torch.from_numpy(rows(rng, m, D)).to(DEV).to(torch.bfloat16)
+    r0 = torch.from_numpy(rows(rng, m, D)).to(DEV).to(torch.bfloat16)
+    wp = pack(lib, cp, (rng.standard_normal((D, D)) * 0.03).astype(np.float32))
+    bp = torch.from_numpy(vt.bf16_round((rng.standard_normal(D) * 0.1).astype(np.float32))).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    x, parts = rowstats_dense(lib, cp, x0, wp, bp, r0, D, D, ws, nb.value)
+    rows_n, k = (m, D) if shape == "fc1" else (m // 4, 4 * D)
+    n = 4096
+    g, b = ln_params(rng, k)
+    w_h = (rng.standard_normal((k, n)) * 0.03).astype(np.float32)
+    b_h = vt.bf16_round((rng.standard_normal(n) * 0.1).astype(np.float32))
+    wf, cd = fold(lib, cp, pack(lib, cp, w_h), g, b)
+    bias = torch.from_numpy(b_h).to(DEV)
+    y_parts = torch.empty((rows_n, n), dtype=torch.bfloat16, device=DEV)
+    y_stats = torch.empty_like(y_parts)
+    cp.check(lib.qvl_dense_ln_parts_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, x.data_ptr(), k,
+                                       wf.data_ptr(), cd.data_ptr(), parts.data_ptr(), k // 128, EPS, bias.data_ptr(),
+                                       y_parts.data_ptr(), n, rows_n, n, k, ws.data_ptr(), nb.value))
+    st = stats(lib, cp, x.view(rows_n, k), k)
+    cp.check(lib.qvl_dense_ln_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, x.data_ptr(), k, wf.data_ptr(),
+                                 cd.data_ptr(), st.data_ptr(), bias.data_ptr(), y_stats.data_ptr(), n, rows_n, n, k,
+                                 ws.data_ptr(), nb.value))
+    torch.cuda.synchronize()
+    got, alt = to_np(y_parts), to_np(y_stats)
+    xh = to_np(x).reshape(rows_n, k)
+    xn64 = ln64(xh, g, b)
+    exact = gelu64(xn64 @ vt.bf16_round(w_h).astype(np.float64) + b_h)
+    ref = ref_bf16_dense(vt.bf16_round(xn64.astype(np.float32)), w_h, b_h, 1)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, alt) <= 2e-3
+    assert rel_l2(got, ref) <= 6e-3
+    assert rel_l2(got, exact) <= 1.25 * rel_l2(ref, exact) + 5e-4
+
+
+def test_rowstats_rejects_bad_shapes(pkg, lib):
+    """Row statistics need 128-column groups and 8-element row strides; the folded entries need
+    groups * 128 == the LayerNorm width and a positive eps (checked on the host, no launch)."""
+    cp = pkg.capi
+    bad = []
+    p = torch.empty(1 << 16, dtype=torch.uint8, device=DEV)
+    a = p.data_ptr()
+    bad.append(lib.qvl_dense_rowstats_ws(stream(), cp.QVL_DTYPE_BF16, a, 64, a, a, a, 192, a, 192, 8, 192, 64, a, a, 4096))
+    bad.append(lib.qvl_dense_rowstats_ws(stream(), cp.QVL_DTYPE_BF16, a, 64, a, a, a, 132, a, 132, 8, 128, 64, a, a, 4096))
+    bad.append(lib.qvl_dense_ln_parts_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS, a, 256, a, a, a, 1, EPS, a, a,
+                                         128, 8, 128, 256, a, 4096))
+    bad.append(lib.qvl_dense_ln_parts_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS, a, 256, a, a, a, 2, 0.0, a, a,
+                                         128, 8, 128, 256, a, 4096))
+    bad.append(lib.qvl_dense_ln_parts_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_RESIDUAL, a, 256, a, a, a, 2, EPS,
+                                         a, a, 128, 8, 128, 256, a, 4096))
+    assert all(rc != cp.QVL_OK for rc in bad), bad
