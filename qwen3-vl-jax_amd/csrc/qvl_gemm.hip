@@ -453,9 +453,8 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
 #pragma unroll
     for (int b = 0; b < S::MB; ++b) token_pos(p, base + b * 32 + l32, ph[b], pw[b]);
   }
-  LnRows<S::MB> L;
-  if constexpr (LN) L = ln_rows<S::MB>(lcd + BN, wm * S::TM + l32);
-  // one (head, 4 dims, token block) unit: bias, the folded LayerNorm (LN), rotary, into LDS
+  // one (head, 4 dims, token block) unit: bias, the folded LayerNorm (LN: the token's (rstd,
+  // -mean * rstd) from the LDS copy, read where the unit needs it), rotary, into LDS
   auto unit = [&](int h2, int g, int b, const f32x4& blo, const f32x4& bhi) {
     const int d = 8 * g + 4 * hh, n = nw + h2 * 64 + d;
     const int t = b * 32 + l32;
@@ -463,8 +462,9 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmParams& p,
 #pragma unroll
     for (int e = 0; e < 4; ++e) { lo[e] = acc[2 * h2][b][4 * g + e]; hi[e] = acc[2 * h2 + 1][b][4 * g + e]; }
     if constexpr (LN) {
-      ln_fold_group(lcd, L.r[b], L.nm[b], n - n0, lo);
-      ln_fold_group(lcd, L.r[b], L.nm[b], n - n0 + 32, hi);
+      const f32x2 rs = lcd[BN + wm * S::TM + t];
+      ln_fold_group(lcd, rs.x, rs.y, n - n0, lo);
+      ln_fold_group(lcd, rs.x, rs.y, n - n0 + 32, hi);
     }
     f32x4 c01 = {}, c23 = {};
     if (which < 2) {
