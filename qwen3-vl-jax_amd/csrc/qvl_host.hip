@@ -521,7 +521,7 @@ static int run_merger(hipStream_t st, const qvl_vision_config* c, const TowerLay
   const int64_t N = L.N, D = L.D, D4 = 4 * L.D;
   const int dt = L.dtype;
   if (postshuffle && dt == QVL_DTYPE_BF16 && mw.fc1_ln.w && mw.fc1_ln.cd && stats) {
-    if (parts_groups > 0) {
+    if (parts_groups > 0 && 4 * parts_groups <= 64) {   // (hidden <= 2048: the merger LayerNorm's width bound)
       QVL_TRY_RC(qvl_dense_ln_parts_ws(st, dt, QVL_EPI_BIAS_GELU, x, D4, mw.fc1_ln.w, mw.fc1_ln.cd, stats,
                                        4 * parts_groups, c->ln_eps, mw.fc1_b, h, D4, N / 4, D4, D4, part, L.part_bytes));
     } else {

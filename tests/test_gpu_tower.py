@@ -263,3 +263,25 @@ def test_encode_vision_api(pkg, params2b):
     assert tuple(cat.tokens.shape) == (20, 2048) and tuple(cat.deepstack[1].shape) == (20, 2048)
     with pytest.raises(ValueError, match="Vision backbone"):
         pkg.Qwen3VLModel(None).encode_vision(px, grids)
+
+
+def test_wide_tower_most_partial_groups(pkg):
+    """The widest tower the deepstack mergers take (hidden 2048: their LayerNorm spans 4 x 2048 =
+    8192 columns, the LayerNorm kernels' limit): 16 partial groups per token row and 64 per merged
+    row, the most the folded GEMMs combine (4 chunks of 16): tokens and the deepstack feature within
+    1e-2 of the bf16 oracle, with the LayerNorms fused and with LayerNorm launches."""
+    import dataclasses
+    spec = dataclasses.replace(pkg.spec_2b(), hidden_size=2048, num_heads=32, intermediate_size=1024, depth=2,
+                               deepstack_visual_indexes=(0,), out_hidden_size=512, fullatt_block_indexes=None)
+    ospec = vt.VisionSpec(hidden_size=2048, out_hidden_size=512, depth=2, num_heads=32,
+                          intermediate_size=1024, deepstack_visual_indexes=(0,))
+    params = pkg.random_params(spec, seed=5)
+    grids = [(1, 8, 12)]
+    px = pixels(grids, 6)
+    ref = vt.encode_vision(params, px, grids, ospec, "bf16")
+    g = np.array(grids, np.int32)
+    for fold in (True, False):
+        tower = pkg.Qwen3VisionTransformer(spec, ln_fold=fold).bind(params)
+        tok, ds = tower(px, g)
+        assert rel_l2(to_np(tok), ref.tokens) <= TOL, fold
+        assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, fold
