@@ -3,8 +3,10 @@
 //   y[M, N] = epi(x[M, K] . W[N, K]^T + bias)     (nn.Dense: model.py:556, 570, 601, 611-613, 655-656)
 //
 // Both operands are K-contiguous ("TN"): activations are row-major [tokens, features] and the
-// packed weights are the Flax kernel transposed. A workgroup of 8 waves (two per SIMD) computes a
-// BM x BN tile; each wave owns a (BM/4) x (BN/2) sub-tile of v_mfma_f32_32x32x16_bf16 blocks.
+// packed weights are the Flax kernel transposed. A workgroup of WM x WN waves computes a BM x BN
+// tile (the planner's shapes: 288x256 and 288x128 on 12 waves, three per SIMD; 256x256 and 256x128
+// on 8 waves, two per SIMD); each wave owns a (BM/WM) x (BN/WN) sub-tile of
+// v_mfma_f32_32x32x16_bf16 blocks.
 // The MFMA "A" operand is the weight tile and "B" the activation tile, so each lane's
 // accumulator holds one token row and runs of 4 consecutive output features: the epilogue
 // stores 8-byte pieces of a row instead of scattered 2-byte elements.
