@@ -285,3 +285,27 @@ def test_wide_tower_most_partial_groups(pkg):
         tok, ds = tower(px, g)
         assert rel_l2(to_np(tok), ref.tokens) <= TOL, fold
         assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, fold
+
+
+def test_tower_rows_not_in_128_column_groups(pkg):
+    """head_dim 72 with 8 heads (hidden 576): the qkv Dense still takes the fused rotary epilogue
+    (whole 4-head tiles), but 576 columns are not whole 128-column groups, so the residual epilogues
+    write no row partials and every fused LayerNorm (blocks and deepstack merger) takes its row
+    statistics from a qvl_row_stats launch instead: tokens and the deepstack feature within 1e-2 of
+    the bf16 oracle, with the LayerNorms fused and with LayerNorm launches."""
+    import dataclasses
+    spec = dataclasses.replace(pkg.spec_8b(), hidden_size=576, num_heads=8, intermediate_size=1152, depth=2,
+                               deepstack_visual_indexes=(0,), out_hidden_size=512, fullatt_block_indexes=None)
+    assert spec.head_dim == 72 and spec.hidden_size % 128
+    ospec = vt.VisionSpec(hidden_size=576, out_hidden_size=512, depth=2, num_heads=8,
+                          intermediate_size=1152, deepstack_visual_indexes=(0,))
+    params = pkg.random_params(spec, seed=7)
+    grids = [(1, 8, 12), (1, 6, 4)]
+    px = pixels(grids, 8)
+    ref = vt.encode_vision(params, px, grids, ospec, "bf16")
+    g = np.array(grids, np.int32)
+    for fold in (True, False):
+        tower = pkg.Qwen3VisionTransformer(spec, ln_fold=fold).bind(params)
+        tok, ds = tower(px, g)
+        assert rel_l2(to_np(tok), ref.tokens) <= TOL, fold
+        assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, fold
