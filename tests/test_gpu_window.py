@@ -58,6 +58,25 @@ def test_window_tower_vs_oracle(pkg, grids, window, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_window_tower_head_dim72_vs_oracle(pkg, dtype):
+    """Window attention on the 8B shape (head_dim 72: the general attention kernel over the window
+    work list, the rotary relayout for the windowed order): tokens and deepstack features against
+    the fp64 oracle (fp32: 1e-4) and the bf16 oracle (bf16: 1e-2)."""
+    grids = [(1, 8, 12), (2, 4, 4)]
+    spec, ospec = window_specs(pkg, depth=2, fullatt=(1,), ds=(0,), shape="8b")
+    assert spec.use_window and spec.head_dim == 72
+    params = pkg.random_params(spec, seed=33)
+    n = sum(t * h * w for t, h, w in grids)
+    px = np.random.default_rng(6).standard_normal((n, 1536), dtype=np.float32)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype=dtype).bind(params)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    ref = vt.encode_vision(params, px, grids, ospec, "fp64" if dtype == "float32" else "bf16")
+    tol = 1e-4 if dtype == "float32" else 1e-2
+    for got, r in [(to_np(tok), ref.tokens)] + [(to_np(a), b) for a, b in zip(ds, ref.deepstack)]:
+        assert rel_l2(got, r) <= tol
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 def test_window_tower_without_pos_embed(pkg, dtype):
     """A Qwen2.5-style spec: window attention and no learned pos-embed table
     (num_position_embeddings None, model.py:676-680 / 803-806): the tower runs the patch embed
