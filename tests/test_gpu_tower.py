@@ -309,3 +309,27 @@ def test_tower_rows_not_in_128_column_groups(pkg):
         tok, ds = tower(px, g)
         assert rel_l2(to_np(tok), ref.tokens) <= TOL, fold
         assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, fold
+
+
+@pytest.mark.parametrize("grids", [[(1, 2, 2)], [(1, 2, 2), (2, 2, 2), (1, 2, 4)]])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_tower_smallest_grids(pkg, grids, dtype):
+    """The smallest inputs: one 2x2 patch group (4 tokens, one merged token) and a mix of 4- and
+    8-token segments with a 2-frame video, through qvl_encode_vision: GEMM tiles of a few live
+    rows, attention segments far shorter than a query tile, mergers of 1-4 rows. Tokens and the
+    deepstack feature against the fp64 oracle (fp32: 1e-4) and the bf16 oracle (bf16: 1e-2)."""
+    import dataclasses
+    spec = dataclasses.replace(pkg.spec_2b(), depth=2, deepstack_visual_indexes=(0,))
+    ospec = vt.VisionSpec(hidden_size=spec.hidden_size, out_hidden_size=spec.out_hidden_size, depth=2,
+                          num_heads=spec.num_heads, intermediate_size=spec.intermediate_size,
+                          deepstack_visual_indexes=(0,))
+    params = pkg.random_params(spec, seed=9)
+    px = pixels(grids, 10)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype=dtype).bind(params)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    n_merged = sum(t * h * w for t, h, w in grids) // 4
+    assert tuple(tok.shape) == (n_merged, spec.out_hidden_size) and len(ds) == 1
+    ref = vt.encode_vision(params, px, grids, ospec, "fp64" if dtype == "float32" else "bf16")
+    tol = 1e-4 if dtype == "float32" else TOL
+    assert rel_l2(to_np(tok), ref.tokens) <= tol
+    assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= tol
