@@ -161,7 +161,7 @@ int qvl_rotary_table(void* stream, int32_t dtype, const int32_t* d_pos_hw, int64
  * (block-diagonal, non-causal, fp32 online softmax). Output [n_tokens, num_heads*head_dim]
  * row stride ld_out. `d_tiles` / `n_tiles` are the qvl_attention_worklist items (device copy)
  * and their count.
- * Workspace: qvl_vision_attention_workspace_size(). head_dim in {64, 72}. */
+ * Workspace: qvl_vision_attention_workspace_size(). head_dim in {64, 72, 80}. */
 int qvl_vision_attention_workspace_size(int32_t dtype, int64_t n_tokens, int32_t num_heads, int32_t head_dim,
                                         size_t* bytes);
 int qvl_vision_attention(void* stream, int32_t dtype, const void* d_q, const void* d_k,
@@ -270,8 +270,8 @@ int qvl_dense_qkv_rotary_ln_parts(void* stream, int32_t dtype, const void* d_x, 
 
 /* The varlen attention kernel alone, on head-major operands (model.py:585-600):
  * out[n, h*head_dim + d] for every n inside a segment of `d_tiles`. Layout for head_dim 64: the
- * one qvl_dense_qkv_rotary writes; for head_dim 72: q, k [H][Np][88] (dims 72..87 zero) and
- * v^T [H][72][Np], keys at the same quad-swapped positions. fp32: q, k
+ * one qvl_dense_qkv_rotary writes; for head_dim 72 or 80: q, k [H][Np][88] (dims head_dim..87
+ * zero) and v^T [H][head_dim][Np], keys at the same quad-swapped positions. fp32: q, k
  * [H][Np][head_dim], v^T [H][32*ceil(head_dim/32)][Np] (extra rows zero), keys in order. */
 int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const void* d_k, const void* d_vt,
                             const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,

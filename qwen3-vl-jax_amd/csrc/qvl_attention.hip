@@ -326,26 +326,26 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// head_dim 72 (the 8B tower): Q/K [H][Np][88] (dims 72..87 zero; the QK MFMAs use dims 0..79),
-// V^T [H][72][Np] (keys at vt_pos). Same work items, unshifted softmax with the exact fallback,
-// and block-at-a-time steady state as the hd-64 kernel. K tiles arrive by LDS DMA as contiguous
-// 176-byte rows: 11 16-byte chunks, an odd count, so the 16 rows one fragment read touches fall on
-// 16 distinct bank groups without a swizzle. V^T tiles arrive as 128-byte rows with the hd-64 kernel's XOR swizzle; the
-// third 32-row PV block reads LDS rows 72..95, which the DMA never writes: row 72 holds ones, so
-// output row 72 accumulates the softmax row sums (no VALU adds for them); rows 73..95 only feed
-// output rows that are not stored (an MFMA output row depends on its own A row only).
+// head_dim HD = 72 (the 8B tower) or 80: Q/K [H][Np][88] (dims HD..87 zero; the QK MFMAs use dims
+// 0..79), V^T [H][HD][Np] (keys at vt_pos). Same work items, unshifted softmax with the exact
+// fallback, and block-at-a-time steady state as the hd-64 kernel. K tiles arrive by LDS DMA as
+// contiguous 176-byte rows: 11 16-byte chunks, an odd count, so the 16 rows one fragment read touches
+// fall on 16 distinct bank groups without a swizzle. V^T tiles arrive as 128-byte rows with the hd-64
+// kernel's XOR swizzle; the third 32-row PV block reads LDS rows 64..95, of which the DMA writes rows
+// below HD: row HD holds ones, so output row HD accumulates the softmax row sums (no VALU adds for
+// them); the rows above it only feed output rows that are not stored (an MFMA output row depends on
+// its own A row only).
 // ---------------------------------------------------------------------------------------------
-constexpr int kHD72 = 72;
 constexpr int kQK72 = 88;                  // Q/K row length (elements)
 constexpr int kKS72 = 5;                   // QK k-steps (dims 0..79)
-constexpr int kVR72 = 72;                  // V^T rows written by the DMA
 constexpr int kNDB72 = 3;                  // 32-row PV blocks (rows 0..95)
 constexpr int kKTile72 = kAttnBN * kQK72;  // K tile elements (11 KB)
 constexpr int kVTile72 = 96 * kAttnBN;     // V^T tile elements (12 KB)
 
 __device__ __forceinline__ int k72_off(int row, int chunk) { return row * kQK72 + (chunk << 3); }
 
-__global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
+template <int HD>
+__global__ __launch_bounds__(256, 3) void attn_fwd_qk88_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
     const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo, int n_whole,
     float* __restrict__ part) {
@@ -362,7 +362,8 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
 
-  const size_t qk_head = (size_t)Np * kQK72, v_head = (size_t)kVR72 * Np;
+  static_assert(HD == 72 || HD == 80, "88-element Q/K rows, three 32-row PV blocks");
+  const size_t qk_head = (size_t)Np * kQK72, v_head = (size_t)HD * Np;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + head * qk_head, (uint32_t)(qk_head * 2));
   const int qrow = q0 + wave * 32 + l32;
   bf16x8 qf[kKS72];
@@ -370,10 +371,10 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   for (int ks = 0; ks < kKS72; ++ks)
     qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qrow * kQK72 + ks * 16 + hh * 8) * 2)));
 
-  // Tile DMA, 20 instructions of 1 KB, 5 per wave: K instructions 0..10 copy the tile's 11264
-  // contiguous bytes (lane j -> byte 16j of the kilobyte); V^T instructions 0..8 fill rows
-  // [8i, 8i+8), lane j in row 8i + j/8 at physical chunk j%8, fetching the logical chunk the read
-  // swizzle maps there ((row/2)%8 alternates with the parity of i).
+  // Tile DMA, 11 + HD/8 instructions of 1 KB dealt round-robin to the 4 waves: K instructions 0..10
+  // copy the tile's 11264 contiguous bytes (lane j -> byte 16j of the kilobyte); V^T instructions
+  // 0..HD/8-1 fill rows [8i, 8i+8), lane j in row 8i + j/8 at physical chunk j%8, fetching the
+  // logical chunk the read swizzle maps there ((row/2)%8 alternates with the parity of i).
   const u32x4 rk = rsrc_words(K + head * qk_head, (uint32_t)(qk_head * 2));
   const u32x4 rv = rsrc_words(Vt + head * v_head, (uint32_t)(v_head * 2));
   const uint32_t k_lane = (uint32_t)(lane * 16);
@@ -384,12 +385,13 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   constexpr uint32_t kStageBytes = (kKTile72 + kVTile72) * 2;
   auto dma_tile = [&](int kb, int stage) {
     const uint32_t kl = lds0 + stage * kStageBytes, vl = kl + kKTile72 * 2;
+    constexpr int kInstr = 11 + HD / 8;
 #pragma unroll
-    for (int j = 0; j < 5; ++j) {
-      const int n = wave + 4 * j;             // instruction 0..19, wave-uniform
+    for (int j = 0; j < (kInstr + 3) / 4; ++j) {
+      const int n = wave + 4 * j;             // instruction 0..kInstr-1, wave-uniform
       if (n < 11) {
         dma16(rk, k_lane, (uint32_t)(kb * kQK72 * 2 + n * 1024), kl + n * 1024);
-      } else {
+      } else if (kInstr % 4 == 0 || n < kInstr) {   // (72: 20 instructions, 5 per wave, no check)
         const int i = n - 11;                 // V^T rows [8i, 8i+8)
         dma16(rv, v_lane[i & 1], (uint32_t)(((int64_t)8 * i * Np + kb) * 2), vl + 8 * i * kAttnBN * 2);
       }
@@ -404,10 +406,10 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
   const int n_kt = t1 - t0;
   dma_tile(k_begin, 0);
-  // Row 72 of both V^T stages holds ones (the DMA fills rows 0..71 only): the third PV block then
-  // accumulates each query's row sum of the bf16 P in O^T row 72.
+  // Row HD of both V^T stages holds ones (the DMA fills rows 0..HD-1 only): the third PV block then
+  // accumulates each query's row sum of the bf16 P in O^T row HD.
   if (tid < 16)
-    *reinterpret_cast<u32x4*>(smem + (tid >> 3) * (kKTile72 + kVTile72) + kKTile72 + kVR72 * kAttnBN + (tid & 7) * 8) =
+    *reinterpret_cast<u32x4*>(smem + (tid >> 3) * (kKTile72 + kVTile72) + kKTile72 + HD * kAttnBN + (tid & 7) * 8) =
         u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   wait_dma();
   __syncthreads();
@@ -472,19 +474,21 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
     step(std::true_type{}, int_c<1>{}, it);
   }
 
-  // O^T row 72 (block 2, register 4 of the lanes with hh = 0) is the row sum of query l32
-  const float l_row = oacc[2][4], l_swap = __shfl_xor(l_row, 32);
-  float l_tot = hh ? l_swap : l_row;
-  // |O| over the stored rows: block 2 holds output rows 64..71 in registers 0..3; its other
-  // registers are the row sum (row 72) and rows 73..95, products of LDS rows the DMA never writes
+  // O^T row HD is the row sum of query l32: block 2's local row RS = HD - 64 sits in register
+  // 4 (RS / 8) + RS % 4 of the lanes with hh = (RS % 8) / 4 (72: register 4, 80: register 8; hh 0)
+  constexpr int RS = HD - 64, RS_REG = 4 * (RS / 8) + RS % 4, RS_HH = (RS % 8) / 4;
+  const float l_row = oacc[2][RS_REG], l_swap = __shfl_xor(l_row, 32);
+  float l_tot = hh == RS_HH ? l_row : l_swap;
+  // |O| over the stored rows: block 2 holds output rows 64..HD-1 in registers 0..4 (RS / 8) - 1; its
+  // other registers are the row sum (row HD) and rows above it, products of LDS rows the DMA never writes
   float omax = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) omax = fmaxf(omax, fmaxf(fabsf(oacc[0][r]), fabsf(oacc[1][r])));
 #pragma unroll
-  for (int r = 0; r < 4; ++r) omax = fmaxf(omax, fabsf(oacc[2][r]));
+  for (int r = 0; r < 4 * (RS / 8); ++r) omax = fmaxf(omax, fabsf(oacc[2][r]));
   if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !(omax <= 0x1p120f)) != 0) {
     // As in attn_fwd_hd64_kernel: recompute this wave's rows shifted by the exact row max, from
-    // global memory; the row sum by fp32 adds (V^T rows past 71 read as zero: one head's range).
+    // global memory; the row sum by fp32 adds (V^T rows past HD - 1 read as zero: one head's range).
     const __amdgpu_buffer_rsrc_t rkg = make_rsrc(K + head * qk_head, (uint32_t)(qk_head * 2));
     const __amdgpu_buffer_rsrc_t rvg = make_rsrc(Vt + head * v_head, (uint32_t)(v_head * 2));
     bf16x8 qg[kKS72];
@@ -540,30 +544,30 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_hd72_kernel(
   }
   if (parts) {
     if (qrow < seg_e) {
-      float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(kHD72);
+      float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(HD);
       const int ql = wave * 32 + l32;
 #pragma unroll
       for (int db = 0; db < kNDB72; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = db * 32 + 8 * g + 4 * hh;
-          if (d >= kHD72) continue;
-          *reinterpret_cast<f32x4*>(pp + ql * kHD72 + d) =
+          if (d >= HD) continue;
+          *reinterpret_cast<f32x4*>(pp + ql * HD + d) =
               f32x4{oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]};
         }
-      if (hh == 0) *reinterpret_cast<f32x2*>(pp + kAttnBM * kHD72 + 2 * ql) = f32x2{m_run, l_tot};
+      if (hh == 0) *reinterpret_cast<f32x2*>(pp + kAttnBM * HD + 2 * ql) = f32x2{m_run, l_tot};
     }
     return;
   }
   const float inv = 1.0f / l_tot;
   if (qrow < seg_e) {
-    bf16* orow = O + (int64_t)qrow * ldo + head * kHD72;
+    bf16* orow = O + (int64_t)qrow * ldo + head * HD;
 #pragma unroll
     for (int db = 0; db < kNDB72; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + 8 * g + 4 * hh;
-        if (d >= kHD72) continue;
+        if (d >= HD) continue;
         u32x2 o = {pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
                    pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv)};
         *reinterpret_cast<u32x2*>(orow + d) = o;
@@ -685,13 +689,19 @@ __global__ __launch_bounds__(256) void attn_relayout_general_kernel(
 int attention_general(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
                       int H, int hd, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole, float* part) {
   if (n_tiles == 0) return QVL_OK;
-  if (hd != kHD72) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (general kernel: 72)", hd);
+  if (hd != 72 && hd != 80)
+    return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (general kernel: 72, 80)", hd);
   if (n_whole < 0) n_whole = n_tiles;
-  hipLaunchKernelGGL(attn_fwd_hd72_kernel, dim3((unsigned)n_tiles), dim3(256), 0, stream, Qb, Kb, Vtb, d_tiles, Np, H,
-                     out, ldo, (int)n_whole, part);
-  int rc = check_launch("attn_fwd_hd72");
+  if (hd == 72)
+    hipLaunchKernelGGL(attn_fwd_qk88_kernel<72>, dim3((unsigned)n_tiles), dim3(256), 0, stream, Qb, Kb, Vtb, d_tiles,
+                       Np, H, out, ldo, (int)n_whole, part);
+  else
+    hipLaunchKernelGGL(attn_fwd_qk88_kernel<80>, dim3((unsigned)n_tiles), dim3(256), 0, stream, Qb, Kb, Vtb, d_tiles,
+                       Np, H, out, ldo, (int)n_whole, part);
+  int rc = check_launch("attn_fwd_qk88");
   if (rc || n_whole >= n_tiles || !part) return rc;
-  return launch_combine<kHD72>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
+  return hd == 72 ? launch_combine<72>(d_tiles, n_tiles, n_whole, part, out, ldo, stream)
+                  : launch_combine<80>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
 }
 
 int attention_relayout_general(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,

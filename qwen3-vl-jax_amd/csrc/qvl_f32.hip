@@ -489,8 +489,11 @@ int attention_f32(const float* Qb, const float* Kb, const float* Vtb, const int*
   else if (hd == 72)
     hipLaunchKernelGGL(attn_fwd_f32_kernel<72>, dim3((unsigned)n_items), dim3(256), 0, stream, Qb, Kb, Vtb, d_items,
                        Np, out, ldo);
+  else if (hd == 80)
+    hipLaunchKernelGGL(attn_fwd_f32_kernel<80>, dim3((unsigned)n_items), dim3(256), 0, stream, Qb, Kb, Vtb, d_items,
+                       Np, out, ldo);
   else
-    return set_error(QVL_ERR_UNSUPPORTED, "attention f32: head_dim=%d (supported: 64, 72)", hd);
+    return set_error(QVL_ERR_UNSUPPORTED, "attention f32: head_dim=%d (supported: 64, 72, 80)", hd);
   return check_launch("attn_fwd_f32");
 }
 

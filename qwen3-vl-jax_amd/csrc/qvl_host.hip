@@ -190,11 +190,12 @@ static int64_t attn_np(int64_t n) { return round_up(std::max<int64_t>(n, 1), 64)
 // head_dim 72 stores Q/K rows of 88 (176 bytes, the hd-72 kernel's DMA / LDS row) and V^T rows
 // 0..71; fp32 keeps Q/K exact and pads V^T to 32-row blocks.
 static int attn_dims(int dtype, int hd, int* hdp, int* vrows) {
-  if (hd != 64 && hd != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72)", hd);
+  if (hd != 64 && hd != 72 && hd != 80)
+    return set_error(QVL_ERR_UNSUPPORTED, "attention: head_dim=%d (supported: 64, 72, 80)", hd);
   if (dtype == QVL_DTYPE_F32) { *hdp = hd; *vrows = (int)round_up(hd, 32); return QVL_OK; }
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention: dtype %d", dtype);
   *hdp = hd == 64 ? 64 : 88;
-  *vrows = hd == 64 ? 64 : 72;
+  *vrows = hd;
   return QVL_OK;
 }
 
@@ -404,7 +405,8 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* q, const vo
 int qvl_attention_split_workspace_size(int32_t head_dim, int64_t n_tiles, int64_t n_whole, size_t* bytes) {
   if (!bytes || n_tiles < 0 || n_whole < 0 || n_whole > n_tiles)
     return set_error(QVL_ERR_INVALID_ARG, "attention split ws: bad args");
-  if (head_dim != 64 && head_dim != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", head_dim);
+  if (head_dim != 64 && head_dim != 72 && head_dim != 80)
+    return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", head_dim);
   *bytes = (size_t)(n_tiles - n_whole) * attn_partial_floats(head_dim) * sizeof(float);
   return QVL_OK;
 }
@@ -413,7 +415,7 @@ int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* q, co
                                   const int32_t* tiles, int64_t n_tiles, int64_t n_whole, int64_t n_tokens, int32_t H,
                                   int32_t hd, void* out, int64_t ld_out, void* ws, size_t ws_bytes) {
   if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention split: bf16 only");
-  if (hd != 64 && hd != 72) return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", hd);
+  if (hd != 64 && hd != 72 && hd != 80) return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", hd);
   if (n_tokens < 0 || H <= 0 || n_tiles < 0 || n_whole < 0 || n_whole > n_tiles || ld_out < (int64_t)H * hd ||
       ld_out % 4)
     return set_error(QVL_ERR_INVALID_ARG, "attention split: bad sizes");

@@ -261,15 +261,15 @@ int qvl_attention_worklist_split(const int32_t* cu, int64_t n_seg, int32_t num_h
                                  int32_t n_cus, int32_t* items, int64_t capacity, int64_t* n_items,
                                  int64_t* n_whole) {
   if (!n_items || !n_whole) return set_error(QVL_ERR_INVALID_ARG, "worklist_split: n_items / n_whole is NULL");
-  if (head_dim != 64 && head_dim != 72)
-    return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: head_dim=%d (supported: 64, 72)", head_dim);
+  if (head_dim != 64 && head_dim != 72 && head_dim != 80)
+    return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: head_dim=%d (supported: 64, 72, 80)", head_dim);
   if (n_cus <= 0) return set_error(QVL_ERR_INVALID_ARG, "worklist_split: n_cus=%d", n_cus);
   if (num_heads > kAttnHeadMask) return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: num_heads=%d", num_heads);
   int64_t n = 0;
   QVL_TRY_RC(qvl_attention_worklist(cu, n_seg, num_heads, nullptr, 0, &n));
   std::vector<int32_t> base(4 * (size_t)std::max<int64_t>(n, 1));
   QVL_TRY_RC(qvl_attention_worklist(cu, n_seg, num_heads, base.data(), n, &n));
-  // The last round of workgroup slots: the kernels run 4 (head_dim 64) or 3 (72) workgroups per
+  // The last round of workgroup slots: the kernels run 4 (head_dim 64) or 3 (72, 80) workgroups per
   // CU. When that round's items leave at least half of the CUs idle, each is split along its key
   // tiles into up to 8 parts (at least 2 tiles each) so that the parts fill the slots. A round
   // with one workgroup on most CUs is not split: a CU's lone workgroup runs faster than one of

@@ -53,7 +53,7 @@ int qvl_attention_headmajor_split_noalloc(void* stream, int32_t dtype, const voi
                                           const int32_t* tiles, int64_t n_tiles, int64_t n_whole, int64_t n_tokens,
                                           int32_t H, int32_t hd, void* out, int64_t ld_out) {
   size_t need = 0;
-  if (n_tiles >= 0 && n_whole >= 0 && n_whole <= n_tiles && (hd == 64 || hd == 72)) {
+  if (n_tiles >= 0 && n_whole >= 0 && n_whole <= n_tiles && (hd == 64 || hd == 72 || hd == 80)) {
     int rc = qvl_attention_split_workspace_size(hd, n_tiles, n_whole, &need);
     if (rc) return rc;
     if (need > kNoAllocScratchBytes)

@@ -582,7 +582,7 @@ class Qwen3VisionTransformer:
             md.window_tiles = tens["window_tiles"].data_ptr()
             md.window_index = tens["window_index"].data_ptr()
             md.window_reverse = tens["window_reverse"].data_ptr()
-        if self.split_attention and self.qdtype == capi.QVL_DTYPE_BF16 and s.head_dim in (64, 72):
+        if self.split_attention and self.qdtype == capi.QVL_DTYPE_BF16 and s.head_dim in (64, 72, 80):
             n_cus = torch.cuda.get_device_properties(torch.device(self.device)).multi_processor_count
             cu_full = m.cu_full if s.use_window else m.cu_seqlens
             split, n_whole = attention_worklist_split(cu_full, s.num_heads, s.head_dim, n_cus)

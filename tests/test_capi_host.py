@@ -217,6 +217,7 @@ def _split_list(pkg, cu, heads, hd, n_cus):
                                                ([0, 7056], 16, 72, 256),                # config 4: 6 parts
                                                ([0, 1024, 2048, 6144], 16, 72, 256),    # 768 items, 768 slots
                                                ([0, 4096, 4100], 16, 72, 58),   # 1-tile items stay whole
+                                               ([0, 130, 4226], 2, 80, 22),     # head_dim 80: 3 per CU
                                                ([0, 200], 2, 64, 8)])
 def test_attention_worklist_split(pkg, cu, heads, hd, n_cus):
     """The split list keeps the whole items in place, empties those of the last partial round of
@@ -258,7 +259,7 @@ def test_attention_worklist_split_checks(pkg):
     cu = np.array([0, 256], np.int32)
     n, nw = C.c_int64(), C.c_int64()
     p = cu.ctypes.data_as(C.POINTER(C.c_int32))
-    assert lib.qvl_attention_worklist_split(p, 1, 16, 80, 256, None, 0, C.byref(n), C.byref(nw)) == -2
+    assert lib.qvl_attention_worklist_split(p, 1, 16, 96, 256, None, 0, C.byref(n), C.byref(nw)) == -2
     assert lib.qvl_attention_worklist_split(p, 1, 16, 64, 0, None, 0, C.byref(n), C.byref(nw)) == -1
     assert lib.qvl_attention_worklist_split(p, 1, 16, 64, 256, None, 0, C.byref(n), C.byref(nw)) == 0
     small = np.zeros((1, 4), np.int32)

@@ -145,9 +145,9 @@ def test_attention_f32_config1_vs_fp64(pkg, lib):
     assert rel_l2(got, ref) <= 1e-5
 
 
-@pytest.mark.parametrize("hd", [64, 72])
+@pytest.mark.parametrize("hd", [64, 72, 80])
 def test_attention_f32_ragged_vs_fp64(pkg, lib, hd):
-    """Ragged segments (4..130 tokens) and head_dim 72: per-segment rel-L2 <= 1e-5."""
+    """Ragged segments (4..130 tokens) at head_dim 64, 72 and 80: per-segment rel-L2 <= 1e-5."""
     got, ref, m = _attention_f32(pkg, lib, [(1, 2, 2), (1, 4, 2), (3, 2, 6), (1, 10, 14), (1, 64, 2)], 3, hd, 4)
     assert np.isfinite(got).all()
     cu = m.cu_seqlens

@@ -227,9 +227,12 @@ def test_attention_config4_hd72_vs_oracle(pkg, lib):
     assert rel_l2(got, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("hd", [72, 80])
 @pytest.mark.parametrize("grids", [[(1, 2, 2), (1, 4, 2), (3, 2, 6)], [(1, 10, 14), (2, 6, 8)]])
-def test_attention_hd72_ragged(pkg, lib, grids):
-    got, ref, m = _attention_case(pkg, lib, grids, H=2, hd=72, seed=4)
+def test_attention_hd72_ragged(pkg, lib, grids, hd):
+    """The 88-element-row kernel (head_dim 72 and 80) on tiny and ragged segments: per-segment
+    rel-L2 <= 1e-2 against the oracle, every row finite."""
+    got, ref, m = _attention_case(pkg, lib, grids, H=2, hd=hd, seed=4)
     assert np.isfinite(got).all()
     cu = m.cu_seqlens
     for i in range(len(cu) - 1):
@@ -237,10 +240,18 @@ def test_attention_hd72_ragged(pkg, lib, grids):
         assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (i, s, e)
 
 
+def test_attention_hd80_vs_oracle(pkg, lib):
+    """head_dim 80 (a 1280-wide, 16-head tower's heads; here 4 heads) on one 2304-token segment: the
+    88-element-row kernel with the ones row at 80 for the row sums, rel-L2 <= 1e-2 vs the oracle."""
+    got, ref, _ = _attention_case(pkg, lib, [(1, 48, 48)], H=4, hd=80, seed=10)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) <= 1e-2
+
+
 def _headmajor_operands(H, hd, cu, seed):
     """Random head-major attention operands in qvl_attention_headmajor's bf16 layout: q (already
     scaled by head_dim^-0.5 * log2 e) and k as [H][Np][hdp], v^T as [H][vrows][Np] with the keys
-    at their vt_pos positions (hdp, vrows = 64, 64 or 88, 72), padding zero."""
+    at their vt_pos positions (hdp, vrows = 64, 64 or 88, hd), padding zero."""
     N = int(cu[-1])
     Np = (max(N, 1) + 63) // 64 * 64
     hdp = 64 if hd == 64 else 88
@@ -271,7 +282,8 @@ def _headmajor_operands(H, hd, cu, seed):
 @pytest.mark.parametrize("hd,cu,H,n_cus", [(64, [0, 4096, 8192, 18432], 16, 280),     # config 2's segments, 8 parts
                                            (72, [0, 7056], 16, 256),                   # config 4, 6 parts
                                            (64, [0, 1000, 1003, 5099, 5100], 4, 20),  # ragged, 1-key segments
-                                           (72, [0, 130, 4226], 2, 22)])
+                                           (72, [0, 130, 4226], 2, 22),
+                                           (80, [0, 130, 4226], 2, 22)])
 def test_attention_split_items_match_whole(pkg, lib, hd, cu, H, n_cus):
     """qvl_attention_headmajor_split on a split list agrees with qvl_attention_headmajor on the
     whole list (rel-L2 <= 5e-3: only the bf16 rounding of P against the parts' running maxima
@@ -309,7 +321,7 @@ def test_attention_split_items_match_whole(pkg, lib, hd, cu, H, n_cus):
             assert rel_l2(parts[s:e], ref[s:e]) <= 1e-2, (s, e)
 
 
-@pytest.mark.parametrize("hd", [64, 72])
+@pytest.mark.parametrize("hd", [64, 72, 80])
 @pytest.mark.parametrize("spike", [40.0, 100.0])
 def test_attention_late_score_spike(pkg, lib, hd, spike):
     """Scores far above the first key tile's maximum: the kernels hold the first tile's max m and

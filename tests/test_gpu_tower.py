@@ -333,3 +333,30 @@ def test_tower_smallest_grids(pkg, grids, dtype):
     tol = 1e-4 if dtype == "float32" else TOL
     assert rel_l2(to_np(tok), ref.tokens) <= tol
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= tol
+
+
+@pytest.mark.parametrize("window", [False, True])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_tower_head_dim80(pkg, dtype, window):
+    """head_dim 80 (hidden 640, 8 heads): the qkv Dense writes h (the fused rotary epilogue covers
+    head_dim 64 and 72), the rotary relayout forms the 88-element Q/K rows and V^T of 80 rows, and the
+    88-row attention kernel runs on the split lists (full attention) or the window lists. Tokens and
+    the deepstack feature against the fp64 oracle (fp32: 1e-4) and the bf16 oracle (bf16: 1e-2)."""
+    import dataclasses
+    fullatt = (1,) if window else None
+    spec = dataclasses.replace(pkg.spec_2b(), hidden_size=640, num_heads=8, intermediate_size=1280, depth=2,
+                               deepstack_visual_indexes=(0,), out_hidden_size=512, fullatt_block_indexes=fullatt,
+                               window_size=64)
+    assert spec.head_dim == 80 and spec.use_window == window
+    ospec = vt.VisionSpec(hidden_size=640, out_hidden_size=512, depth=2, num_heads=8, intermediate_size=1280,
+                          deepstack_visual_indexes=(0,), window_size=64,
+                          fullatt_block_indexes=fullatt if window else tuple(range(2)))
+    params = pkg.random_params(spec, seed=13)
+    grids = [(1, 8, 12), (2, 4, 4), (1, 16, 20)]
+    px = pixels(grids, 14)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype=dtype).bind(params)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    ref = vt.encode_vision(params, px, grids, ospec, "fp64" if dtype == "float32" else "bf16")
+    tol = 1e-4 if dtype == "float32" else TOL
+    assert rel_l2(to_np(tok), ref.tokens) <= tol
+    assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= tol
