@@ -106,7 +106,8 @@ int main() {
   const int32_t bad_cu[3] = {0, 8, 4};
   CHECK(qvl_attention_worklist(bad_cu, 2, 4, nullptr, 0, &n) != QVL_OK, "non-monotone cu");
   int64_t nw = 0;
-  CHECK(qvl_attention_worklist_split(grid, 1, 4, 80, 8, nullptr, 0, &n, &nw) != QVL_OK, "head_dim 80");
+  CHECK(qvl_attention_worklist_split(grid, 1, 4, 96, 8, nullptr, 0, &n, &nw) != QVL_OK, "head_dim 96");
+  CHECK(qvl_attention_worklist_split(grid, 1, 4, 80, 8, nullptr, 0, &n, &nw) == QVL_OK, "head_dim 80");
   CHECK(qvl_window_metadata(grid, 1, 2, 16, 8, nullptr, nullptr, 0, &n, nullptr) != QVL_OK, "window < patch*merge");
   float inv[32];
   CHECK(qvl_rotary_inv_freq(128, 10000.f, inv) == QVL_OK, "inv_freq 128");
