@@ -439,7 +439,7 @@ int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* q, co
 struct TowerLayout {
   int dtype;
   size_t esz;
-  int64_t N, Np, D, I_pad, PV, hd, H;
+  int64_t N, Np, D, I_pad, PV, PVp, hd, H;   // PVp: the pixel rows' width in the patch-embed GEMM
   int hdp, vrows;
   size_t off_x, off_xn, off_q, off_k, off_vt, off_h, off_cs, off_part, part_bytes, off_apart, off_stats, apart_bytes, total;
   int stat_groups;   // 128-column groups of a row's LayerNorm partials (hidden / 128; 0: hidden % 128 != 0)
@@ -464,8 +464,10 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   const int64_t hd = c->hidden_size / c->num_heads;
   int hdp, vrows;
   QVL_TRY_RC(attn_dims(c->dtype, (int)hd, &hdp, &vrows));
-  if (c->hidden_size % 64 || c->patch_volume % 64 || c->out_hidden_size % 64)
-    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden, patch_volume and out_hidden_size must be multiples of 64");
+  if (c->hidden_size % 64 || c->out_hidden_size % 64)
+    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden and out_hidden_size must be multiples of 64");
+  if (c->patch_volume <= 0 || c->patch_volume % 4)
+    return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: patch_volume=%d (a multiple of 4)", c->patch_volume);
   if (c->dtype == QVL_DTYPE_BF16 && hd == 64 && c->hidden_size % 128)
     return set_error(QVL_ERR_UNSUPPORTED, "encode_vision: hidden %% 128 != 0 with head_dim 64");
   if (c->n_deepstack < 0 || c->n_deepstack > 8) return set_error(QVL_ERR_INVALID_ARG, "n_deepstack=%d", c->n_deepstack);
@@ -474,10 +476,13 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   L->esz = dtype_size(c->dtype);
   L->N = N; L->Np = attn_np(N); L->D = c->hidden_size; L->I_pad = round_up(c->intermediate_size, 64);
   L->PV = c->patch_volume; L->hd = hd; L->H = c->num_heads; L->hdp = hdp; L->vrows = vrows;
+  // the patch-embed GEMM runs K = the packed patch weight's zero-padded width (a multiple of 64):
+  // pixel rows of another width are staged zero-padded to it
+  L->PVp = round_up(L->PV, 64);
   const bool fused_qkv = fused_qkv_rotary(c->dtype, (int)hd, c->num_heads);
   // h hosts the bf16 pixels, the MLP hidden, the merger hidden and (unless the qkv GEMM writes
   // head-major operands itself) the qkv output.
-  int64_t hcols = std::max<int64_t>({L->I_pad, L->PV, (int64_t)c->hidden_size});
+  int64_t hcols = std::max<int64_t>({L->I_pad, L->PVp, (int64_t)c->hidden_size});
   if (!fused_qkv) hcols = std::max<int64_t>(hcols, 3 * (int64_t)c->hidden_size);
   const size_t e = L->esz;
   size_t o = 0;
@@ -584,12 +589,16 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   }
 
   // patch embed + learned pos-embed (model.py:802-806), rotary table (807, 821-823); in fp32 the
-  // pixels feed the GEMM directly. Window mode: the pixel rows are taken in window order (the
+  // pixels feed the GEMM directly when their rows are a multiple of 64 wide (else they are copied
+  // zero-padded, as the bf16 cast is). Window mode: the pixel rows are taken in window order (the
   // reference shuffles x after the row-wise patch embed and pos-embed add, model.py:809-812; the
   // metadata's taps and rotary ids arrive in window order).
   const void* px_in = px;
   if (win) {
-    QVL_TRY_RC(qvl_gather_rows(st, QVL_DTYPE_F32, px, L.PV, dt, h, L.PV, meta->window_index, N, 4, L.PV));
+    QVL_TRY_RC(gather_rows_pad(st, QVL_DTYPE_F32, px, L.PV, dt, h, L.PVp, meta->window_index, N, 4, L.PV, L.PVp));
+    px_in = h;
+  } else if (L.PVp != L.PV) {
+    QVL_TRY_RC(gather_rows_pad(st, QVL_DTYPE_F32, px, L.PV, dt, h, L.PVp, nullptr, N, 1, L.PV, L.PVp));
     px_in = h;
   } else if (!f32) {
     QVL_TRY_RC(qvl_cast(st, QVL_DTYPE_BF16, px, h, N * L.PV));
@@ -622,15 +631,15 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   if (c->num_position_embeddings > 0) {
     QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
     if (G) {
-      QVL_TRY_RC(qvl_dense_rowstats_ws(st, dt, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PV, stats,
+      QVL_TRY_RC(qvl_dense_rowstats_ws(st, dt, px_in, L.PVp, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PVp, stats,
                                        part, PB));
       have_parts = true;
     } else {
-      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PV, W->patch_w, W->patch_b, xn, D, x, D, N, D,
-                              L.PV, part, PB));
+      QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS_RESIDUAL, px_in, L.PVp, W->patch_w, W->patch_b, xn, D, x, D, N, D,
+                              L.PVp, part, PB));
     }
   } else {   // no learned pos-embed table (model.py:676-680, 803-806): the patch embed alone
-    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, px_in, L.PV, W->patch_w, W->patch_b, nullptr, 0, x, D, N, D, L.PV,
+    QVL_TRY_RC(qvl_dense_ws(st, dt, QVL_EPI_BIAS, px_in, L.PVp, W->patch_w, W->patch_b, nullptr, 0, x, D, N, D, L.PVp,
                             part, PB));
   }
 

@@ -272,14 +272,17 @@ __global__ __launch_bounds__(256) void scatter_rows_vec_kernel(HT* __restrict__ 
 
 // ---------------------------------------------------------------------------------------------
 // Row gather (model.py:809-812 shuffle / 845-848 unshuffle of the window path): out row r is
-// in row idx[r / group] * group + r % group, cast to the output dtype. VEC elements per step.
+// in row idx[r / group] * group + r % group (row r itself without idx), cast to the output dtype;
+// out columns [width, pad_to) are written zero (the tower's bf16 pixel rows padded to a multiple
+// of 64 for the patch-embed GEMM). VEC elements per step.
 // ---------------------------------------------------------------------------------------------
 template <int VEC, typename IT, typename OT>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const IT* __restrict__ src, int64_t ld_src,
                                                           OT* __restrict__ dst, int64_t ld_dst,
-                                                          const int32_t* __restrict__ idx, int group, int64_t width) {
+                                                          const int32_t* __restrict__ idx, int group, int64_t width,
+                                                          int64_t pad_to) {
   const int64_t r = blockIdx.x;
-  const int64_t sr = (int64_t)idx[r / group] * group + r % group;
+  const int64_t sr = idx ? (int64_t)idx[r / group] * group + r % group : r;
   const IT* s = src + sr * ld_src;
   OT* d = dst + r * ld_dst;
   for (int64_t c = (int64_t)threadIdx.x * VEC; c < width; c += 256 * VEC) {
@@ -296,6 +299,38 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const IT* __restrict__
       d[c] = (OT)(float)s[c];
     }
   }
+  for (int64_t c = width + threadIdx.x; c < pad_to; c += 256) d[c] = (OT)0.f;
+}
+
+int gather_rows_pad(void* stream, int32_t src_dtype, const void* src, int64_t ld_src, int32_t dst_dtype,
+                         void* dst, int64_t ld_dst, const int32_t* idx, int64_t n_rows, int32_t group, int64_t width,
+                         int64_t pad_to) {
+  const bool sok = src_dtype == QVL_DTYPE_F32 || src_dtype == QVL_DTYPE_BF16;
+  const bool dok = dst_dtype == QVL_DTYPE_F32 || dst_dtype == QVL_DTYPE_BF16;
+  if (!sok || !dok) return set_error(QVL_ERR_UNSUPPORTED, "gather_rows: dtypes %d/%d", src_dtype, dst_dtype);
+  if (n_rows < 0 || width < 0 || group <= 0 || n_rows % group || ld_src < width || pad_to < width || ld_dst < pad_to)
+    return set_error(QVL_ERR_INVALID_ARG, "gather_rows: bad sizes");
+  if (n_rows == 0 || pad_to == 0) return QVL_OK;
+  if (n_rows > 0x7fffffffLL) return set_error(QVL_ERR_UNSUPPORTED, "gather_rows: n_rows");
+  if (!src || !dst) return set_error(QVL_ERR_INVALID_ARG, "gather_rows: NULL pointer");
+  const size_t sa = src_dtype == QVL_DTYPE_F32 ? 16 : 8, da = dst_dtype == QVL_DTYPE_F32 ? 16 : 8;
+  const bool vec = width % 4 == 0 && ld_src % 4 == 0 && ld_dst % 4 == 0 && (uintptr_t)src % sa == 0 &&
+                   (uintptr_t)dst % da == 0;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)n_rows);
+#define QVL_GATHER(V, IT, OT)                                                                                 \
+  hipLaunchKernelGGL((gather_rows_kernel<V, IT, OT>), grid, dim3(256), 0, st, (const IT*)src, ld_src, (OT*)dst, \
+                     ld_dst, idx, group, width, pad_to)
+  const bool sb = src_dtype == QVL_DTYPE_BF16, db = dst_dtype == QVL_DTYPE_BF16;
+  if (vec) {
+    if (sb && db) QVL_GATHER(4, bf16, bf16); else if (sb) QVL_GATHER(4, bf16, float);
+    else if (db) QVL_GATHER(4, float, bf16); else QVL_GATHER(4, float, float);
+  } else {
+    if (sb && db) QVL_GATHER(1, bf16, bf16); else if (sb) QVL_GATHER(1, bf16, float);
+    else if (db) QVL_GATHER(1, float, bf16); else QVL_GATHER(1, float, float);
+  }
+#undef QVL_GATHER
+  return check_launch("gather_rows");
 }
 
 }  // namespace qvl
@@ -354,33 +389,10 @@ int qvl_patchify(void* stream, int32_t dtype, const uint8_t* frames, int64_t n_f
 
 int qvl_gather_rows(void* stream, int32_t src_dtype, const void* src, int64_t ld_src, int32_t dst_dtype, void* dst,
                     int64_t ld_dst, const int32_t* idx, int64_t n_rows, int32_t group, int64_t width) {
-  const bool sok = src_dtype == QVL_DTYPE_F32 || src_dtype == QVL_DTYPE_BF16;
-  const bool dok = dst_dtype == QVL_DTYPE_F32 || dst_dtype == QVL_DTYPE_BF16;
-  if (!sok || !dok) return set_error(QVL_ERR_UNSUPPORTED, "gather_rows: dtypes %d/%d", src_dtype, dst_dtype);
-  if (n_rows < 0 || width < 0 || group <= 0 || n_rows % group || ld_src < width || ld_dst < width)
-    return set_error(QVL_ERR_INVALID_ARG, "gather_rows: bad sizes");
-  if (n_rows == 0 || width == 0) return QVL_OK;
-  if (n_rows > 0x7fffffffLL) return set_error(QVL_ERR_UNSUPPORTED, "gather_rows: n_rows");
-  if (!src || !dst || !idx) return set_error(QVL_ERR_INVALID_ARG, "gather_rows: NULL pointer");
-  const size_t sa = src_dtype == QVL_DTYPE_F32 ? 16 : 8, da = dst_dtype == QVL_DTYPE_F32 ? 16 : 8;
-  const bool vec = width % 4 == 0 && ld_src % 4 == 0 && ld_dst % 4 == 0 && (uintptr_t)src % sa == 0 &&
-                   (uintptr_t)dst % da == 0;
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)n_rows);
-#define QVL_GATHER(V, IT, OT)                                                                                 \
-  hipLaunchKernelGGL((gather_rows_kernel<V, IT, OT>), grid, dim3(256), 0, st, (const IT*)src, ld_src, (OT*)dst, \
-                     ld_dst, idx, group, width)
-  const bool sb = src_dtype == QVL_DTYPE_BF16, db = dst_dtype == QVL_DTYPE_BF16;
-  if (vec) {
-    if (sb && db) QVL_GATHER(4, bf16, bf16); else if (sb) QVL_GATHER(4, bf16, float);
-    else if (db) QVL_GATHER(4, float, bf16); else QVL_GATHER(4, float, float);
-  } else {
-    if (sb && db) QVL_GATHER(1, bf16, bf16); else if (sb) QVL_GATHER(1, bf16, float);
-    else if (db) QVL_GATHER(1, float, bf16); else QVL_GATHER(1, float, float);
-  }
-#undef QVL_GATHER
-  return check_launch("gather_rows");
+  if (!idx && n_rows > 0 && width > 0) return set_error(QVL_ERR_INVALID_ARG, "gather_rows: NULL pointer");
+  return gather_rows_pad(stream, src_dtype, src, ld_src, dst_dtype, dst, ld_dst, idx, n_rows, group, width, width);
 }
+
 
 int qvl_vision_positions(void* stream, const int32_t* tokens, int64_t batch, int64_t seq_len, int32_t match,
                          int64_t n_rows, int32_t* pos, int32_t* count) {

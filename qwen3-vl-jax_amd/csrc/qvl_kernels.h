@@ -118,5 +118,8 @@ int attention_relayout_f32(const float* q, const float* k, const float* v, int64
 int attention_f32(const float* Qb, const float* Kb, const float* Vtb, const int* d_items, int64_t n_items, int Np,
                   int hd, float* out, int64_t ldo, hipStream_t stream);
 int pack_weight_bf16(const float* w, int64_t k_in, int64_t n_out, bf16* out, hipStream_t stream);
+// qvl_gather_rows with the identity order when idx is NULL and out columns [width, pad_to) zeroed.
+int gather_rows_pad(void* stream, int32_t src_dtype, const void* src, int64_t ld_src, int32_t dst_dtype, void* dst,
+                    int64_t ld_dst, const int32_t* idx, int64_t n_rows, int32_t group, int64_t width, int64_t pad_to);
 
 }  // namespace qvl

@@ -360,3 +360,30 @@ def test_tower_head_dim80(pkg, dtype, window):
     tol = 1e-4 if dtype == "float32" else TOL
     assert rel_l2(to_np(tok), ref.tokens) <= tol
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= tol
+
+
+@pytest.mark.parametrize("window", [False, True])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_tower_patch14(pkg, dtype, window):
+    """Patch size 14 (patch_volume 3 x 2 x 14 x 14 = 1176, not a multiple of 64): bf16 pixel rows are
+    staged zero-padded to the packed patch weight's 1216 columns (in window order for a window
+    spec), fp32 rows feed the GEMM as they are. Tokens and the deepstack feature against the fp64
+    oracle (fp32: 1e-4) and the bf16 oracle (bf16: 1e-2)."""
+    import dataclasses
+    fullatt = (1,) if window else None
+    spec = dataclasses.replace(pkg.spec_2b(), patch_size=14, depth=2, deepstack_visual_indexes=(0,),
+                               fullatt_block_indexes=fullatt, window_size=112)
+    assert spec.patch_volume == 1176 and spec.use_window == window
+    ospec = vt.VisionSpec(hidden_size=spec.hidden_size, out_hidden_size=spec.out_hidden_size, depth=2,
+                          num_heads=spec.num_heads, intermediate_size=spec.intermediate_size, patch_size=14,
+                          deepstack_visual_indexes=(0,), window_size=112,
+                          fullatt_block_indexes=fullatt if window else tuple(range(2)))
+    params = pkg.random_params(spec, seed=15)
+    grids = [(1, 8, 12), (2, 4, 4), (1, 16, 20)]
+    px = pixels(grids, 16, patch_volume=1176)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype=dtype).bind(params)
+    tok, ds = tower(px, np.array(grids, np.int32))
+    ref = vt.encode_vision(params, px, grids, ospec, "fp64" if dtype == "float32" else "bf16")
+    tol = 1e-4 if dtype == "float32" else TOL
+    assert rel_l2(to_np(tok), ref.tokens) <= tol
+    assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= tol
