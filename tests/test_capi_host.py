@@ -148,7 +148,21 @@ def test_workspace_sizes(pkg):
     cfg.dtype = pkg.capi.QVL_DTYPE_BF16
     cfg.spatial_merge_size = 3
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == -2
+    cfg.spatial_merge_size = 2
+    # head_dim 64, 72 and 80 (1280 / 16) are taken, 96 is not; patch volumes that are multiples of 4
+    # (patch 14: 1176) are taken (their rows are staged zero-padded to 1216), others are not
+    for dt in (pkg.capi.QVL_DTYPE_BF16, pkg.capi.QVL_DTYPE_F32):
+        cfg.dtype = dt
+        for hidden, heads, rc in ((1280, 16, 0), (1152, 16, 0), (1536, 16, -2)):
+            cfg.hidden_size, cfg.num_heads = hidden, heads
+            assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == rc, (dt, hidden)
+        cfg.hidden_size, cfg.num_heads = 1024, 16
+        for pv, rc in ((1176, 0), (1350, -2), (768, 0)):
+            cfg.patch_volume = pv
+            assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == rc, (dt, pv)
+        cfg.patch_volume = 1536
     for dt, hd, want in ((pkg.capi.QVL_DTYPE_BF16, 72, 16 * 64 * (88 + 88 + 72) * 2),
+                         (pkg.capi.QVL_DTYPE_BF16, 80, 16 * 64 * (88 + 88 + 80) * 2),
                          (pkg.capi.QVL_DTYPE_F32, 72, 16 * 64 * (72 + 72 + 96) * 4),
                          (pkg.capi.QVL_DTYPE_F32, 64, 16 * 64 * (64 + 64 + 64) * 4)):
         assert lib.qvl_vision_attention_workspace_size(dt, 10, 16, hd, C.byref(nb)) == 0
