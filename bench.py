@@ -137,12 +137,81 @@ WORKLOADS = {
 }
 
 
+CONFIG1_GRIDS = [(1, 32, 32), (1, 24, 40), (1, 16, 16), (1, 48, 48)]
+
+
+def attention_config1(args):
+    """the standalone varlen vision attention (model.py:569-600 between the qkv and
+    proj Dense: 2D rotary, softmax(q k^T / sqrt(d)) v per cu_seqlens segment), bf16, four images packed
+    by cu_seqlens (grids (1,32,32), (1,24,40), (1,16,16), (1,48,48): 4544 tokens), 16 heads x head_dim
+    64, q/k/v N(0,1) from a seed: qvl_vision_attention (rotary relayout + attention over the work list,
+    operands resident in HBM) timed with HIP events over 10 x --steps launches after 10 x --warmup (a
+    launch is ~60 us: the clock settles over the first milliseconds)."""
+    import ctypes as C
+    import torch
+    from __graft_entry__ import load_package
+    pkg = load_package()
+    cp = pkg.capi
+    lib = cp.load()
+    H, hd = 16, 64
+    D = H * hd
+    m = pkg.grid_metadata(CONFIG1_GRIDS, num_heads=H)
+    N = m.n_tokens
+    dev = "cuda:0"
+    st = torch.cuda.current_stream()
+    s_ = st.cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(0)
+    qkv = torch.randn((N, 3 * D), generator=g).to(torch.bfloat16).to(dev)
+    pos = torch.from_numpy(m.pos_hw).to(dev)
+    cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, device=dev)
+    cp.check(lib.qvl_rotary_table(s_, cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
+    tiles = torch.from_numpy(m.tiles).to(dev)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_vision_attention_workspace_size(cp.QVL_DTYPE_BF16, N, H, hd, C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+    out = torch.empty((N, D), dtype=torch.bfloat16, device=dev)
+
+    def run():
+        cp.check(lib.qvl_vision_attention(s_, cp.QVL_DTYPE_BF16, qkv.data_ptr(), qkv.data_ptr() + 2 * D,
+                                          qkv.data_ptr() + 4 * D, 3 * D, cs.data_ptr(), tiles.data_ptr(),
+                                          len(m.tiles), out.data_ptr(), D, N, H, hd, ws.data_ptr(), nb.value))
+    steps, warmup = 10 * args.steps, 10 * args.warmup
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        run()
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / max(steps, 1)
+    seg = [h * w for _, h, w in CONFIG1_GRIDS]
+    flops = sum(4.0 * L * L * D for L in seg)
+    tflops = flops / (ms / 1e3) / 1e12
+    out_line = {"metric": "varlen vision attention (2D rotary + softmax(q k^T) v per segment), bf16, 1 GPU",
+                "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+                "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+                "vs_baseline": None, "dtype": "bf16", "data": "synthetic (q/k/v N(0,1), seed 0)",
+                "config": {"workload": "BASELINE config 1: standalone varlen vision attention, 4 images packed by "
+                                       "cu_seqlens (grids (1,32,32), (1,24,40), (1,16,16), (1,48,48)) = 4544 tokens, "
+                                       "16 heads x head_dim 64, qvl_vision_attention (rotary relayout + attention)",
+                           "tokens": N, "parallelism": "single GPU"},
+                "tokens_per_s": round(N / (ms / 1e3), 1),
+                "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2516.6, "unit": "TFLOP/s",
+                             "frac": round(tflops / 2516.6, 4), "traffic": None,
+                             "note": "FLOPs 4 * sum(L^2) * D over the 4 segments; the time includes the "
+                                     "rotary relayout launch"},
+                "secondary": "BASELINE config 1: a parity config, not the headline bench line"}
+    print(json.dumps(out_line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS),
+    ap.add_argument("--config", type=int, default=2, choices=[1] + sorted(WORKLOADS),
                     help="BASELINE config to run (2 = the headline metric's workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cpu-compiled", action="store_true", help="skip the torch.compile CPU variant (~35 s)")
@@ -157,6 +226,8 @@ def main():
               "the tower shards by segment with no communication until a final all-gather, "
               "which is not part of this single-GPU build.", file=sys.stderr)
         sys.exit(2)
+    if args.config == 1:
+        return attention_config1(args)
 
     import torch
     from __graft_entry__ import load_package
