@@ -764,9 +764,70 @@ int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d
   return launch_combine<kHD>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
 }
 
+// attn_relayout_hd64_kernel with 16-byte accesses: thread = (token t, dims [j0, j0+8) and
+// [j0+32, j0+40)), 4 threads per token; the same per-element arithmetic (bit-identical output).
+// V is transposed through LDS (written at the token's vt_pos column) and leaves as 16-byte rows.
+// Requires q, k, v, cs 16-byte aligned and ld % 8 == 0.
+__global__ __launch_bounds__(256) void attn_relayout_hd64_vec_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t ld,
+    const f32x2* __restrict__ cs, int N, int Np, float qscale,
+    bf16* __restrict__ Qo, bf16* __restrict__ Ko, bf16* __restrict__ Vto) {
+  __shared__ __attribute__((aligned(16))) bf16 tv[kHD][64 + 8];   // [dim][key position]
+  const int n0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
+  const int t = tid >> 2, j0 = (tid & 3) * 8, n = n0 + t;
+  const int64_t base = (int64_t)n * ld + head * kHD;
+  bf16x8 qlo = {}, qhi = {}, klo = {}, khi = {}, vlo = {}, vhi = {};
+  if (n < N) {
+    const bf16x8 alo = *reinterpret_cast<const bf16x8*>(q + base + j0);
+    const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(q + base + j0 + 32);
+    const bf16x8 blo = *reinterpret_cast<const bf16x8*>(k + base + j0);
+    const bf16x8 bhi = *reinterpret_cast<const bf16x8*>(k + base + j0 + 32);
+    vlo = *reinterpret_cast<const bf16x8*>(v + base + j0);
+    vhi = *reinterpret_cast<const bf16x8*>(v + base + j0 + 32);
+    f32x2 c[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(cs + (int64_t)n * 32 + j0 + 2 * i);
+      c[2 * i] = f32x2{w[0], w[1]};
+      c[2 * i + 1] = f32x2{w[2], w[3]};
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a1 = (float)alo[e], a2 = (float)ahi[e], b1 = (float)blo[e], b2 = (float)bhi[e];
+      qlo[e] = (bf16)(round_bf16(rope_bf16(a1, a2, c[e], true)) * qscale);
+      qhi[e] = (bf16)(round_bf16(rope_bf16(a2, a1, c[e], false)) * qscale);
+      klo[e] = (bf16)rope_bf16(b1, b2, c[e], true);
+      khi[e] = (bf16)rope_bf16(b2, b1, c[e], false);
+    }
+  }
+  bf16* qd = Qo + ((int64_t)head * Np + n) * kHD;
+  bf16* kd = Ko + ((int64_t)head * Np + n) * kHD;
+  *reinterpret_cast<bf16x8*>(qd + j0) = qlo;
+  *reinterpret_cast<bf16x8*>(qd + j0 + 32) = qhi;
+  *reinterpret_cast<bf16x8*>(kd + j0) = klo;
+  *reinterpret_cast<bf16x8*>(kd + j0 + 32) = khi;
+  const int p = vt_pos(t);   // n0 is a multiple of 64: vt_pos(n0 + t) = n0 + vt_pos(t)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    tv[j0 + e][p] = vlo[e];
+    tv[j0 + 32 + e][p] = vhi[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = tid; i < kHD * 8; i += 256) {
+    const int d = i >> 3, c8 = (i & 7) * 8;
+    *reinterpret_cast<bf16x8*>(Vto + ((int64_t)head * kHD + d) * Np + n0 + c8) =
+        *reinterpret_cast<const bf16x8*>(&tv[d][c8]);
+  }
+}
+
 int attention_relayout_hd64(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N,
                             int Np, int H, float qscale, bf16* Qo, bf16* Ko, bf16* Vto, hipStream_t stream) {
-  hipLaunchKernelGGL(attn_relayout_hd64_kernel, dim3((unsigned)(Np / 64), (unsigned)H), dim3(256), 0, stream,
+  if (Np % 64) return set_error(QVL_ERR_INVALID_ARG, "relayout: Np=%d not a multiple of 64", Np);
+  const auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool vec = a16(q) && a16(k) && a16(v) && a16(cs) && ld % 8 == 0 && a16(Qo) && a16(Ko) && a16(Vto);
+  hipLaunchKernelGGL(vec ? attn_relayout_hd64_vec_kernel : attn_relayout_hd64_kernel,
+                     dim3((unsigned)(Np / 64), (unsigned)H), dim3(256), 0, stream,
                      q, k, v, ld, cs, N, Np, qscale, Qo, Ko, Vto);
   return check_launch("attn_relayout_hd64");
 }

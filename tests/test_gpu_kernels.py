@@ -192,6 +192,41 @@ def test_attention_config1_vs_oracle(pkg, lib):
     assert rel_l2(got, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("grids", [[(1, 32, 32), (1, 24, 40), (1, 16, 16), (1, 48, 48)], [(1, 10, 14), (2, 6, 8)]])
+def test_attention_relayout_paths_bit_exact(pkg, lib, grids):
+    """qvl_vision_attention (head_dim 64) takes the 16-byte relayout kernel for aligned q/k/v and a
+    row stride that is a multiple of 8 elements, and the element-wise one otherwise: the same
+    q/k/v stored with row stride 3D (aligned) and 3D + 4 give bit-identical outputs."""
+    cp = pkg.capi
+    H, hd = 16, 64
+    m = pkg.grid_metadata(grids, num_heads=H)
+    N, D = m.n_tokens, H * hd
+    rng = np.random.default_rng(11)
+    qkv = vt.bf16_round(rng.standard_normal((N, 3 * D)).astype(np.float32))
+    wide = np.zeros((N, 3 * D + 4), np.float32)
+    wide[:, :3 * D] = qkv
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    cs = torch.empty((N, hd // 2, 2), dtype=torch.float32, device=DEV)
+    cp.check(lib.qvl_rotary_table(stream(), cp.QVL_DTYPE_BF16, pos.data_ptr(), N, hd, 10000.0, cs.data_ptr()))
+    tiles = torch.from_numpy(m.tiles).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_vision_attention_workspace_size(cp.QVL_DTYPE_BF16, N, H, hd, C.byref(nb)))
+    outs = []
+    for arr in (qkv, wide):
+        t = bf(arr)
+        ld = arr.shape[1]
+        ws = torch.full((nb.value // 2,), float("nan"), dtype=torch.bfloat16, device=DEV)
+        out = torch.full((N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+        cp.check(lib.qvl_vision_attention(stream(), cp.QVL_DTYPE_BF16, t.data_ptr(), t.data_ptr() + 2 * D,
+                                          t.data_ptr() + 4 * D, ld, cs.data_ptr(), tiles.data_ptr(), len(m.tiles),
+                                          out.data_ptr(), D, N, H, hd, ws.data_ptr(), nb.value))
+        torch.cuda.synchronize()
+        outs.append((to_np(out), ws.view(torch.int16).cpu().numpy()))
+    assert np.isfinite(outs[0][0]).all()
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])      # the staged Q | K | V^T, padding rows included
+
+
 @pytest.mark.parametrize("grids", [[(1, 2, 2)], [(1, 2, 2), (1, 4, 2), (3, 2, 6)], [(1, 10, 14), (2, 6, 8)],
                                    [(1, 64, 2)]])
 def test_attention_ragged_segments(pkg, lib, grids):
