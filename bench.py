@@ -242,7 +242,7 @@ def main():
     seg = [int(h * w) for t, h, w in grid_list for _ in range(t)]
     params = pkg.random_params(spec, seed=0)
     px_host = np.random.default_rng(1).standard_normal((N, spec.patch_volume), dtype=np.float32)
-    tower = pkg.Qwen3VisionTransformer(spec).bind(params)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params)
     px = torch.from_numpy(px_host).to("cuda:0")
     tower.metadata(grids)
     torch.cuda.synchronize()

@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import ctypes as C
 from collections import OrderedDict
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import Dict, Optional, Sequence, Tuple
 
 import numpy as np
@@ -65,12 +65,30 @@ class VisionBackboneSpec:
 
 
 @dataclass
+class TextBackboneSpec:
+    """The reference's text spec (model.py:67-81). The text decoder is outside this build; the spec
+    is parsed (with the reference's key lookups and errors) so that `Qwen3VLSpec` and
+    `spec_from_config` keep the reference's shape."""
+    hidden_size: int
+    num_attention_heads: int
+    num_hidden_layers: int
+    num_key_value_heads: int
+    head_dim: int
+    intermediate_size: int
+    rope_theta: float
+    rope_section: Sequence[int]
+    rope_scaling_type: Optional[str]
+    rope_scaling_factor: Optional[float]
+    mrope_interleaved: bool
+    rms_norm_eps: float
+    vocab_size: int
+
+
+@dataclass
 class Qwen3VLSpec:
-    """The parts of the reference's Qwen3VLSpec (model.py:101-107) this vision path uses: the
-    vision spec and the special token ids. The text backbone is outside this build; its raw HF
-    config dict is kept as `text_config`."""
+    """The reference's model spec (model.py:101-107): text spec, optional vision spec, token ids."""
+    text: Optional[TextBackboneSpec]
     vision: Optional[VisionBackboneSpec]
-    text_config: Dict = field(default_factory=dict)
     pad_token_id: Optional[int] = None
     bos_token_id: Optional[int] = None
     eos_token_id: Optional[int] = None
@@ -104,20 +122,39 @@ def vision_spec_from_config(vision_cfg: Optional[Dict]) -> Optional[VisionBackbo
 
 
 def spec_from_config(cfg: Dict) -> Qwen3VLSpec:
-    """HF `config.json` dict -> Qwen3VLSpec (model.py:987-1049): the vision spec from
-    `vision_config` and the token ids; like the reference, a vision model without
-    `rope_scaling.mrope_section` (or with one of other than 3 entries) is rejected."""
+    """HF `config.json` dict -> Qwen3VLSpec (model.py:987-1049), with the reference's lookups,
+    defaults and errors: head_dim = text head_dim or hidden_size // num_attention_heads; a
+    `vision_config` key (even an empty one) without `rope_scaling.mrope_section` is rejected; a
+    vision model's section must have 3 entries; unless `mrope_interleaved`, the section must sum
+    to head_dim // 2 (model.py:1000-1009); missing text keys raise KeyError as there."""
     text_cfg = cfg.get("text_config", cfg)
     rope_cfg = text_cfg.get("rope_scaling", cfg.get("rope_scaling", {}))
+    head_dim = text_cfg.get("head_dim") or text_cfg["hidden_size"] // text_cfg["num_attention_heads"]
     vision_cfg = cfg.get("vision_config")
-    section = rope_cfg.get("mrope_section") if isinstance(rope_cfg, dict) else None
-    if vision_cfg and section is None:
-        raise ValueError("Missing rope_scaling.mrope_section for vision model")
-    if vision_cfg and section is not None and len(section) != 3:
-        raise ValueError("mrope_section must have 3 entries for vision models")
-    return Qwen3VLSpec(vision=vision_spec_from_config(vision_cfg), text_config=dict(text_cfg),
-                       pad_token_id=cfg.get("pad_token_id"), bos_token_id=cfg.get("bos_token_id"),
-                       eos_token_id=cfg.get("eos_token_id"))
+    is_dict = isinstance(rope_cfg, dict)
+    rope_type = rope_cfg.get("type") if is_dict else None
+    rope_factor = rope_cfg.get("factor", rope_cfg.get("finetuned_factor")) if is_dict else None
+    interleaved = bool(rope_cfg.get("mrope_interleaved", False)) if is_dict else False
+    raw_section = rope_cfg.get("mrope_section") if is_dict else None
+    if raw_section is None:
+        if vision_cfg is not None:
+            raise ValueError("Missing rope_scaling.mrope_section for vision model")
+        section = [head_dim // 2]
+    else:
+        section = [int(x) for x in raw_section]
+        if vision_cfg and len(section) != 3:
+            raise ValueError("mrope_section must have 3 entries for vision models")
+        if not interleaved and sum(section) != head_dim // 2:
+            raise ValueError(f"mrope_section sum must equal head_dim//2 ({head_dim // 2})")
+    text = TextBackboneSpec(
+        hidden_size=text_cfg["hidden_size"], num_attention_heads=text_cfg["num_attention_heads"],
+        num_hidden_layers=text_cfg["num_hidden_layers"], num_key_value_heads=text_cfg["num_key_value_heads"],
+        head_dim=head_dim, intermediate_size=text_cfg["intermediate_size"],
+        rope_theta=text_cfg.get("rope_theta", cfg.get("rope_theta", 10000.0)), rope_section=section,
+        rope_scaling_type=rope_type, rope_scaling_factor=float(rope_factor) if rope_factor else None,
+        mrope_interleaved=interleaved, rms_norm_eps=text_cfg["rms_norm_eps"], vocab_size=text_cfg["vocab_size"])
+    return Qwen3VLSpec(text=text, vision=vision_spec_from_config(vision_cfg), pad_token_id=cfg.get("pad_token_id"),
+                       bos_token_id=cfg.get("bos_token_id"), eos_token_id=cfg.get("eos_token_id"))
 
 
 def spec_2b() -> VisionBackboneSpec:
@@ -316,11 +353,12 @@ def _ptr(t) -> int:
 
 class Qwen3VisionTransformer:
     """The vision tower on libqvl. Bind params once (`bind`), then call like the reference module:
-    `tokens, deepstack = tower(pixel_values, grid_thw)`."""
+    `tokens, deepstack = tower(pixel_values, grid_thw)`. `dtype` defaults to float32, as the
+    reference module's does (model.py:661); "bfloat16" is the reference's bf16 tower."""
 
     META_CACHE_SIZE = 16   # grids whose device metadata stays cached (LRU)
 
-    def __init__(self, spec: VisionBackboneSpec, dtype: str = "bfloat16", device: str = "cuda:0",
+    def __init__(self, spec: VisionBackboneSpec, dtype: str = "float32", device: str = "cuda:0",
                  split_attention: bool = True, ln_fold: bool = True):
         if dtype not in ("bfloat16", "float32"):
             raise NotImplementedError(f"dtype {dtype!r}: the tower runs in bfloat16 or float32")
@@ -917,11 +955,23 @@ class Qwen3VisionTransformer:
 
 
 class Qwen3VLModel:
-    """The `encode_vision` entry of the reference model (model.py:940-944)."""
+    """The `encode_vision` entry of the reference model (model.py:858-871, 940-944).
 
-    def __init__(self, vision_spec: Optional[VisionBackboneSpec], dtype: str = "bfloat16", device: str = "cuda:0"):
-        self.vision_spec = vision_spec
-        self.visual = Qwen3VisionTransformer(vision_spec, dtype, device) if vision_spec is not None else None
+    `spec` is the reference's `Qwen3VLSpec` (as `spec_from_config` returns it); a bare
+    `VisionBackboneSpec` is accepted as the vision spec of a model without a text spec. As in the
+    reference, the tower is built in float32 unless asked otherwise (model.py:871 builds
+    `Qwen3VisionTransformer(spec.vision)`, whose dtype defaults to float32, model.py:661; `dtype`
+    is the text backbone's, which this build does not run). `vision_dtype="bfloat16"` selects the
+    bf16 tower (the reference's `Qwen3VisionTransformer(spec, dtype=jnp.bfloat16)`)."""
+
+    def __init__(self, spec, dtype: str = "bfloat16", device: str = "cuda:0", vision_dtype: str = "float32"):
+        if isinstance(spec, VisionBackboneSpec):
+            spec = Qwen3VLSpec(text=None, vision=spec)
+        self.spec = spec
+        self.dtype = dtype
+        vision = spec.vision if spec is not None else None
+        self.vision_spec = vision
+        self.visual = Qwen3VisionTransformer(vision, vision_dtype, device) if vision else None
         self._bound = None
 
     def encode_vision(self, pixel_values, grid_thw) -> VisionEmbeddings:

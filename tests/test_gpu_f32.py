@@ -179,7 +179,8 @@ def test_config0_fp32_tower_per_layer_and_final(pkg, params2b):
     assert g.tolist() == [[1, 28, 28]] and px.shape == (784, 1536)
     ref = vt.encode_vision(params2b, px, g, ospec, "fp64", keep_layers=True)
     r32 = vt.encode_vision(params2b, px, g, ospec, "fp32")
-    model = pkg.Qwen3VLModel(spec, dtype="float32")
+    model = pkg.Qwen3VLModel(pkg.Qwen3VLSpec(text=None, vision=spec))   # float32 tower, as the reference builds it
+    assert model.visual.dtype == "float32"
     emb = model.apply({"params": params2b}, px, g)
     assert emb.tokens.dtype == torch.float32 and emb.tokens.shape == (196, 2048)
     outs = [(to_np(emb.tokens), ref.tokens, r32.tokens)] + [

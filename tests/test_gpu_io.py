@@ -69,7 +69,7 @@ def test_preprocess_image_into_tower(pkg):
     assert np.array_equal(bits(px.cpu().numpy()), bits(ref))
     spec = pkg.spec_2b()
     spec.depth, spec.deepstack_visual_indexes = 2, (0,)
-    tower = pkg.Qwen3VisionTransformer(spec).bind(pkg.random_params(spec, seed=3))
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(pkg.random_params(spec, seed=3))
     a = tower(px, g)
     b = tower(torch.from_numpy(ref).cuda(), g)
     assert torch.equal(a[0], b[0]) and all(torch.equal(x, y) for x, y in zip(a[1], b[1]))
@@ -137,7 +137,7 @@ def test_inject_vision_embeddings_pack(pkg):
     io = pkg.decoder_io
     spec = pkg.spec_2b()
     spec.depth, spec.deepstack_visual_indexes = 3, (0, 2)
-    tower = pkg.Qwen3VisionTransformer(spec).bind(pkg.random_params(spec, seed=9))
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(pkg.random_params(spec, seed=9))
     grid = np.array([[1, 8, 8]], np.int32)
     px = torch.from_numpy(np.random.default_rng(2).standard_normal((64, 1536), dtype=np.float32)).cuda()
     tokens_v, ds = tower(px, grid)
@@ -196,8 +196,8 @@ def test_hf_checkpoint_into_tower(pkg, tmp_path):
           if "inv_freq" not in k}
     save_file(sd, str(tmp_path / "m.safetensors"))
     loaded = pkg.weights.load_hf_vision_params(str(tmp_path))
-    t1 = pkg.Qwen3VisionTransformer(spec).bind(loaded)
-    t2 = pkg.Qwen3VisionTransformer(spec).bind(params)
+    t1 = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(loaded)
+    t2 = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params)
     grid = np.array([[1, 8, 8]], np.int32)
     px = torch.from_numpy(np.random.default_rng(4).standard_normal((64, 1536), dtype=np.float32)).cuda()
     a, b = t1(px, grid), t2(px, grid)

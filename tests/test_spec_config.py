@@ -78,15 +78,93 @@ def test_fullatt_fallback_to_deepstack_indexes(pkg):
 
 def test_config_errors_and_text_only(pkg):
     with pytest.raises(ValueError, match="mrope_section"):
-        pkg.spec_from_config({"vision_config": VISION_2B, "text_config": {"rope_scaling": {}}})
+        pkg.spec_from_config({"vision_config": VISION_2B, "text_config": dict(hf_config({})["text_config"],
+                                                                               rope_scaling={})})
     with pytest.raises(ValueError, match="3 entries"):
         pkg.spec_from_config(hf_config(VISION_2B, mrope=(64, 64)))
     top = hf_config(VISION_2B)
     del top["vision_config"]
     s = pkg.spec_from_config(top)
-    assert s.vision is None and s.eos_token_id == 151645
+    assert s.vision is None and s.eos_token_id == 151645 and s.text.head_dim == 128
     with pytest.raises(KeyError):
         pkg.vision_spec_from_config({k: v for k, v in VISION_2B.items() if k != "depth"})
+
+
+def test_mrope_section_rules(pkg):
+    """model.py:991-1009. A `vision_config` key that is present but empty still demands a section
+    (the reference tests `is not None` there); the 3-entry rule applies only to a non-empty vision
+    config; unless `mrope_interleaved`, the section must sum to head_dim // 2, with head_dim from
+    the text config (`head_dim`, else hidden_size // num_attention_heads)."""
+    top = hf_config(VISION_2B)
+    top["vision_config"] = {}
+    del top["text_config"]["rope_scaling"]
+    with pytest.raises(ValueError, match="Missing rope_scaling.mrope_section"):
+        pkg.spec_from_config(top)
+    top = hf_config({}, mrope=(32, 32))                  # empty vision config: no 3-entry rule
+    top["text_config"]["rope_scaling"]["mrope_interleaved"] = False
+    s = pkg.spec_from_config(top)
+    assert s.vision is None and list(s.text.rope_section) == [32, 32]
+    # non-interleaved: the sum must be head_dim // 2 = 64
+    top = hf_config(VISION_2B, mrope=(24, 20, 20))
+    top["text_config"]["rope_scaling"]["mrope_interleaved"] = False
+    assert pkg.spec_from_config(top).vision == pkg.spec_2b()
+    top["text_config"]["rope_scaling"]["mrope_section"] = [24, 20, 16]
+    with pytest.raises(ValueError, match=r"mrope_section sum must equal head_dim//2 \(64\)"):
+        pkg.spec_from_config(top)
+    top["text_config"]["rope_scaling"]["mrope_interleaved"] = True     # interleaved: no sum rule
+    assert pkg.spec_from_config(top).text.mrope_interleaved
+    # head_dim from hidden_size // num_attention_heads when the text config has none
+    top = hf_config(VISION_2B, mrope=(16, 24, 24))
+    top["text_config"]["rope_scaling"]["mrope_interleaved"] = False
+    del top["text_config"]["head_dim"]
+    top["text_config"]["hidden_size"] = 2048
+    top["text_config"]["num_attention_heads"] = 16
+    s = pkg.spec_from_config(top)
+    assert s.text.head_dim == 128 and list(s.text.rope_section) == [16, 24, 24]
+    # without a section, a text-only model gets [head_dim // 2]
+    top = hf_config(VISION_2B)
+    del top["vision_config"]
+    del top["text_config"]["rope_scaling"]
+    assert list(pkg.spec_from_config(top).text.rope_section) == [64]
+
+
+def test_text_spec_fields_and_missing_keys(pkg):
+    """The text half of spec_from_config (model.py:1011-1025): the fields it reads, their
+    defaults (rope_theta 10000, scaling type / factor None) and a KeyError for a missing
+    required key, as the reference raises."""
+    top = hf_config(VISION_2B)
+    top["text_config"]["rope_scaling"].update(type="mrope", factor=2)
+    t = pkg.spec_from_config(top).text
+    assert (t.hidden_size, t.num_attention_heads, t.num_hidden_layers, t.num_key_value_heads) == (2048, 16, 28, 8)
+    assert (t.intermediate_size, t.rms_norm_eps, t.vocab_size) == (6144, 1e-6, 151936)
+    assert t.rope_theta == 10000.0 and t.rope_scaling_type == "mrope" and t.rope_scaling_factor == 2.0
+    top["rope_theta"] = 5e6
+    assert pkg.spec_from_config(top).text.rope_theta == 5e6
+    for key in ("num_hidden_layers", "vocab_size", "rms_norm_eps"):
+        bad = hf_config(VISION_2B)
+        del bad["text_config"][key]
+        with pytest.raises(KeyError):
+            pkg.spec_from_config(bad)
+
+
+def test_model_construction_like_the_reference(pkg):
+    """Qwen3VLModel(spec) takes the Qwen3VLSpec that spec_from_config returns and builds the
+    vision tower in float32, as the reference does (model.py:858-871 builds
+    Qwen3VisionTransformer(spec.vision), whose dtype defaults to float32, model.py:661);
+    vision_dtype selects the bf16 tower; a spec without vision gives no tower; a bare
+    VisionBackboneSpec is taken as the vision spec. No GPU work: construction only."""
+    spec = pkg.spec_from_config(hf_config(VISION_2B))
+    m = pkg.Qwen3VLModel(spec)
+    assert m.spec is spec and m.visual is not None and m.visual.dtype == "float32"
+    assert m.visual.spec == pkg.spec_2b()
+    assert pkg.Qwen3VLModel(spec, vision_dtype="bfloat16").visual.dtype == "bfloat16"
+    assert pkg.Qwen3VisionTransformer(pkg.spec_2b()).dtype == "float32"
+    assert pkg.Qwen3VLModel(pkg.spec_8b()).visual.spec == pkg.spec_8b()
+    top = hf_config(VISION_2B)
+    del top["vision_config"]
+    assert pkg.Qwen3VLModel(pkg.spec_from_config(top)).visual is None
+    with pytest.raises(ValueError, match="Vision backbone"):
+        pkg.Qwen3VLModel(pkg.spec_from_config(top)).encode_vision(None, None)
 
 
 @pytest.mark.parametrize("fullatt", [None, (), (1, 3), tuple(range(24))])
