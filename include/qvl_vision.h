@@ -13,7 +13,9 @@
  *     the last failure on the calling thread. The only other state is thread-local
  *     (qvl_set_gemm_plan) or a write-once per-device cache (compute-unit counts, kernel
  *     attributes set once per process): entries are re-entrant and may be called concurrently
- *     from several host threads on different streams.
+ *     from several host threads on different streams. One exception:
+ *     qvl_attention_headmajor_split_noalloc keeps its partial outputs in one file-scope device
+ *     array per GPU (no workspace argument), so calls of it that overlap on one GPU race.
  *   - Activations are row-major [tokens, features]. "Packed" dense weights are [n_out, k_in]
  *     row-major (the transpose of the reference's Flax kernel [in, out], model.py:1152-1153),
  *     with n_out and k_in zero-padded to multiples of 64; biases and LayerNorm affine
@@ -250,6 +252,18 @@ int qvl_dense_rowstats_ws(void* stream, int32_t dtype, const void* d_x, int64_t 
                           const float* d_bias, const void* d_residual, int64_t ldr, void* d_y, int64_t ldc,
                           int64_t m, int64_t n, int64_t k, float* d_parts, void* d_workspace,
                           size_t workspace_bytes);
+
+/* The patch embed with the learned pos-embed added in its epilogue (model.py:549-556, 751-764,
+ * 802-806): y = bf16(bf16(bf16(x . W) + bias) + pos), where row m's pos is gathered from its 4
+ * bilinear taps (d_tap_idx / d_tap_w [4][m], as qvl_vision_metadata writes them) over d_table
+ * [*, n] in the arithmetic of qvl_pos_embed (each tap product and partial sum rounded to bf16), so
+ * y equals qvl_pos_embed followed by the residual Dense bit for bit without the [m, n] pos-embed
+ * buffer. d_parts non-NULL: also the row partials of qvl_dense_rowstats_ws (n % 128 == 0). bf16,
+ * n and ldc multiples of 8; no split-K (the workspace is unused). */
+int qvl_dense_pos_embed_ws(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
+                           const float* d_bias, const void* d_table, const int32_t* d_tap_idx, const float* d_tap_w,
+                           void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k, float* d_parts,
+                           void* d_workspace, size_t workspace_bytes);
 
 /* qvl_dense_ln_ws with the row statistics given as qvl_dense_rowstats_ws partials of x: `groups`
  * 128-column groups per row (k == 128 * groups; a row of the deepstack mergers' [N/4, 4D] view is 4

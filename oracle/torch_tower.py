@@ -119,13 +119,24 @@ class TorchTower:
 
     def __call__(self, pixel_values, grid_thw) -> Tuple[object, List[object]]:
         """(tokens, deepstack) as torch tensors in the tower dtype (model.py:801-851)."""
+        out = self.run(pixel_values, grid_thw)
+        return out["tokens"], out["deepstack"]
+
+    def run(self, pixel_values, grid_thw, keep_layers: bool = False) -> Dict[str, object]:
+        """The forward with its taps: {"tokens", "deepstack"} and, with keep_layers, "embed" (x after
+        the patch embed and pos-embed add) and "layers" (x after each block), torch tensors in the
+        tower dtype."""
         torch = _torch()
         grid = np.asarray(grid_thw, np.int64).reshape(-1, 3)
         px = torch.from_numpy(np.ascontiguousarray(pixel_values, np.float32)).to(self.dt)
+        out: Dict[str, object] = {}
         with torch.inference_mode():
             x = self._dense(px, self.patch)
             if self.pos_table is not None:
                 x = x + self._pos_embed(grid)
+            if keep_layers:
+                out["embed"] = x.clone()
+                out["layers"] = []
             rot = ix.rotary_half_ref(grid, self.spec.hidden_size // self.spec.num_heads, self.spec.spatial_merge_size)
             emb = torch.from_numpy(np.concatenate([rot, rot], axis=-1).astype(np.float32))
             cos, sin = emb.cos().to(self.dt)[:, None, :], emb.sin().to(self.dt)[:, None, :]
@@ -135,6 +146,10 @@ class TorchTower:
             for i, blk in enumerate(self.blocks):
                 x = x + self._attention(self._ln(x, blk["norm1"]), blk, cos, sin, cu)
                 x = x + self._dense(self._gelu(self._dense(self._ln(x, blk["norm2"]), blk["fc1"])), blk["fc2"])
+                if keep_layers:
+                    out["layers"].append(x.clone())
                 if i in ds:
                     feats.append(self._merger(x, self.deepstack[len(feats)], True))
-            return self._merger(x, self.merger, False), feats
+            out["tokens"] = self._merger(x, self.merger, False)
+            out["deepstack"] = feats
+        return out

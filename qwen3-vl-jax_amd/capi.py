@@ -88,6 +88,8 @@ SIGNATURES = {
                                           _i64, _i32, _p, _sz]),
     "qvl_dense_rowstats_ws": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _p,
                                         _sz]),
+    "qvl_dense_pos_embed_ws": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p,
+                                         _p, _sz]),
     "qvl_dense_ln_parts_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _i64, _i64, _i64,
                                         _i64, _p, _sz]),
     "qvl_dense_qkv_rotary_ln_parts": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _p, _p, _i32,

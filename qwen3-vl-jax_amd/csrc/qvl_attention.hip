@@ -240,10 +240,12 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
 
   const float la = __shfl(lacc[0], lane & 15), lb = __shfl(lacc[1], lane & 15);
   float l_tot = (l32 & 16) ? lb : la;   // lanes q and q + 32 both hold query q's sum
-  float omax = 0.f;
+  // Every accumulator finite and at most 2^120: one comparison each, which inf and NaN fail (a
+  // running fmaxf would skip a NaN, e.g. the +inf + -inf of an overflowed PV sum).
+  bool o_ok = true;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) omax = fmaxf(omax, fmaxf(fabsf(oacc[0][r]), fabsf(oacc[1][r])));
-  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !(omax <= 0x1p120f)) != 0) {
+  for (int r = 0; r < 16; ++r) o_ok = o_ok & (fabsf(oacc[0][r]) <= 0x1p120f) & (fabsf(oacc[1][r]) <= 0x1p120f);
+  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !o_ok) != 0) {
     // Some row's sum of 2^s left [2^-64, 2^96] (or O grew past 2^120, or anything overflowed):
     // recompute this wave's rows shifted by the exact row max, reading K and V^T from global
     // memory (the other waves may be done).
@@ -481,12 +483,13 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_qk88_kernel(
   float l_tot = hh == RS_HH ? l_row : l_swap;
   // |O| over the stored rows: block 2 holds output rows 64..HD-1 in registers 0..4 (RS / 8) - 1; its
   // other registers are the row sum (row HD) and rows above it, products of LDS rows the DMA never writes
-  float omax = 0.f;
+  // (every accumulator finite and at most 2^120, tested by comparisons as in attn_fwd_hd64_kernel)
+  bool o_ok = true;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) omax = fmaxf(omax, fmaxf(fabsf(oacc[0][r]), fabsf(oacc[1][r])));
+  for (int r = 0; r < 16; ++r) o_ok = o_ok & (fabsf(oacc[0][r]) <= 0x1p120f) & (fabsf(oacc[1][r]) <= 0x1p120f);
 #pragma unroll
-  for (int r = 0; r < 4 * (RS / 8); ++r) omax = fmaxf(omax, fabsf(oacc[2][r]));
-  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !(omax <= 0x1p120f)) != 0) {
+  for (int r = 0; r < 4 * (RS / 8); ++r) o_ok = o_ok & (fabsf(oacc[2][r]) <= 0x1p120f);
+  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !o_ok) != 0) {
     // As in attn_fwd_hd64_kernel: recompute this wave's rows shifted by the exact row max, from
     // global memory; the row sum by fp32 adds (V^T rows past HD - 1 read as zero: one head's range).
     const __amdgpu_buffer_rsrc_t rkg = make_rsrc(K + head * qk_head, (uint32_t)(qk_head * 2));

@@ -84,6 +84,30 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
   b = bf16_hi(w);
 }
 
+// The learned pos-embed of token m at features n..n+7 (model.py:751-764) for kEpiBiasPosEmbed, in
+// the arithmetic of the pos-embed kernel: each tap product rounded to bf16, the partial sums taken
+// left to right and rounded, taps of weight 0 skipped (their products are zeros).
+__device__ __forceinline__ void pos_embed_oct(const GemmParams& p, int m, int n, float (&acc)[8]) {
+  bool first = true;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float tw = p.pe_w[(int64_t)j * p.M + m];
+    if (tw == 0.f) continue;
+    const int ti = p.pe_idx[(int64_t)j * p.M + m];
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p.pe_table + (int64_t)ti * p.N + n);
+    const float v[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
+                        bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float t = round_bf16(tw * v[e]);
+      acc[e] = first ? t : round_bf16(acc[e] + t);
+    }
+    first = false;
+  }
+}
+
 // Same on 8 consecutive features n..n+7 whose products arrive already rounded to bf16 (packed
 // pairs, from the LDS-staged tile), with the bias of those features preloaded (b0 | b1, zeros
 // past N): 16-byte loads/stores when the rows are 16-byte aligned. The products are exact bf16
@@ -102,6 +126,16 @@ __device__ __forceinline__ u32x4 epi_store_oct(const GemmParams& p, int m, int n
     for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]);
   }
   bf16* dst = p.y + (int64_t)m * p.ldc + n;
+  if constexpr (EPI == kEpiBiasPosEmbed) {
+    // (the host guarantees whole, 16-byte aligned octets for this epilogue)
+    float r[8];
+    pos_embed_oct(p, m, n, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += r[e];
+    const u32x4 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst));
+    return o;
+  }
   if (vec16 && full) {
     if constexpr (EPI == kEpiBiasResidual) {
       const u32x4 r = *reinterpret_cast<const u32x4*>(p.res + (int64_t)m * p.ldr + n);
@@ -367,7 +401,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
     if (m >= p.M) break;               // rows only grow with i
     const u32x4 raw = *reinterpret_cast<const u32x4*>(smem + r * BN + ((c ^ (r % CH)) << 3));
     const u32x4 out = epi_store_oct<EPI>(p, m, n, raw, b0, b1, full, vec16);
-    if constexpr (EPI == kEpiBiasResidual) {
+    if constexpr (EPI == kEpiBiasResidual || EPI == kEpiBiasPosEmbed) {
       // 16 consecutive threads, aligned to 16, hold the 16 octets of one 128-column group of row m
       static_assert(CH % 16 == 0, "row statistics need 128-column groups within a tile row");
       if (p.rs_part) row_group_stats(p, m, n, out);
@@ -985,10 +1019,14 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI, LN>), dim3(grid), dim3(S::THREADS), lds, stream, p);
   int rc = check_launch("gemm_bf16");
   if (rc || g.tail == 0) return rc;
+  if constexpr (EPI == kEpiBiasPosEmbed) {
+    return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: the pos-embed epilogue has no split-K tail");
+  } else {
   const int64_t items = (int64_t)g.tail * BM * ((EPI == kEpiQkvRope) ? BN / 8 : BN / 4);
   hipLaunchKernelGGL((gemm_splitk_reduce_kernel<BM, BN, EPI>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                      stream, p, g.tail);
   return check_launch("gemm_splitk_reduce");
+  }
 }
 
 // Tile choice by the cost model above. Shapes (per-CU MAC rates measured on the tower's GEMMs):
@@ -1005,7 +1043,8 @@ template <int EPI, bool LN>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const int cus = gemm_device_cus();
   ForcedPlan f = t_plan;
-  if (p.rs_part) f.split_mode = -1;   // the split-K reduction writes no row statistics
+  // the split-K reduction writes no row statistics and computes no pos-embed
+  if (p.rs_part || EPI == kEpiBiasPosEmbed) f.split_mode = -1;
   const GemmPlan a = plan_gemm<288, 256>(p, cus, kRate288x256, f.split_mode);
   const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
@@ -1051,7 +1090,7 @@ static int dispatch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
 // rotary epilogues: the Dense layers that follow a LayerNorm); the others carry no trace of it.
 int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream) {
   const bool ln = p.ln_stats != nullptr || p.ln_part != nullptr;
-  if (p.rs_part && (epi != kEpiBiasResidual || p.N % 128))
+  if (p.rs_part && ((epi != kEpiBiasResidual && epi != kEpiBiasPosEmbed) || p.N % 128))
     return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: row statistics need the residual epilogue and N %% 128 == 0");
   if (ln && !p.ln_cd) return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: folded LayerNorm without (c, d)");
   switch (epi) {
@@ -1062,6 +1101,10 @@ int gemm_bf16(const GemmParams& p, int epi, hipStream_t stream) {
     case kEpiBiasResidual:
       if (ln) return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: no folded LayerNorm with the residual epilogue");
       return dispatch_gemm<kEpiBiasResidual, false>(p, stream);
+    case kEpiBiasPosEmbed:
+      if (ln || !p.pe_table || !p.pe_idx || !p.pe_w || p.N % 8 || p.ldc % 8)
+        return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: pos-embed epilogue operands");
+      return dispatch_gemm<kEpiBiasPosEmbed, false>(p, stream);
     case kEpiQkvRope:
       return ln ? dispatch_gemm<kEpiQkvRope, true>(p, stream) : dispatch_gemm<kEpiQkvRope, false>(p, stream);
   }

@@ -355,6 +355,37 @@ int qvl_dense_rowstats_ws(void* stream, int32_t dtype, const void* x, int64_t ld
                     nullptr, nullptr, nullptr, 0, 0.f, parts);
 }
 
+int qvl_dense_pos_embed_ws(void* stream, int32_t dtype, const void* x, int64_t lda, const void* w, const float* bias,
+                           const void* table, const int32_t* tap_idx, const float* tap_w, void* y, int64_t ldc,
+                           int64_t m, int64_t n, int64_t k, float* parts, void* ws, size_t ws_bytes) {
+  (void)ws;
+  (void)ws_bytes;
+  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "dense_pos_embed: dtype %d (bf16 only)", dtype);
+  if (m < 0 || n <= 0 || k <= 0 || k % 64 || n % 8)
+    return set_error(QVL_ERR_INVALID_ARG, "dense_pos_embed: m=%lld n=%lld (multiple of 8) k=%lld (multiple of 64)",
+                     (long long)m, (long long)n, (long long)k);
+  if (m == 0) return QVL_OK;
+  if (!x || !w || !bias || !y || !table || !tap_idx || !tap_w)
+    return set_error(QVL_ERR_INVALID_ARG, "dense_pos_embed: NULL operand");
+  if (lda < k || ldc < n) return set_error(QVL_ERR_INVALID_ARG, "dense_pos_embed: leading dimension too small");
+  if (parts && n % 128)
+    return set_error(QVL_ERR_UNSUPPORTED, "dense_pos_embed: row partials need n %% 128 == 0 (n=%lld)", (long long)n);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || !aligned16(table) || lda % 8 ||
+      ldc % 8 || ((uintptr_t)parts & 7) || ((uintptr_t)tap_idx & 3) || ((uintptr_t)tap_w & 3))
+    return set_error(QVL_ERR_MISALIGNED, "dense_pos_embed: operands 16-byte aligned, lda and ldc multiples of 8");
+  if (m * lda * 2 >= (int64_t)UINT32_MAX || n * k * 2 >= (int64_t)UINT32_MAX)
+    return set_error(QVL_ERR_UNSUPPORTED, "dense_pos_embed: operand larger than 4 GiB");
+  GemmParams p{};
+  p.x = (const bf16*)x; p.lda = lda; p.w = (const bf16*)w; p.bias = bias;
+  p.y = (bf16*)y; p.ldc = ldc;
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  p.rs_part = (f32x2*)parts;
+  p.pe_table = (const bf16*)table;
+  p.pe_idx = tap_idx;
+  p.pe_w = tap_w;
+  return gemm_bf16(p, kEpiBiasPosEmbed, (hipStream_t)stream);
+}
+
 int qvl_dense_ln_parts_ws(void* stream, int32_t dtype, int32_t epi, const void* x, int64_t lda, const void* w,
                           const float* cd, const float* parts, int32_t groups, float eps, const float* bias, void* y,
                           int64_t ldc, int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes) {
@@ -609,11 +640,12 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   // LDS table (measured on MI355X at config 2: 126.6 vs 127.9 us per qkv launch; at head_dim 72
   // the table's 4-byte LDS reads were slower than the per-token loads, 89.3 vs 86.5 us)
   const bool fused_qkv = fused_qkv_rotary(dt, (int)L.hd, (int)L.H);
-  // (the folded-LayerNorm kernels leave the table 2 KB less; sized for the tower's first block)
-  const bool fold0 = !f32 && c->depth > 0 && W->blocks[0].qkv_ln.w && W->blocks[0].qkv_ln.cd &&
-                     W->blocks[0].fc1_ln.w && W->blocks[0].fc1_ln.cd;
+  // (the folded-LayerNorm qkv kernels leave the table 2 KB less: when any block's qkv Dense carries
+  // a fold, the table must fit that smaller limit, since every block reads the one table)
+  bool qkv_fold = false;
+  for (int i = 0; i < c->depth && !f32; ++i) qkv_fold = qkv_fold || (W->blocks[i].qkv_ln.w && W->blocks[i].qkv_ln.cd);
   const bool pos_tab = fused_qkv && L.hd == 64 && meta->n_positions > 0 &&
-                       meta->n_positions * (L.hd / 4) * 4 <= rope_table_lds_bytes((int)L.hd, fold0);
+                       meta->n_positions * (L.hd / 4) * 4 <= rope_table_lds_bytes((int)L.hd, qkv_fold);
   if (pos_tab)
     QVL_TRY_RC(qvl_rotary_pos_table(st, (int)L.hd, c->rope_theta, (int)meta->n_positions, (uint32_t*)cs));
   else
@@ -628,7 +660,13 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
   for (int j = 0; j < c->n_deepstack && !f32; ++j) any_fold = any_fold || W->deepstack[j].fc1_ln.w;
   const int G = any_fold ? L.stat_groups : 0;
   bool have_parts = false;
-  if (c->num_position_embeddings > 0) {
+  if (c->num_position_embeddings > 0 && !f32 && D % 8 == 0) {
+    // bf16: the pos-embed gathered per row inside the patch embed's residual epilogue (no [N, D]
+    // pos-embed buffer written and read back), with x's row partials when a fold reads them
+    QVL_TRY_RC(qvl_dense_pos_embed_ws(st, dt, px_in, L.PVp, W->patch_w, W->patch_b, W->pos_table, meta->tap_idx,
+                                      meta->tap_w, x, D, N, D, L.PVp, G ? stats : nullptr, part, PB));
+    have_parts = G != 0;
+  } else if (c->num_position_embeddings > 0) {
     QVL_TRY_RC(qvl_pos_embed(st, dt, W->pos_table, meta->tap_idx, meta->tap_w, xn, N, D));
     if (G) {
       QVL_TRY_RC(qvl_dense_rowstats_ws(st, dt, px_in, L.PVp, W->patch_w, W->patch_b, xn, D, x, D, N, D, L.PVp, stats,

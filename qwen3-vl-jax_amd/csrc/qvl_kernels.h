@@ -7,7 +7,10 @@
 
 namespace qvl {
 
-enum : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiBiasResidual = 2, kEpiQkvRope = 3, kEpiQkvRope72 = 4 };
+// kEpiBiasPosEmbed: the residual epilogue whose residual is the learned pos-embed, gathered per row from
+// its bilinear taps (the patch embed of the tower, model.py:802-806).
+enum : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiBiasResidual = 2, kEpiQkvRope = 3, kEpiQkvRope72 = 4,
+             kEpiBiasPosEmbed = 5 };
 
 struct GemmParams {
   const bf16* x; int64_t lda;
@@ -49,6 +52,11 @@ struct GemmParams {
   // Residual epilogue: also write those partials of the bf16 output rows (rs_part[m * N / 128 + g]),
   // the statistics of the LayerNorm that reads them next (N % 128 == 0, no split-K tail).
   f32x2* rs_part;
+  // kEpiBiasPosEmbed: row m's residual is sum_j pe_w[j][m] * pe_table[pe_idx[j][m]][:] (j < 4, taps
+  // [4][M], table rows of N bf16), in the pos-embed kernel's bf16 arithmetic (no split-K tail).
+  const bf16* pe_table;
+  const int* pe_idx;
+  const float* pe_w;
 };
 
 // fp32 GEMM (qvl_f32.hip): w packed [n_rows_w][ldw] fp32 (ldw = k padded to 64), Kp = ldw.

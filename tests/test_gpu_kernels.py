@@ -131,6 +131,58 @@ def test_pos_embed_vs_oracle(pkg, lib, grids):
         np.testing.assert_array_equal(to_np(out), vt.bf16_round(table)[row])
 
 
+@pytest.mark.parametrize("grids,k,parts", [([(1, 48, 48), (1, 48, 48)], 1536, True), ([(1, 84, 84), (3, 10, 6)], 1536, True),
+                                           ([(8, 32, 32)], 1216, False), ([(1, 20, 36)], 64, True)])
+def test_dense_pos_embed_equals_pos_embed_then_residual(pkg, lib, grids, k, parts):
+    """qvl_dense_pos_embed_ws (the patch embed with the pos-embed gathered in its epilogue, the
+    tower's bf16 path) against qvl_pos_embed followed by the residual Dense (qvl_dense_rowstats_ws,
+    or qvl_dense_ws with the split-K tail off): the output and the row partials bit for bit, on
+    config 2's two-image grid (48 x 48: single-tap rows), config 4's grid with a ragged image
+    (four live taps per row), config 3's video (the jnp.repeat frame quirk) and a short K."""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    N, D = m.n_tokens, 1024
+    rng = np.random.default_rng(N + k)
+    table = bf(rng.standard_normal((2304, D)).astype(np.float32) * 0.02)
+    x = bf(rng.standard_normal((N, k)).astype(np.float32))
+    w = pack(lib, cp, (rng.standard_normal((k, D)) * 0.03).astype(np.float32))
+    bias = torch.from_numpy(vt.bf16_round((rng.standard_normal(D) * 0.02).astype(np.float32))).to(DEV)
+    idx, tw = torch.from_numpy(m.tap_idx).to(DEV), torch.from_numpy(m.tap_w).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    pos = torch.empty((N, D), dtype=torch.bfloat16, device=DEV)
+    cp.check(lib.qvl_pos_embed(stream(), cp.QVL_DTYPE_BF16, table.data_ptr(), idx.data_ptr(), tw.data_ptr(),
+                               pos.data_ptr(), N, D))
+    y_ref = torch.empty((N, D), dtype=torch.bfloat16, device=DEV)
+    y = torch.full((N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    p_ref = torch.zeros((N, D // 128, 2), dtype=torch.float32, device=DEV)
+    p_got = torch.full((N, D // 128, 2), float("nan"), dtype=torch.float32, device=DEV)
+    try:
+        cp.check(lib.qvl_set_gemm_plan(0, -1, 0))
+        if parts:
+            cp.check(lib.qvl_dense_rowstats_ws(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), k, w.data_ptr(),
+                                               bias.data_ptr(), pos.data_ptr(), D, y_ref.data_ptr(), D, N, D, k,
+                                               p_ref.data_ptr(), ws.data_ptr(), nb.value))
+        else:
+            cp.check(lib.qvl_dense_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_RESIDUAL, x.data_ptr(), k,
+                                      w.data_ptr(), bias.data_ptr(), pos.data_ptr(), D, y_ref.data_ptr(), D, N, D, k,
+                                      ws.data_ptr(), nb.value))
+    finally:
+        cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
+    cp.check(lib.qvl_dense_pos_embed_ws(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), k, w.data_ptr(), bias.data_ptr(),
+                                        table.data_ptr(), idx.data_ptr(), tw.data_ptr(), y.data_ptr(), D, N, D, k,
+                                        p_got.data_ptr() if parts else None, ws.data_ptr(), nb.value))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_np(y), to_np(y_ref))
+    if parts:
+        np.testing.assert_array_equal(p_got.cpu().numpy(), p_ref.cpu().numpy())
+    # and against the oracle's bf16 pos-embed + Dense arithmetic within the GEMM tolerance
+    ref = ref_dense(x, w, bias, torch.from_numpy(vt.pos_embed(to_np(table), grids, vt.VisionSpec(), vt._P("bf16"))).to(DEV),
+                    2, D, k)
+    assert rel_l2(to_np(y), ref.cpu().numpy()) <= 4e-3
+
+
 def test_rotary_table_vs_oracle(pkg, lib):
     """cos/sin table in bf16 mode: the oracle's bf16 cos/sin, up to one bf16 ulp where device and
     numpy float32 cos/sin round a value near a bf16 rounding boundary differently."""
@@ -359,11 +411,13 @@ def test_attention_split_items_match_whole(pkg, lib, hd, cu, H, n_cus):
 @pytest.mark.parametrize("hd", [64, 72, 80])
 @pytest.mark.parametrize("spike", [40.0, 100.0])
 def test_attention_late_score_spike(pkg, lib, hd, spike):
-    """Scores far above the first key tile's maximum: the kernels hold the first tile's max m and
-    carry p = 2^(s - m) > 1 in fp32; a row sum past 2^64 (spike 100, in log2 units) sends the wave
-    to its exact recompute. Keys in a middle tile and in the segment's last (masked) tile spike for
-    some query rows of every head, on the whole and the split work lists: rel-L2 <= 1e-2 against
-    an fp32 reference per segment, every row finite."""
+    """Scores far above the rest of their row, late in the key range. The kernels take p = 2^s
+    unshifted (s in log2 units) and check each wave's rows after the key loop: a row sum outside
+    [2^-64, 2^96] or an accumulator above 2^120 (inf / NaN included) sends the wave to its exact
+    recompute (row max first, then p = 2^(s - max)). A spike of 40 stays inside the fast path's
+    range; a spike of 100 overflows the row sum and takes the recompute. Keys in a middle tile and
+    in the segment's last (masked) tile spike for some query rows of every head, on the whole and
+    the split work lists: rel-L2 <= 1e-2 against an fp32 reference per segment, every row finite."""
     cp = pkg.capi
     H = 4
     cu = np.array([0, 100, 2600, 2700, 7000], np.int32)
@@ -420,6 +474,78 @@ def test_attention_late_score_spike(pkg, lib, hd, spike):
         for rows, key in rows_keys:             # the spiking rows follow their key's value row
             r = np.array(list(rows))
             assert rel_l2(got[r], ref[r]) <= 1e-2, (nw, key)
+
+
+def _run_attention_lists(pkg, lib, q, k, vt, cu, H, hd):
+    """qvl_attention_headmajor on the plain work list and qvl_attention_headmajor_split on the
+    split list of 40 CUs (when it splits): [(label, bf16 output as fp32 numpy)]."""
+    cp = pkg.capi
+    N = int(cu[-1])
+    lists = [(pkg.vision._worklist(lib, cu, H), None)]
+    split, n_whole = pkg.attention_worklist_split(cu, H, hd, 40)
+    if len(split) > n_whole:
+        lists.append((split, n_whole))
+    outs = []
+    for items, nw in lists:
+        t = torch.from_numpy(np.ascontiguousarray(items)).to(DEV)
+        out = torch.full((N, H * hd), float("nan"), dtype=torch.bfloat16, device=DEV)
+        if nw is None:
+            cp.check(lib.qvl_attention_headmajor(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(), vt.data_ptr(),
+                                                 t.data_ptr(), len(items), N, H, hd, out.data_ptr(), H * hd))
+        else:
+            nb = C.c_size_t()
+            cp.check(lib.qvl_attention_split_workspace_size(hd, len(items), nw, C.byref(nb)))
+            ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=DEV)
+            cp.check(lib.qvl_attention_headmajor_split(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(),
+                                                       vt.data_ptr(), t.data_ptr(), len(items), nw, N, H, hd,
+                                                       out.data_ptr(), H * hd, ws.data_ptr(), nb.value))
+        torch.cuda.synchronize()
+        outs.append(("whole" if nw is None else "split", to_np(out)))
+    return outs
+
+
+@pytest.mark.parametrize("hd", [64, 72])
+@pytest.mark.parametrize("case", ["sum_below_2^-64", "sum_zero", "accumulator_above_2^120"])
+def test_attention_exact_recompute_triggers(pkg, lib, hd, case):
+    """The other two triggers of the exact recompute (see test_attention_late_score_spike for the
+    row-sum overflow). "sum_below_2^-64": every score of some rows is about -80 (log2 units), so
+    their unshifted row sums (~L * 2^-80) fall under 2^-64; "sum_zero": about -200, so every
+    2^s underflows fp32 and the unshifted sums are 0 (0/0 without the recompute);
+    "accumulator_above_2^120": scores about +30 (row sums ~L * 2^30, inside the range) against V
+    rows of magnitude ~2^100, so the unnormalised accumulator passes 2^120 (overflows fp32) while
+    the row sums do not. Rows in a short segment, a long one and the last (masked) key tiles, on
+    the whole and the split work lists: rel-L2 <= 1e-2 against an fp32 softmax reference per
+    segment, every row finite."""
+    H = 4
+    cu = np.array([0, 100, 2600, 2700, 7000], np.int32)
+    N = int(cu[-1])
+    q, k, vt, _ = _headmajor_operands(H, hd, cu, seed=31 + hd)
+    q, k, vt = q.cpu(), k.cpu(), vt.cpu()
+    n = np.arange(vt.shape[2])
+    quad = (n >> 2) & 3
+    pos = torch.from_numpy((n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3))
+    v_keys = vt[:, :, pos].float()                         # V^T in key order
+    shift = {"sum_below_2^-64": -80.0, "sum_zero": -200.0, "accumulator_above_2^120": 30.0}[case]
+    rows = list(range(10, 60, 3)) + list(range(2610, 2700, 2)) + list(range(2700, 7000, 13))
+    for r in rows:
+        q[:, r, 0] = 8.0
+    k[:, :N, 0] = shift / 8.0                             # every key: the shifted rows score ~shift
+    if case == "accumulator_above_2^120":
+        v_keys[:, :, :N] *= 2.0 ** 100
+    vt[:, :, pos] = v_keys.to(torch.bfloat16)
+    v_keys = vt[:, :, pos].float()
+    ref = torch.zeros((N, H * hd))
+    for s, e in zip(cu[:-1], cu[1:]):
+        sc = torch.einsum("hqd,hkd->hqk", q[:, s:e, :hd].float(), k[:, s:e, :hd].float())
+        p = torch.softmax(sc * 0.6931471805599453, dim=-1)
+        ref[s:e] = torch.einsum("hqk,hdk->hqd", p, v_keys[:, :, s:e]).permute(1, 0, 2).reshape(e - s, H * hd)
+    ref = ref.numpy()
+    for label, got in _run_attention_lists(pkg, lib, q.to(DEV), k.to(DEV), vt.to(DEV), cu, H, hd):
+        assert np.isfinite(got).all(), label
+        for s, e in zip(cu[:-1], cu[1:]):
+            assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (label, s, e, rel_l2(got[s:e], ref[s:e]))
+        r = np.array(rows)
+        assert rel_l2(got[r], ref[r]) <= 1e-2, label
 
 
 _TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4}

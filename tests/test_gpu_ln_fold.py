@@ -379,6 +379,84 @@ def test_rowstats_feed_folded_dense(pkg, lib, shape):
     assert rel_l2(got, exact) <= 1.25 * rel_l2(ref, exact) + 5e-4
 
 
+@pytest.mark.parametrize("ratio", [100, 1000])
+def test_folded_dense_badly_conditioned_rows(pkg, lib, ratio):
+    """Rows whose mean is `ratio` standard deviations off zero (measured on the bf16 rows: median
+    |mean| / std within a factor 2 of `ratio`). The fold computes rstd * (x . W') - rstd * mean * c,
+    two terms of size ~|mean| / std that cancel, so its fp32 rounding grows with that ratio; the
+    reference subtracts the mean before the Dense. Folded (statistics from qvl_row_stats and from
+    128-column partials) and unfolded (qvl_layer_norm + qvl_dense_ws) bias+GELU Dense against the
+    reference's bf16 LayerNorm + Dense (6e-3) and no further from exact fp64 than it (x1.25 + 5e-4).
+    The measured errors are printed. (A row of identical values has std 0 and rstd = eps^-1/2: the
+    fold then amplifies the rounding of x . W' - mean * c by 1000, which is why ln_fold=False
+    remains available; the tower's rows are never constant.)"""
+    cp = pkg.capi
+    m, k, n = 512, 1024, 4096
+    rng = np.random.default_rng(ratio)
+    sign = np.where(rng.random((m, 1)) < 0.5, -1.0, 1.0)
+    # a bf16 row mean mu (binade [2^e, 2^(e+1)), spacing 2^(e-7)) plus whole bf16 steps, so that the
+    # deviations survive rounding: N(0, s) steps with s = |mu| / spacing / ratio when that is >= 1
+    # (ratio 100); otherwise +-1 steps on c of the k columns, std = spacing * sqrt(c / k)
+    e = rng.integers(-1, 3, (m, 1)).astype(np.float64)
+    mu = sign * 2.0 ** e * rng.uniform(1.0, 1.9, (m, 1))
+    spacing = 2.0 ** (e - 7)
+    s = np.abs(mu) / spacing / ratio
+    steps = np.rint(rng.standard_normal((m, k)) * s)
+    if ratio > 200:
+        c = np.clip(np.rint((np.abs(mu) / spacing / ratio) ** 2 * k), 2, k // 4).astype(int)
+        steps = np.zeros((m, k))
+        for i in range(m):
+            cols = rng.choice(k, size=c[i, 0], replace=False)
+            steps[i, cols] = rng.choice([-1.0, 1.0], size=c[i, 0])
+    x = (vt.bf16_round(mu.astype(np.float32)) + steps * spacing).astype(np.float32)
+    assert np.array_equal(vt.bf16_round(x), x)
+    x64 = x.astype(np.float64)
+    sd = x64.std(-1)
+    assert np.all(sd > 0)
+    cond = np.median(np.abs(x64.mean(-1)) / sd)
+    assert 0.5 * ratio <= cond <= 2 * ratio, cond
+    g, b = ln_params(rng, k)
+    w_h = (rng.standard_normal((k, n)) * 0.03).astype(np.float32)
+    b_h = vt.bf16_round((rng.standard_normal(n) * 0.1).astype(np.float32))
+    w = pack(lib, cp, w_h)
+    wf, cd = fold(lib, cp, w, g, b)
+    xt = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    st = stats(lib, cp, xt, k)
+    parts = torch.from_numpy(host_parts(x)).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    bias = torch.from_numpy(b_h).to(DEV)
+    outs = {name: torch.empty((m, n), dtype=torch.bfloat16, device=DEV) for name in ("stats", "parts", "unfolded")}
+    cp.check(lib.qvl_dense_ln_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, xt.data_ptr(), k, wf.data_ptr(),
+                                 cd.data_ptr(), st.data_ptr(), bias.data_ptr(), outs["stats"].data_ptr(), n, m, n, k,
+                                 ws.data_ptr(), nb.value))
+    cp.check(lib.qvl_dense_ln_parts_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, xt.data_ptr(), k,
+                                       wf.data_ptr(), cd.data_ptr(), parts.data_ptr(), k // 128, EPS, bias.data_ptr(),
+                                       outs["parts"].data_ptr(), n, m, n, k, ws.data_ptr(), nb.value))
+    gt, bt = torch.from_numpy(g).to(DEV), torch.from_numpy(b).to(DEV)
+    xn = torch.empty_like(xt)
+    cp.check(lib.qvl_layer_norm(stream(), cp.QVL_DTYPE_BF16, xt.data_ptr(), k, gt.data_ptr(), bt.data_ptr(),
+                                xn.data_ptr(), k, m, k, EPS))
+    cp.check(lib.qvl_dense_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_GELU, xn.data_ptr(), k, w.data_ptr(),
+                              bias.data_ptr(), None, 0, outs["unfolded"].data_ptr(), n, m, n, k, ws.data_ptr(),
+                              nb.value))
+    torch.cuda.synchronize()
+    xn64 = ln64(x, g, b)
+    exact = gelu64(xn64 @ vt.bf16_round(w_h).astype(np.float64) + b_h)
+    ref = ref_bf16_dense(vt.bf16_round(xn64.astype(np.float32)), w_h, b_h, 1)
+    e_ref = rel_l2(ref, exact)
+    msg = []
+    for name, y in outs.items():
+        got = to_np(y)
+        assert np.isfinite(got).all(), name
+        a, e = rel_l2(got, ref), rel_l2(got, exact)
+        msg.append(f"{name}: vs reference arithmetic {a:.2e}, vs fp64 {e:.2e}")
+        assert a <= 6e-3, name
+        assert e <= 1.25 * e_ref + 5e-4, name
+    print(f"\n[|mean|/std ~ {cond:.0f}] reference arithmetic vs fp64 {e_ref:.2e}; " + "; ".join(msg), flush=True)
+
+
 def test_rowstats_rejects_bad_shapes(pkg, lib):
     """Row statistics need 128-column groups and 8-element row strides; the folded entries need
     groups * 128 == the LayerNorm width and a positive eps (checked on the host, no launch)."""

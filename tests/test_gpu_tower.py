@@ -13,6 +13,8 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+# end-to-end bars of the bf16 tower (measured values and their margins: tests/test_gpu_parity_depth.py)
+from tests.test_gpu_parity_depth import E2E_BF16, E2E_BF16_REL, E2E_DRIFT  # noqa: E402
 
 
 def rel_l2(a, b):
@@ -66,8 +68,9 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
     End to end: the reference's own bf16 mode drifts ~1.4e-2 from its fp32 mode by block 24
     (bf16 rounding noise the 24 residual blocks accumulate), so no bf16 implementation that is
     not bit-identical to it can sit within 1e-2 of it there. The end-to-end bar is therefore: the
-    GPU path is at least as close to the fp32 reference as the reference's bf16 mode is (x1.1),
-    and within 2e-2 of the bf16 reference; both for tokens and every deepstack feature."""
+    GPU path's distance to the fp32 reference within x1.03 of the reference bf16 mode's own, and
+    its distance to the bf16 reference within x1.12 of that and 1.75e-2; both for tokens and every
+    deepstack feature."""
     if shape == "2b":
         spec, ospec = specs(pkg)
         params = params2b
@@ -78,8 +81,8 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
     px = pixels(grids, 1)
     ref = vt.encode_vision(params, px, grids, ospec, "bf16", keep_layers=True)
     f32 = vt.encode_vision(params, px, grids, ospec, "fp32")
-    tower = pkg.Qwen3VisionTransformer(spec, ln_fold=False).bind(params)
-    towerf = pkg.Qwen3VisionTransformer(spec).bind(params)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16", ln_fold=False).bind(params)
+    towerf = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params)
     assert towerf.ln_fold and not tower.ln_fold
     g = np.array(grids, np.int32)
     # per layer, in isolation
@@ -115,8 +118,9 @@ def test_full_depth_small_grids_per_layer_and_accuracy(pkg, params2b, params8b, 
                                                               zip(got_ds, ref.deepstack, f32.deepstack)]
         assert len(pairs) == 4
         for got, rb, rf in pairs:
-            assert rel_l2(got, rf) <= 1.1 * rel_l2(rb, rf)
-            assert rel_l2(got, rb) <= 2e-2
+            e_ref = rel_l2(rb, rf)
+            assert rel_l2(got, rf) <= E2E_DRIFT * e_ref
+            assert rel_l2(got, rb) <= min(E2E_BF16_REL * e_ref, E2E_BF16)
 
 
 @pytest.mark.parametrize("ln_fold", [True, False])
@@ -128,7 +132,7 @@ def test_config2_image_reduced_depth(pkg, params2b, ln_fold):
     grids = [(1, 48, 48)]
     px = pixels(grids, 2)
     ref = vt.encode_vision(params2b, px, grids, ospec, "bf16", keep_layers=True)
-    tower = pkg.Qwen3VisionTransformer(spec, ln_fold=ln_fold).bind(params2b)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16", ln_fold=ln_fold).bind(params2b)
     assert tower.ln_fold == ln_fold
     tok, ds = tower(px, np.array(grids, np.int32))
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
@@ -143,16 +147,16 @@ def test_config2_image_full_depth_fused_path(pkg, params2b):
     deepstack taps after blocks 5/11/17, through the benchmarked path: per block in isolation with
     the fused entries (qvl_dense_qkv_rotary + the tower's attention work list) within rel-L2 1e-2 of
     the bf16 oracle, and the whole-tower entry qvl_encode_vision end to end under the end-to-end
-    rule (at least as close to the fp32 reference as the reference's bf16 mode, x1.1, and within
-    2e-2 of the bf16 reference) for the tokens and every deepstack feature. The measured values
-    are printed."""
+    rule (distance to the fp32 reference within x1.03 of the reference bf16 mode's own; to the bf16
+    reference within x1.12 of that and 1.75e-2) for the tokens and every deepstack feature. The
+    measured values are printed."""
     spec, ospec = specs(pkg)
     grids = [(1, 48, 48)]
     g = np.array(grids, np.int32)
     px = pixels(grids, 3)
     ref = vt.encode_vision(params2b, px, grids, ospec, "bf16", keep_layers=True)
     f32 = vt.encode_vision(params2b, px, grids, ospec, "fp32")
-    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params2b)
     ctx = tower._staged_ctx(g)
     worst = 0.0
     for i in range(spec.depth):
@@ -174,8 +178,8 @@ def test_config2_image_full_depth_fused_path(pkg, params2b):
         got = to_np(got)
         e_b, e_f, e_ref = rel_l2(got, rb), rel_l2(got, rf), rel_l2(rb, rf)
         rows.append(f"{name}: vs bf16 oracle {e_b:.3e}, vs fp32 oracle {e_f:.3e} (oracle bf16 vs fp32 {e_ref:.3e})")
-        assert e_f <= 1.1 * e_ref, name
-        assert e_b <= 2e-2, name
+        assert e_f <= E2E_DRIFT * e_ref, name
+        assert e_b <= min(E2E_BF16_REL * e_ref, E2E_BF16), name
     print(f"\n[config2 image, 24 blocks] worst fused block / deepstack merger in isolation {worst:.3e}; "
           + "; ".join(rows), flush=True)
 
@@ -191,7 +195,7 @@ def test_config3_video_reduced_depth(pkg, params2b):
     px, g = vt.patchify(np.stack(frames), patch=16, tpatch=2, merge=2)
     assert g.tolist() == [[8, 32, 32]]
     ref = vt.encode_vision(params2b, px, g, ospec, "bf16")
-    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params2b)
     tok, ds = tower(px, g)
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
@@ -204,7 +208,7 @@ def test_config4_grid_reduced_depth(pkg, params8b):
     grids = [(1, 84, 84)]
     px = pixels(grids, 6)
     ref = vt.encode_vision(params8b, px, grids, ospec, "bf16")
-    tower = pkg.Qwen3VisionTransformer(spec).bind(params8b)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params8b)
     tok, ds = tower(px, np.array(grids, np.int32))
     assert tuple(tok.shape) == (1764, 4096)
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
@@ -232,7 +236,7 @@ def test_config2_full_batch_invariance(pkg, params2b):
     spec, _ = specs(pkg)
     grids = [(1, 48, 48)] * 8
     px = pixels(grids, 4)
-    tower = pkg.Qwen3VisionTransformer(spec).bind(params2b)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params2b)
     tok, ds = tower(px, np.array(grids, np.int32))
     tok = to_np(tok); ds = [to_np(d) for d in ds]
     assert np.isfinite(tok).all()
@@ -250,19 +254,32 @@ def test_config2_full_batch_invariance(pkg, params2b):
 
 def test_encode_vision_api(pkg, params2b):
     """Qwen3VLModel.apply(..., method="encode_vision") returns VisionEmbeddings with the
-    reference's layout: tokens [N/4, Dout], deepstack tuple of len(deepstack_visual_indexes)."""
-    spec, _ = specs(pkg, depth=2, ds=(0, 1))
-    model = pkg.Qwen3VLModel(spec)
+    reference's layout: tokens [N/4, Dout], deepstack tuple of len(deepstack_visual_indexes).
+    The model is built from the Qwen3VLSpec that spec_from_config returns for an HF config, with a
+    float32 tower by default (model.py:661, 871) and a bf16 tower on request; both agree with the
+    oracle in their precision."""
+    from tests.test_spec_config import VISION_2B, hf_config
+    spec = pkg.spec_from_config(hf_config(dict(VISION_2B, depth=2, deepstack_visual_indexes=[0, 1])))
+    assert isinstance(spec, pkg.Qwen3VLSpec) and spec.vision.depth == 2
     grids = np.array([(1, 4, 4), (2, 2, 6)], np.int32)
     px = pixels(grids.tolist(), 5)
-    out = model.apply({"params": params2b}, px, grids, method="encode_vision")
-    assert isinstance(out, pkg.VisionEmbeddings)
-    assert tuple(out.tokens.shape) == (10, 2048) and len(out.deepstack) == 2
+    ospec = vt.VisionSpec(hidden_size=1024, out_hidden_size=2048, depth=2, num_heads=16, intermediate_size=4096,
+                          deepstack_visual_indexes=(0, 1))
+    for kw, dt, mode, tol in (({}, torch.float32, "fp64", 1e-4), ({"vision_dtype": "bfloat16"}, torch.bfloat16,
+                                                                   "bf16", TOL)):
+        model = pkg.Qwen3VLModel(spec, **kw)
+        out = model.apply({"params": params2b}, px, grids, method="encode_vision")
+        assert isinstance(out, pkg.VisionEmbeddings)
+        assert out.tokens.dtype == dt and all(f.dtype == dt for f in out.deepstack)
+        assert tuple(out.tokens.shape) == (10, 2048) and len(out.deepstack) == 2
+        ref = vt.encode_vision(params2b, px, grids, ospec, mode)
+        assert rel_l2(to_np(out.tokens), ref.tokens) <= tol
+        assert rel_l2(to_np(out.deepstack[1]), ref.deepstack[1]) <= tol
     assert tuple(out.with_batch_dim(3).tokens.shape) == (3, 10, 2048)
     cat = pkg.VisionEmbeddings.concatenate([out, out])
     assert tuple(cat.tokens.shape) == (20, 2048) and tuple(cat.deepstack[1].shape) == (20, 2048)
     with pytest.raises(ValueError, match="Vision backbone"):
-        pkg.Qwen3VLModel(None).encode_vision(px, grids)
+        pkg.Qwen3VLModel(pkg.Qwen3VLSpec(text=spec.text, vision=None)).encode_vision(px, grids)
 
 
 def test_wide_tower_most_partial_groups(pkg):
@@ -281,7 +298,7 @@ def test_wide_tower_most_partial_groups(pkg):
     ref = vt.encode_vision(params, px, grids, ospec, "bf16")
     g = np.array(grids, np.int32)
     for fold in (True, False):
-        tower = pkg.Qwen3VisionTransformer(spec, ln_fold=fold).bind(params)
+        tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16", ln_fold=fold).bind(params)
         tok, ds = tower(px, g)
         assert rel_l2(to_np(tok), ref.tokens) <= TOL, fold
         assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, fold
@@ -305,7 +322,7 @@ def test_tower_rows_not_in_128_column_groups(pkg):
     ref = vt.encode_vision(params, px, grids, ospec, "bf16")
     g = np.array(grids, np.int32)
     for fold in (True, False):
-        tower = pkg.Qwen3VisionTransformer(spec, ln_fold=fold).bind(params)
+        tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16", ln_fold=fold).bind(params)
         tok, ds = tower(px, g)
         assert rel_l2(to_np(tok), ref.tokens) <= TOL, fold
         assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, fold
@@ -387,3 +404,30 @@ def test_tower_patch14(pkg, dtype, window):
     tol = 1e-4 if dtype == "float32" else TOL
     assert rel_l2(to_np(tok), ref.tokens) <= tol
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= tol
+
+
+def test_mixed_block_folds_position_table(pkg):
+    """The C ABI takes LayerNorm folds per block. A tower whose block 0 runs its LayerNorms as
+    launches and whose block 1 is folded, on a grid whose rotary positions (200) fit the per-position
+    table of the unfolded qkv kernel but not the folded one: the whole-tower entry must size the
+    table for the folded kernel (here: fall back to the per-token table) instead of refusing in
+    block 1 after block 0's launches; tokens and the deepstack feature within 1e-2 of the bf16
+    oracle, as with every block folded."""
+    import dataclasses
+    spec = dataclasses.replace(pkg.spec_2b(), depth=2, deepstack_visual_indexes=(1,))
+    ospec = vt.VisionSpec(hidden_size=1024, out_hidden_size=2048, depth=2, num_heads=16, intermediate_size=4096,
+                          deepstack_visual_indexes=(1,))
+    params = pkg.random_params(spec, seed=17)
+    grids = [(1, 2, 200)]
+    px = pixels(grids, 18)
+    g = np.array(grids, np.int32)
+    ref = vt.encode_vision(params, px, grids, ospec, "bf16")
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params)
+    assert tower.metadata(g)[2].n_positions == 200
+    for mixed in (False, True):
+        if mixed:
+            b0 = tower._blocks_arr[0]
+            b0.qkv_ln.w = b0.qkv_ln.cd = b0.fc1_ln.w = b0.fc1_ln.cd = None
+        tok, ds = tower(px, g)
+        assert rel_l2(to_np(tok), ref.tokens) <= TOL, mixed
+        assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, mixed
