@@ -796,11 +796,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   }
 
   // The folded LayerNorm's (c, d) of the tile's columns and (rstd, -mean * rstd) of its rows, copied
-  // once into LDS (published by the first barrier below, read by the epilogue); tail units write
-  // raw partials and skip it.
+  // once into LDS (published by the first barrier below); read by the epilogue, and by the tail
+  // units, which write their partials already folded (the reductions then only sum).
   const f32x2* lcd = nullptr;
   if constexpr (LN) {
-    if (unit < 0) {
+    {
       f32x2* t = reinterpret_cast<f32x2*>(smem + ln_cd_offset<BM, BN, WM, WN, EPI>());
       for (int i = tid; i < BN + BM; i += S::THREADS) {
         if (i < BN) {
@@ -871,8 +871,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   }
 
   if (unit >= 0) {
-    // Tail unit: store the fp32 partial row-major within the tile, part[unit][BM][BN].
+    // Tail unit: store the fp32 partial row-major within the tile, part[unit][BM][BN]. With a
+    // folded LayerNorm the partial is folded here: rstd * acc, plus -mean * rstd * c + d in the
+    // first K part only, so the parts sum to the folded value.
     float* dst = p.part + (size_t)unit * BM * BN;
+    const bool first = unit % p.split == 0;
 #pragma unroll
     for (int a = 0; a < S::NB; ++a)
 #pragma unroll
@@ -880,8 +883,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int mm = wm * S::TM + b * 32 + l32, nn = wn * S::TN + a * 32 + 8 * g + 4 * hh;
-          *reinterpret_cast<f32x4*>(dst + (size_t)mm * BN + nn) =
-              f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+          float v[4] = {acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+          if constexpr (LN) {
+            const f32x2 rs = lcd[BN + mm];
+            const f32x4 cd01 = *reinterpret_cast<const f32x4*>(lcd + nn);
+            const f32x4 cd23 = *reinterpret_cast<const f32x4*>(lcd + nn + 2);
+            const float nm = first ? rs.y : 0.f;
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            ln_fold_cd(first ? cd01 : z, first ? cd23 : z, rs.x, nm, v);
+          }
+          *reinterpret_cast<f32x4*>(dst + (size_t)mm * BN + nn) = f32x4{v[0], v[1], v[2], v[3]};
         }
     return;
   }
@@ -924,12 +935,96 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
       for (int e = 0; e < 4; ++e) hi[e] += b[e];
     }
   }
-  if ((p.ln_stats || p.ln_part) && n < p.N) {
-    ln_fold_quad(p, m, n, lo);
-    if constexpr (EPI == kEpiQkvRope) ln_fold_quad(p, m, n + 32, hi);
-  }
+  // (a folded LayerNorm is already in the partials: the tail units fold before storing)
   if constexpr (EPI == kEpiQkvRope) epi_rope_pair(p, m, n, lo, hi);
   else epi_store_quad<EPI>(p, m, n, lo);
+}
+
+// The split-K reduction of the head_dim-72 rotary qkv GEMM (256 x 288 tiles, 4 heads of one of q, k,
+// v each): the tail tiles' fp32 partials (a folded LayerNorm already applied) summed over their K
+// parts, then the rope72 epilogue's arithmetic (bias, the reference's roundings, rotary, q
+// pre-scale). q / k tiles:
+// one thread per (token, head, 4 rotary pairs), dims d..d+3 and d+36..d+39, the group d = 32 also
+// zeroing dims 72..87 of the 88-wide rows; v tiles: one thread per (head, dim pair, 8 key
+// positions), 16-byte runs of V^T at the vt_pos positions. Tokens in [M, Np) get zeros.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_rope72_kernel(GemmParams p, int tail) {
+  static_assert(BN == 4 * 72 && BM % 8 == 0, "four 72-dim heads per tile");
+  constexpr int QK_ITEMS = BM * 4 * 9, V_ITEMS = 4 * 36 * (BM / 8);
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int t = (int)(idx / QK_ITEMS);
+  const int it = (int)(idx % QK_ITEMS);
+  if (t >= tail) return;
+  int tm, tn;
+  tile_coords(p.full_tiles + t, (max(p.M, p.Np) + BM - 1) / BM, (p.N + BN - 1) / BN, p.group_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int which = n0 / p.D, head0 = (n0 % p.D) / 72;
+  const float* part = p.part + (size_t)t * p.split * BM * BN;
+  auto sum4 = [&](int r, int c, float (&a)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = 0.f;
+    for (int s = 0; s < p.split; ++s) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(part + ((size_t)s * BM + r) * BN + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] += v[e];
+    }
+  };
+  // (a folded LayerNorm is already in the partials: the tail units fold before storing)
+  if (which < 2) {
+    const int r = it / 36, rem = it % 36, h = rem / 9, d = (rem % 9) * 4;
+    const int m = m0 + r;
+    if (m >= p.Np) return;
+    const int n = n0 + h * 72 + d;
+    float lo[4], hi[4];
+    sum4(r, h * 72 + d, lo);
+    sum4(r, h * 72 + d + 36, hi);
+    // (rope_values rounds the sums to bf16 before the bias, as the GEMM's staging does)
+    const f32x4 blo = *reinterpret_cast<const f32x4*>(p.bias + n);
+    const f32x4 bhi = *reinterpret_cast<const f32x4*>(p.bias + n + 36);
+    f32x4 c01, c23;
+    rope_cs_global(p, m, d, c01, c23);
+    u32x2 o1, o2;
+    rope_values(p, which, m, d, blo, bhi, lo, hi, c01, c23, o1, o2);
+    bf16* row = (which == 0 ? p.q : p.k) + ((int64_t)(head0 + h) * p.Np + m) * 88;
+    *reinterpret_cast<u32x2*>(row + d) = o1;
+    *reinterpret_cast<u32x2*>(row + 36 + d) = o2;
+    if (d == 32) {
+      *reinterpret_cast<u32x4*>(row + 72) = u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(row + 80) = u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+  if (it >= V_ITEMS) return;
+  // (dim pairs fastest: the lanes of a wave read one partial row's consecutive columns)
+  const int dp = it % 36, rest = it / 36, h = rest % 4, pc = rest / 4;
+  const int d = 2 * dp, P = m0 + pc * 8;
+  if (P >= p.Np) return;
+  const int n = n0 + h * 72 + d;
+  const float b0 = p.bias[n], b1 = p.bias[n + 1];
+  float v0[8], v1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int m = vt_pos(P + e);               // the token stored at position P + e
+    float a0 = 0.f, a1 = 0.f;
+    for (int s = 0; s < p.split; ++s) {
+      const f32x2 v = *reinterpret_cast<const f32x2*>(part + ((size_t)s * BM + (m - m0)) * BN + h * 72 + d);
+      a0 += v.x;
+      a1 += v.y;
+    }
+    if (m < p.M) {
+      round_bf16_pair(a0, a1);
+      v0[e] = a0 + b0;
+      v1[e] = a1 + b1;
+    } else {
+      v0[e] = 0.f;
+      v1[e] = 0.f;
+    }
+  }
+  bf16* row = p.vt + ((int64_t)(head0 + h) * 72 + d) * p.Np + P;
+  *reinterpret_cast<u32x4*>(row) = u32x4{pack_bf16x2(v0[0], v0[1]), pack_bf16x2(v0[2], v0[3]),
+                                         pack_bf16x2(v0[4], v0[5]), pack_bf16x2(v0[6], v0[7])};
+  *reinterpret_cast<u32x4*>(row + p.Np) = u32x4{pack_bf16x2(v1[0], v1[1]), pack_bf16x2(v1[2], v1[3]),
+                                                pack_bf16x2(v1[4], v1[5]), pack_bf16x2(v1[6], v1[7])};
 }
 
 // Compute units of the current device. A write-once per-device cache: every thread that fills
@@ -972,8 +1067,9 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
   const int tail = tiles % cus;
   GemmPlan g{tiles, 1, 0, (tiles / cus) * tile_us + (tail ? round_fraction(tail, cus) * tile_us : 0.0)};
   if (tail == 0 || !p.part || split_mode < 0) return g;
-  const int split = std::min(std::min(8, KT), cus / tail);
-  if (split < 2 || (int64_t)tail * split * BM * BN > p.part_elems) return g;
+  int split = std::min(std::min(8, KT), cus / tail);
+  while (split >= 2 && (int64_t)tail * split * BM * BN > p.part_elems) --split;   // what the workspace holds
+  if (split < 2) return g;
   const double part_bytes = 2.0 * tail * split * BM * BN * sizeof(float);
   const double cost = (tiles / cus) * tile_us + round_fraction(tail * split, cus) * tile_us / split +
                       part_bytes / kPartialBytesPerUs + kReduceLaunchUs;
@@ -1021,6 +1117,11 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   if (rc || g.tail == 0) return rc;
   if constexpr (EPI == kEpiBiasPosEmbed) {
     return set_error(QVL_ERR_INVALID_ARG, "gemm_bf16: the pos-embed epilogue has no split-K tail");
+  } else if constexpr (EPI == kEpiQkvRope72) {
+    const int64_t items = (int64_t)g.tail * BM * 4 * 9;
+    hipLaunchKernelGGL((gemm_splitk_reduce_rope72_kernel<BM, BN>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                       stream, p, g.tail);
+    return check_launch("gemm_splitk_reduce_rope72");
   } else {
   const int64_t items = (int64_t)g.tail * BM * ((EPI == kEpiQkvRope) ? BN / 8 : BN / 4);
   hipLaunchKernelGGL((gemm_splitk_reduce_kernel<BM, BN, EPI>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
@@ -1077,11 +1178,14 @@ int gemm_set_plan(int tile, int split_mode, int group_n) {
   return QVL_OK;
 }
 
-// head_dim-72 qkv GEMM: 256 x 288 tiles (4 heads each, 12 waves of 64 x 96), no tail split.
+// head_dim-72 qkv GEMM: 256 x 288 tiles (4 heads each, 12 waves of 64 x 96). The last partial round
+// is split along K only when a plan forces it (gemm_splitk_reduce_rope72_kernel applies the
+// epilogue): at config 4 (336 tiles on 256 CUs) the split ran its GEMM in 76 us and the reduction of
+// the 47 MB of fp32 partials in 16 us, against 91-93 us unsplit (MI355X), so it is not the default.
 constexpr double kRate256x288 = 1.50e6;
 
 static int dispatch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
-  const GemmPlan g = plan_gemm<256, 288>(p, gemm_device_cus(), kRate256x288, -1);
+  const GemmPlan g = plan_gemm<256, 288>(p, gemm_device_cus(), kRate256x288, t_plan.split_mode == 1 ? 1 : -1);
   if (p.ln_stats || p.ln_part) return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, true>(p, g, stream);
   return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, false>(p, g, stream);
 }
