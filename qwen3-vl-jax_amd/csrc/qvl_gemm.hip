@@ -84,24 +84,31 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
   b = bf16_hi(w);
 }
 
-// The learned pos-embed of token m at features n..n+7 (model.py:751-764) for kEpiBiasPosEmbed, in
-// the arithmetic of the pos-embed kernel: each tap product rounded to bf16, the partial sums taken
-// left to right and rounded, taps of weight 0 skipped (their products are zeros).
-__device__ __forceinline__ void pos_embed_oct(const GemmParams& p, int m, int n, float (&acc)[8]) {
+// The learned pos-embed of one token at features n..n+7 (model.py:751-764) for kEpiBiasPosEmbed,
+// in the arithmetic of the pos-embed kernel: each tap product rounded to bf16, the partial sums
+// taken left to right and rounded, taps of weight 0 skipped (their products are zeros). `tap`: the
+// token's 4 (index, weight bits) pairs, staged in LDS; every live tap's table row is loaded before
+// any is combined.
+__device__ __forceinline__ void pos_embed_oct(const GemmParams& p, const int2* tap, int n, float (&acc)[8]) {
+  const int4 t01 = *reinterpret_cast<const int4*>(tap), t23 = *reinterpret_cast<const int4*>(tap + 2);
+  const int ti[4] = {t01.x, t01.z, t23.x, t23.z};
+  const float tw[4] = {__int_as_float(t01.y), __int_as_float(t01.w), __int_as_float(t23.y), __int_as_float(t23.w)};
+  u32x4 row[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    row[j] = tw[j] != 0.f ? *reinterpret_cast<const u32x4*>(p.pe_table + (int64_t)ti[j] * p.N + n) : u32x4{0u, 0u, 0u, 0u};
   bool first = true;
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float tw = p.pe_w[(int64_t)j * p.M + m];
-    if (tw == 0.f) continue;
-    const int ti = p.pe_idx[(int64_t)j * p.M + m];
-    const u32x4 w = *reinterpret_cast<const u32x4*>(p.pe_table + (int64_t)ti * p.N + n);
+    if (tw[j] == 0.f) continue;
+    const u32x4 w = row[j];
     const float v[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
                         bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float t = round_bf16(tw * v[e]);
+      const float t = round_bf16(tw[j] * v[e]);
       acc[e] = first ? t : round_bf16(acc[e] + t);
     }
     first = false;
@@ -114,7 +121,7 @@ __device__ __forceinline__ void pos_embed_oct(const GemmParams& p, int m, int n,
 // values, so only the sum with the bias is rounded (pairwise, one conversion per two values).
 template <int EPI>
 __device__ __forceinline__ u32x4 epi_store_oct(const GemmParams& p, int m, int n, u32x4 raw, const f32x4& b0,
-                                               const f32x4& b1, bool full, bool vec16) {
+                                               const f32x4& b1, bool full, bool vec16, const int2* tap = nullptr) {
   float v[8] = {bf16_lo(raw.x) + b0[0], bf16_hi(raw.x) + b0[1], bf16_lo(raw.y) + b0[2], bf16_hi(raw.y) + b0[3],
                 bf16_lo(raw.z) + b1[0], bf16_hi(raw.z) + b1[1], bf16_lo(raw.w) + b1[2], bf16_hi(raw.w) + b1[3]};
   if constexpr (EPI != kEpiBias) {
@@ -129,7 +136,7 @@ __device__ __forceinline__ u32x4 epi_store_oct(const GemmParams& p, int m, int n
   if constexpr (EPI == kEpiBiasPosEmbed) {
     // (the host guarantees whole, 16-byte aligned octets for this epilogue)
     float r[8];
-    pos_embed_oct(p, m, n, r);
+    pos_embed_oct(p, tap, n, r);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] += r[e];
     const u32x4 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
@@ -356,7 +363,7 @@ template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
                                                   f32x16 (&acc)[GemmShape<BM, BN, WM, WN>::NB][GemmShape<BM, BN, WM, WN>::MB],
                                                   int m0, int n0, int wm, int wn, int lane, int tid, bf16* smem,
-                                                  const f32x2* lcd) {
+                                                  const f32x2* lcd, const int2* ltaps) {
   using S = GemmShape<BM, BN, WM, WN>;
   constexpr int CH = BN / 8;
   const int l32 = lane & 31, hh = lane >> 5;
@@ -400,7 +407,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmParams& p,
     const int m = m0 + r;
     if (m >= p.M) break;               // rows only grow with i
     const u32x4 raw = *reinterpret_cast<const u32x4*>(smem + r * BN + ((c ^ (r % CH)) << 3));
-    const u32x4 out = epi_store_oct<EPI>(p, m, n, raw, b0, b1, full, vec16);
+    const u32x4 out = epi_store_oct<EPI>(p, m, n, raw, b0, b1, full, vec16, ltaps ? ltaps + 4 * r : nullptr);
     if constexpr (EPI == kEpiBiasResidual || EPI == kEpiBiasPosEmbed) {
       // 16 consecutive threads, aligned to 16, hold the 16 octets of one 128-column group of row m
       static_assert(CH % 16 == 0, "row statistics need 128-column groups within a tile row");
@@ -814,6 +821,19 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
     }
   }
 
+  // kEpiBiasPosEmbed: the tile's rows' 4 bilinear taps (index, weight bits) copied once into LDS above
+  // the ring / staging area (published by the first barrier below, read by the epilogue).
+  const int2* ltaps = nullptr;
+  if constexpr (EPI == kEpiBiasPosEmbed) {
+    int2* t = reinterpret_cast<int2*>(smem + rope_tab_offset<BM, BN, WM, WN, EPI, LN>());
+    for (int i = tid; i < BM * 4; i += S::THREADS) {
+      const int m = m0 + (i >> 2), j = i & 3;
+      t[i] = m < p.M ? int2{p.pe_idx[(int64_t)j * p.M + m], __float_as_int(p.pe_w[(int64_t)j * p.M + m])}
+                     : int2{0, 0};
+    }
+    ltaps = t;
+  }
+
   f32x16 acc[S::NB][S::MB];
 #pragma unroll
   for (int a = 0; a < S::NB; ++a)
@@ -902,7 +922,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   } else if constexpr (EPI == kEpiQkvRope72) {
     gemm_epilogue_rope72_lds<BM, BN, WM, WN, LN>(p, acc, m0, n0, wm, wn, lane, tid, smem, ltab, lcd);
   } else {
-    gemm_epilogue_lds<BM, BN, WM, WN, EPI, LN>(p, acc, m0, n0, wm, wn, lane, tid, smem, lcd);
+    gemm_epilogue_lds<BM, BN, WM, WN, EPI, LN>(p, acc, m0, n0, wm, wn, lane, tid, smem, lcd, ltaps);
   }
 }
 
@@ -1100,10 +1120,12 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   constexpr bool kRope = EPI == kEpiQkvRope || EPI == kEpiQkvRope72;
   // rotary epilogues: room for the largest position table (rope_table_lds_bytes) after the ring
   // (and the folded LayerNorm's (c, d))
+  // (the pos-embed epilogue's tap table takes the same place: BM rows x 4 taps x 8 bytes)
+  constexpr size_t pe_taps = EPI == kEpiBiasPosEmbed ? (size_t)BM * 4 * 8 : 0;
   constexpr size_t lds_max = (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16) +
-                             (kRope ? rope_table_lds_bytes(EPI == kEpiQkvRope ? 64 : 72, LN) : 0);
+                             (kRope ? rope_table_lds_bytes(EPI == kEpiQkvRope ? 64 : 72, LN) : 0) + pe_taps;
   static_assert(lds_max <= 163840, "LDS budget");
-  const size_t lds = p.rtab ? lds_max : (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16);
+  const size_t lds = p.rtab ? lds_max : (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16) + pe_taps;
   // once per instantiation (a C++ function-local static: initialised exactly once, thread-safe)
   static const hipError_t attr_rc = hipFuncSetAttribute((const void*)gemm_bf16_kernel<BM, BN, WM, WN, EPI, LN>,
                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
