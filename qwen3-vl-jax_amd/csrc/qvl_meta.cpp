@@ -101,7 +101,6 @@ int qvl_vision_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int
         cu[s++] = (int32_t)acc;
       }
   }
-  const int mm = merge * merge;
   int64_t off = 0;
   std::vector<double> hs, ws;
   std::vector<int32_t> hf, wf;
@@ -123,36 +122,42 @@ int qvl_vision_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int
     };
     if (tap_idx || tap_w) { linspace(h, hs, hf); linspace(w, ws, wf); }
     const int64_t hw = (int64_t)h * w;
-    for (int64_t n = 0; n < (int64_t)t * hw; ++n) {
-      const int64_t f = n / hw, r = n % hw, g = r / mm;
-      const int hb = (int)(g / bw), wb = (int)(g % bw);
-      const int mi = (int)((r % mm) / merge), mj = (int)(r % merge);
-      const int row = merge * hb + mi, col = merge * wb + mj;
-      const int64_t tok = off + n;
-      if (pos_hw) { pos_hw[2 * tok] = row; pos_hw[2 * tok + 1] = col; }
-      if (tap_idx || tap_w) {
-        // jnp.repeat(.., t, axis=0) frame expansion: raster row (f*h*w + row*w + col) // t.
-        const int64_t src = (f * hw + (int64_t)row * w + col) / t;
-        const int pr = (int)(src / w), pc = (int)(src % w);
-        const int h0 = hf[pr], w0 = wf[pc];
-        const int h1 = std::min(h0 + 1, num_grid - 1), w1 = std::min(w0 + 1, num_grid - 1);
-        const double dh = hs[pr], dw = ws[pc];
-        if (tap_idx) {
-          tap_idx[0 * N + tok] = h0 * num_grid + w0;
-          tap_idx[1 * N + tok] = h0 * num_grid + w1;
-          tap_idx[2 * N + tok] = h1 * num_grid + w0;
-          tap_idx[3 * N + tok] = h1 * num_grid + w1;
-        }
-        if (tap_w) {
-          const double wv[4] = {(1.0 - dh) * (1.0 - dw), (1.0 - dh) * dw, dh * (1.0 - dw), dh * dw};
-          for (int j = 0; j < 4; ++j) {
-            float v = (float)wv[j];
-            if (dtype == QVL_DTYPE_BF16) v = host_round_bf16(v);
-            tap_w[j * N + tok] = v;
-          }
-        }
-      }
-    }
+    // Tokens in merge-block order, walked structurally (no per-token division): frame f, block row
+    // hb, block column wb, then the merge x merge positions (mi, mj) of the block.
+    int64_t tok = off;
+    for (int f = 0; f < t; ++f)
+      for (int hb = 0; hb < h / merge; ++hb)
+        for (int wb = 0; wb < bw; ++wb)
+          for (int mi = 0; mi < merge; ++mi)
+            for (int mj = 0; mj < merge; ++mj, ++tok) {
+              const int row = merge * hb + mi, col = merge * wb + mj;
+              if (pos_hw) { pos_hw[2 * tok] = row; pos_hw[2 * tok + 1] = col; }
+              if (!(tap_idx || tap_w)) continue;
+              // jnp.repeat(.., t, axis=0) frame expansion: raster row (f*h*w + row*w + col) // t.
+              int pr = row, pc = col;
+              if (t > 1) {
+                const int64_t src = (f * hw + (int64_t)row * w + col) / t;
+                pr = (int)(src / w);
+                pc = (int)(src - (int64_t)pr * w);
+              }
+              const int h0 = hf[pr], w0 = wf[pc];
+              const int h1 = std::min(h0 + 1, num_grid - 1), w1 = std::min(w0 + 1, num_grid - 1);
+              const double dh = hs[pr], dw = ws[pc];
+              if (tap_idx) {
+                tap_idx[0 * N + tok] = h0 * num_grid + w0;
+                tap_idx[1 * N + tok] = h0 * num_grid + w1;
+                tap_idx[2 * N + tok] = h1 * num_grid + w0;
+                tap_idx[3 * N + tok] = h1 * num_grid + w1;
+              }
+              if (tap_w) {
+                const double wv[4] = {(1.0 - dh) * (1.0 - dw), (1.0 - dh) * dw, dh * (1.0 - dw), dh * dw};
+                for (int j = 0; j < 4; ++j) {
+                  float v = (float)wv[j];
+                  if (dtype == QVL_DTYPE_BF16) v = host_round_bf16(v);
+                  tap_w[j * N + tok] = v;
+                }
+              }
+            }
     off += (int64_t)t * hw;
   }
   return QVL_OK;

@@ -351,6 +351,28 @@ def _ptr(t) -> int:
     return t.data_ptr() if t is not None else 0
 
 
+def _to_device_packed(arrays: Dict[str, np.ndarray], device) -> Dict[str, object]:
+    """Copy 4-byte host arrays (int32 / float32) to the device in one transfer: packed into one
+    int32 buffer at 256-byte-aligned offsets, returned as device views of their shapes and dtypes
+    (the views share the one device allocation)."""
+    torch = _torch()
+    offs, total = {}, 0
+    for name, a in arrays.items():
+        if a.dtype.itemsize != 4:
+            raise TypeError(f"{name}: {a.dtype} (4-byte elements expected)")
+        offs[name] = total
+        total += -(-a.size // 64) * 64
+    buf = np.zeros(max(total, 64), np.int32)
+    for name, a in arrays.items():
+        buf[offs[name]: offs[name] + a.size] = np.ascontiguousarray(a).reshape(-1).view(np.int32)
+    dev = torch.from_numpy(buf).to(device)
+    out = {}
+    for name, a in arrays.items():
+        v = dev[offs[name]: offs[name] + a.size].view(a.shape)
+        out[name] = v.view(torch.float32) if a.dtype == np.float32 else v
+    return out
+
+
 class Qwen3VisionTransformer:
     """The vision tower on libqvl. Bind params once (`bind`), then call like the reference module:
     `tokens, deepstack = tower(pixel_values, grid_thw)`. `dtype` defaults to float32, as the
@@ -602,10 +624,20 @@ class Qwen3VisionTransformer:
         m = grid_metadata(g, s.spatial_merge_size, s.num_position_embeddings, self.qdtype, s.num_heads)
         if s.use_window:
             m = window_grid_metadata(m, g, s.spatial_merge_size, s.patch_size, s.window_size, s.num_heads)
-        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
         nz = lambda a: a if a is not None and len(a) else np.zeros((1, 4), np.int32)
-        tens = {"cu_seqlens": dev(m.cu_seqlens), "pos_hw": dev(m.pos_hw), "tap_idx": dev(m.tap_idx),
-                "tap_w": dev(m.tap_w), "tiles": dev(nz(m.tiles))}
+        host = {"cu_seqlens": m.cu_seqlens, "pos_hw": m.pos_hw, "tap_idx": m.tap_idx, "tap_w": m.tap_w,
+                "tiles": nz(m.tiles)}
+        if s.use_window:
+            host["window_tiles"] = nz(m.window_tiles)
+            host["window_index"] = m.window_index if len(m.window_index) else np.zeros(1, np.int32)
+            host["window_reverse"] = m.window_reverse if len(m.window_reverse) else np.zeros(1, np.int32)
+        split = None
+        if self.split_attention and self.qdtype == capi.QVL_DTYPE_BF16 and s.head_dim in (64, 72, 80):
+            n_cus = torch.cuda.get_device_properties(torch.device(self.device)).multi_processor_count
+            cu_full = m.cu_full if s.use_window else m.cu_seqlens
+            split, n_whole = attention_worklist_split(cu_full, s.num_heads, s.head_dim, n_cus)
+            host["split_tiles"] = nz(split)
+        tens = _to_device_packed(host, self.device)
         md = capi.VisionMetadataDev()
         md.n_tokens = m.n_tokens
         md.n_positions = m.n_positions
@@ -613,18 +645,11 @@ class Qwen3VisionTransformer:
         md.pos_hw, md.tap_idx, md.tap_w, md.tiles = (tens["pos_hw"].data_ptr(), tens["tap_idx"].data_ptr(),
                                                      tens["tap_w"].data_ptr(), tens["tiles"].data_ptr())
         if s.use_window:
-            tens["window_tiles"] = dev(nz(m.window_tiles))
-            tens["window_index"] = dev(m.window_index if len(m.window_index) else np.zeros(1, np.int32))
-            tens["window_reverse"] = dev(m.window_reverse if len(m.window_reverse) else np.zeros(1, np.int32))
             md.n_window_tiles = len(m.window_tiles)
             md.window_tiles = tens["window_tiles"].data_ptr()
             md.window_index = tens["window_index"].data_ptr()
             md.window_reverse = tens["window_reverse"].data_ptr()
-        if self.split_attention and self.qdtype == capi.QVL_DTYPE_BF16 and s.head_dim in (64, 72, 80):
-            n_cus = torch.cuda.get_device_properties(torch.device(self.device)).multi_processor_count
-            cu_full = m.cu_full if s.use_window else m.cu_seqlens
-            split, n_whole = attention_worklist_split(cu_full, s.num_heads, s.head_dim, n_cus)
-            tens["split_tiles"] = dev(nz(split))
+        if split is not None:
             md.n_split_tiles = len(split)
             md.n_split_whole = n_whole
             md.split_tiles = tens["split_tiles"].data_ptr()

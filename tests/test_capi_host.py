@@ -282,3 +282,22 @@ def test_attention_worklist_split_checks(pkg):
     nb = C.c_size_t()
     assert lib.qvl_attention_split_workspace_size(64, 10, 4, C.byref(nb)) == 0 and nb.value == 6 * 128 * 66 * 4
     assert lib.qvl_attention_split_workspace_size(72, 10, 11, C.byref(nb)) == -1
+
+
+def test_metadata_packed_into_one_transfer(pkg):
+    """The per-grid device metadata goes to the device in one copy (_to_device_packed): every array
+    comes back with its shape, dtype and bits, at a 256-byte-aligned offset of one allocation
+    (run on the CPU device here; the tower passes its GPU)."""
+    import torch
+    m = pkg.grid_metadata([(1, 48, 48), (2, 10, 14)])
+    host = {"cu_seqlens": m.cu_seqlens, "pos_hw": m.pos_hw, "tap_idx": m.tap_idx, "tap_w": m.tap_w, "tiles": m.tiles}
+    out = pkg.vision._to_device_packed(host, "cpu")
+    base = out["cu_seqlens"].data_ptr()
+    for name, a in host.items():
+        t = out[name]
+        assert tuple(t.shape) == a.shape, name
+        assert t.dtype == (torch.float32 if a.dtype == np.float32 else torch.int32), name
+        np.testing.assert_array_equal(t.numpy(), a)
+        assert (t.data_ptr() - base) % 256 == 0, name
+    with pytest.raises(TypeError):
+        pkg.vision._to_device_packed({"x": np.zeros(3, np.int64)}, "cpu")
