@@ -102,6 +102,13 @@ class TorchTower:
             out[s:e] = o.transpose(0, 1).to(self.dt)
         return self._dense(out.reshape(n, D), blk["proj"])
 
+    def block(self, i, x, cos, sin, cu):
+        """VisionBlock i (model.py:627-630) on x [N, D] in the tower dtype; cos / sin [N, 1, hd] in the
+        tower dtype, cu the segment bounds."""
+        blk = self.blocks[i]
+        x = x + self._attention(self._ln(x, blk["norm1"]), blk, cos, sin, cu)
+        return x + self._dense(self._gelu(self._dense(self._ln(x, blk["norm2"]), blk["fc1"])), blk["fc2"])
+
     def _merger(self, x, m, postshuffle):
         D4 = 4 * self.spec.hidden_size
         if postshuffle:
@@ -143,9 +150,8 @@ class TorchTower:
             cu = ix.cu_seqlens_ref(grid)
             feats = []
             ds = list(self.spec.deepstack_visual_indexes)
-            for i, blk in enumerate(self.blocks):
-                x = x + self._attention(self._ln(x, blk["norm1"]), blk, cos, sin, cu)
-                x = x + self._dense(self._gelu(self._dense(self._ln(x, blk["norm2"]), blk["fc1"])), blk["fc2"])
+            for i in range(len(self.blocks)):
+                x = self.block(i, x, cos, sin, cu)
                 if keep_layers:
                     out["layers"].append(x.clone())
                 if i in ds:
