@@ -715,27 +715,55 @@ __device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, 
   tn = panel * group_n + r % width;
 }
 
-// Dynamic LDS of the GEMM (elements): the 2-stage operand ring or the epilogue staging, whichever
-// is larger; the rotary epilogues put their position table right after it.
+// Dynamic LDS of the GEMM. Elements [0, E): the operand ring (`stages` stages) or the epilogue
+// staging, whichever is larger. Above it: for a folded LayerNorm (LN kernels) the tile's BN columns'
+// (c, d) then its BM rows' (rstd, -mean * rstd), 8 bytes each; then the rotary epilogues'
+// per-position table or the pos-embed epilogue's taps.
 template <int BM, int BN, int WM, int WN, int EPI>
-__host__ __device__ constexpr int gemm_lds_elems() {
-  return (2 * GemmShape<BM, BN, WM, WN>::LDS_ELEMS > (EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN))
-             ? 2 * GemmShape<BM, BN, WM, WN>::LDS_ELEMS
+__host__ __device__ constexpr int gemm_lds_elems_n(int stages) {
+  return (stages * GemmShape<BM, BN, WM, WN>::LDS_ELEMS > (EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN))
+             ? stages * GemmShape<BM, BN, WM, WN>::LDS_ELEMS
              : (EPI == kEpiQkvRope72 ? BM * kR72 : BM * BN);
 }
-// Above the ring / staging area: for a folded LayerNorm (LN kernels) the tile's BN columns' (c, d)
-// then its BM rows' (rstd, -mean * rstd), 8 bytes each; then the rotary epilogues' per-position table.
-template <int BM, int BN, int WM, int WN, int EPI>
-__host__ __device__ constexpr int ln_cd_offset() { return (gemm_lds_elems<BM, BN, WM, WN, EPI>() + 7) / 8 * 8; }
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
+__host__ __device__ constexpr int gemm_lds_bytes_n(int stages) {
+  return (((gemm_lds_elems_n<BM, BN, WM, WN, EPI>(stages) + 7) / 8 * 8) + (LN ? (BN + BM) * 4 : 0)) * 2 +
+         (EPI == kEpiQkvRope || EPI == kEpiQkvRope72 ? rope_table_lds_bytes(EPI == kEpiQkvRope ? 64 : 72, LN) : 0) +
+         (EPI == kEpiBiasPosEmbed ? BM * 4 * 8 : 0);
+}
+// Operand-ring stages: three (the DMA runs two k-steps ahead, which hides the latency of operands
+// that come cold from HBM behind tiles whose k-step is short) where that fits the 160 KB of LDS and
+// every wave issues the same number of DMA instructions per stage (the ring's partial vmcnt wait
+// counts them); else two.
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
+__host__ __device__ constexpr int gemm_stages() {
+  using S = GemmShape<BM, BN, WM, WN>;
+  return (BM % S::ROWS_PER_PASS == 0 && BN % S::ROWS_PER_PASS == 0 &&
+          gemm_lds_bytes_n<BM, BN, WM, WN, EPI, LN>(3) <= 163840) ? 3 : 2;
+}
+template <int BM, int BN, int WM, int WN, int EPI, bool LN>
+__host__ __device__ constexpr int ln_cd_offset() {
+  return (gemm_lds_elems_n<BM, BN, WM, WN, EPI>(gemm_stages<BM, BN, WM, WN, EPI, LN>()) + 7) / 8 * 8;
+}
 template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __host__ __device__ constexpr int rope_tab_offset() {
-  return ln_cd_offset<BM, BN, WM, WN, EPI>() + (LN ? (BN + BM) * 4 : 0);
+  return ln_cd_offset<BM, BN, WM, WN, EPI, LN>() + (LN ? (BN + BM) * 4 : 0);
+}
+
+// Waits until at most N of this wave's vector memory operations are outstanding (they complete in
+// issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "I"(N) : "memory");
 }
 
 template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
   using S = GemmShape<BM, BN, WM, WN>;
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];   // [2][BM+BN][64]
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];   // [NS][BM+BN][64]
+  constexpr int NS = gemm_stages<BM, BN, WM, WN, EPI, LN>();
+  constexpr int kDmaPerStage = S::XPT + S::WPT;   // per wave (uniform when NS == 3)
 
   // Work assignment: workgroups [0, full_tiles) each own a whole tile (XCD-remapped); the rest
   // own 1/split of the K range of one of the remaining "tail" tiles and write fp32 partials.
@@ -787,8 +815,12 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         dma16(rww, wv, (uint32_t)((i * S::ROWS_PER_PASS * p.K + k0) * 2), wa + (i * S::ROWS_PER_PASS + wave * 8) * kBK * 2);
   };
 
-  // The first k-step's operands are on their way while the prologue below copies its tables.
+  // The first k-step's operands (and with three stages the second's) are on their way while the
+  // prologue below copies its tables.
   dma_stage(kt0 * kBK, 0);
+  if constexpr (NS == 3) {
+    if (kt0 + 1 < kt1) dma_stage((kt0 + 1) * kBK, 1);
+  }
 
   // The qkv rotary epilogues' per-position (cos, sin) table, copied once into LDS above the
   // operand ring / staging area (its first barrier below publishes it).
@@ -808,7 +840,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   const f32x2* lcd = nullptr;
   if constexpr (LN) {
     {
-      f32x2* t = reinterpret_cast<f32x2*>(smem + ln_cd_offset<BM, BN, WM, WN, EPI>());
+      f32x2* t = reinterpret_cast<f32x2*>(smem + ln_cd_offset<BM, BN, WM, WN, EPI, LN>());
       for (int i = tid; i < BN + BM; i += S::THREADS) {
         if (i < BN) {
           t[i] = n0 + i < p.N ? p.ln_cd[n0 + i] : f32x2{0.f, 0.f};
@@ -864,15 +896,22 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   };
   constexpr int NMF = S::NB * S::MB;
 
-  wait_dma();
+  // Stage s of the ring holds k-step kt0 + s (mod NS); a stage is refilled one barrier after its
+  // last read. The wait before each barrier lets only the newest stage's DMA stay in flight.
+  if (NS == 3 && kt0 + 1 < kt1) wait_vmcnt<kDmaPerStage>(); else wait_dma();
   __syncthreads();
   read_frags(smem, 0, 0);
 
+  int cur = 0;
   for (int kt = kt0; kt < kt1; ++kt) {
-    const int cur = (kt - kt0) & 1;
     const bf16* xs = smem + cur * S::LDS_ELEMS;
     const bool more = kt + 1 < kt1;
-    if (more) dma_stage((kt + 1) * kBK, cur ^ 1);
+    const int nxt = NS == 3 ? (cur == 2 ? 0 : cur + 1) : (cur ^ 1);
+    if constexpr (NS == 3) {
+      if (kt + 2 < kt1) dma_stage((kt + 2) * kBK, cur == 0 ? 2 : cur - 1);
+    } else {
+      if (more) dma_stage((kt + 1) * kBK, nxt);
+    }
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       if (ks + 1 < kBK / 16) read_frags(xs, ks + 1, (ks + 1) & 1);
@@ -885,9 +924,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         }
       }
     }
-    wait_dma();
+    if (NS == 3 && kt + 2 < kt1) wait_vmcnt<kDmaPerStage>(); else wait_dma();
     __syncthreads();
-    if (more) read_frags(smem + (cur ^ 1) * S::LDS_ELEMS, 0, 0);
+    if (more) read_frags(smem + nxt * S::LDS_ELEMS, 0, 0);
+    cur = nxt;
   }
 
   if (unit >= 0) {
@@ -1124,6 +1164,8 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
   constexpr size_t pe_taps = EPI == kEpiBiasPosEmbed ? (size_t)BM * 4 * 8 : 0;
   constexpr size_t lds_max = (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16) +
                              (kRope ? rope_table_lds_bytes(EPI == kEpiQkvRope ? 64 : 72, LN) : 0) + pe_taps;
+  static_assert(lds_max == (size_t)gemm_lds_bytes_n<BM, BN, WM, WN, EPI, LN>(gemm_stages<BM, BN, WM, WN, EPI, LN>()),
+                "LDS layout");
   static_assert(lds_max <= 163840, "LDS budget");
   const size_t lds = p.rtab ? lds_max : (size_t)rope_tab_offset<BM, BN, WM, WN, EPI, LN>() * sizeof(bf16) + pe_taps;
   // once per instantiation (a C++ function-local static: initialised exactly once, thread-safe)
