@@ -732,14 +732,11 @@ __host__ __device__ constexpr int gemm_lds_bytes_n(int stages) {
          (EPI == kEpiBiasPosEmbed ? BM * 4 * 8 : 0);
 }
 // Operand-ring stages: three (the DMA runs two k-steps ahead, which hides the latency of operands
-// that come cold from HBM behind tiles whose k-step is short) where that fits the 160 KB of LDS and
-// every wave issues the same number of DMA instructions per stage (the ring's partial vmcnt wait
-// counts them); else two.
+// that come cold from HBM behind tiles whose k-step is short) where that fits the 160 KB of LDS;
+// else two.
 template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __host__ __device__ constexpr int gemm_stages() {
-  using S = GemmShape<BM, BN, WM, WN>;
-  return (BM % S::ROWS_PER_PASS == 0 && BN % S::ROWS_PER_PASS == 0 &&
-          gemm_lds_bytes_n<BM, BN, WM, WN, EPI, LN>(3) <= 163840) ? 3 : 2;
+  return gemm_lds_bytes_n<BM, BN, WM, WN, EPI, LN>(3) <= 163840 ? 3 : 2;
 }
 template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __host__ __device__ constexpr int ln_cd_offset() {
@@ -757,13 +754,23 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" :: "I"(N) : "memory");
 }
+// The same for a wave-uniform count n <= MAX (a scalar branch to the matching immediate).
+template <int MAX>
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+  if constexpr (MAX > 0) {
+    if (n < MAX) {
+      wait_vmcnt_upto<MAX - 1>(n);
+      return;
+    }
+  }
+  wait_vmcnt<MAX>();
+}
 
 template <int BM, int BN, int WM, int WN, int EPI, bool LN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p) {
   using S = GemmShape<BM, BN, WM, WN>;
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];   // [NS][BM+BN][64]
   constexpr int NS = gemm_stages<BM, BN, WM, WN, EPI, LN>();
-  constexpr int kDmaPerStage = S::XPT + S::WPT;   // per wave (uniform when NS == 3)
 
   // Work assignment: workgroups [0, full_tiles) each own a whole tile (XCD-remapped); the rest
   // own 1/split of the K range of one of the remaining "tail" tiles and write fp32 partials.
@@ -803,6 +810,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
   const u32x4 rxw = rsrc_words(p.x, (uint32_t)((int64_t)p.M * p.lda * 2));
   const u32x4 rww = rsrc_words(p.w, (uint32_t)((int64_t)p.N * p.K * 2));
   const uint32_t lds_base = lds_addr_of(smem);
+  // DMA instructions this wave issues per stage (the last pass of an operand may skip it).
+  const int dma_per_stage = (BM % S::ROWS_PER_PASS == 0 || (S::XPT - 1) * S::ROWS_PER_PASS + wave * 8 < BM ? S::XPT : S::XPT - 1) +
+                            (BN % S::ROWS_PER_PASS == 0 || (S::WPT - 1) * S::ROWS_PER_PASS + wave * 8 < BN ? S::WPT : S::WPT - 1);
+  // Wait for every stage but the newest one (its dma_per_stage operations may stay in flight).
+  auto wait_all_but_newest = [&]() {
+    if constexpr (BM % S::ROWS_PER_PASS == 0 && BN % S::ROWS_PER_PASS == 0)
+      wait_vmcnt<S::XPT + S::WPT>();
+    else
+      wait_vmcnt_upto<S::XPT + S::WPT>(dma_per_stage);
+  };
   auto dma_stage = [&](int k0, int stage) {
     const uint32_t xa = lds_base + stage * S::LDS_ELEMS * 2, wa = xa + BM * kBK * 2;
 #pragma unroll
@@ -898,7 +915,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
 
   // Stage s of the ring holds k-step kt0 + s (mod NS); a stage is refilled one barrier after its
   // last read. The wait before each barrier lets only the newest stage's DMA stay in flight.
-  if (NS == 3 && kt0 + 1 < kt1) wait_vmcnt<kDmaPerStage>(); else wait_dma();
+  if (NS == 3 && kt0 + 1 < kt1) wait_all_but_newest(); else wait_dma();
   __syncthreads();
   read_frags(smem, 0, 0);
 
@@ -924,7 +941,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
         }
       }
     }
-    if (NS == 3 && kt + 2 < kt1) wait_vmcnt<kDmaPerStage>(); else wait_dma();
+    if (NS == 3 && kt + 2 < kt1) wait_all_but_newest(); else wait_dma();
     __syncthreads();
     if (more) read_frags(smem + nxt * S::LDS_ELEMS, 0, 0);
     cur = nxt;
