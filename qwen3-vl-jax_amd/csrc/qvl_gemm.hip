@@ -1215,10 +1215,12 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 //   288x256 on 12 waves (three per SIMD, 96x64 each): 64 row tiles cover 18432 tokens, so the
 //     N = 1024 / 3072 / 4096 GEMMs fill exactly 1 / 3 / 4 rounds of 256 CUs;
 //   256x256 on 8 waves (two per SIMD, 64x128 each): the least LDS traffic per MFMA;
-//   256x128 on 8 waves (64x64 each): half the work per tile, for balancing small grids;
+//   256x128 on 8 waves (64x64 each): half the work per tile, for balancing small grids (its
+//     three-stage ring keeps it fed on cold weights; with it the 8192-token qkv's 3 rounds of
+//     these beat 1.5 rounds of 256x256: 70 against 74 us);
 //   288x128 on 12 waves (96x32 each): fills the CUs where 288x256 tiles would cover only half
 //     of them (the merger's 4608 x 2048 output is exactly 256 such tiles).
-constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.36e6,
+constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.42e6,
                  kRate288x128 = 1.36e6;   // MACs/us/CU
 
 template <int EPI, bool LN>
@@ -1232,16 +1234,16 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
   const GemmPlan d = plan_gemm<288, 128>(p, cus, kRate288x128, f.split_mode);
   int pick = f.tile;
-  if (EPI == kEpiQkvRope && pick >= 3) pick = 2;     // 64-feature heads need TN % 64 == 0
+  if (EPI == kEpiQkvRope && pick == 4) pick = 3;     // 64-feature heads need TN % 64 == 0 (288x128: 32)
   if (pick == 0) {
-    const double cost[4] = {a.cost_us, b.cost_us, EPI == kEpiQkvRope ? 1e30 : c.cost_us,
-                            EPI == kEpiQkvRope ? 1e30 : d.cost_us};
+    const double cost[4] = {a.cost_us, b.cost_us, c.cost_us, EPI == kEpiQkvRope ? 1e30 : d.cost_us};
     pick = 1;
     for (int i = 1; i < 4; ++i)
       if (cost[i] < cost[pick - 1]) pick = i + 1;
   }
   if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI, LN>(p, a, stream);
   if constexpr (EPI == kEpiQkvRope) {
+    if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
     return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
   } else {
     if (pick == 2) return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
