@@ -610,7 +610,8 @@ def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
 @pytest.mark.parametrize("grids", [[(1, 48, 48)] * 8, [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
 def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     """The fused qkv+rotary GEMM writes bit-identical head-major Q/K/V^T (including the zeroed
-    padding rows [N, Np)) with 288x256 and 256x256 tiles; with the tail split within rel-L2 2e-3."""
+    padding rows [N, Np)) with 288x256, 256x256 and 256x128 tiles (the last with the three-stage
+    operand ring and one head per wave); with the tail split within rel-L2 2e-3."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
     N, D, H = m.n_tokens, 1024, 16
@@ -626,7 +627,8 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
     Np = -(-N // 64) * 64
     outs = {}
-    for plan in ["256x256:nosplit", "288x256:nosplit", "256x256:split", "288x256:split", None]:
+    for plan in ["256x256:nosplit", "288x256:nosplit", "256x128:nosplit", "256x256:split", "288x256:split",
+                 "256x128:split", None]:
         set_plan(lib, cp, plan)
         q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
         k, vt = q.clone(), q.clone()

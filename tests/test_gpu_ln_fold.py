@@ -186,13 +186,16 @@ def vt_positions(n):
     return (n & ~15) | (np.choose(quad, [0, 2, 1, 3]) << 2) | (n & 3)
 
 
-@pytest.mark.parametrize("hd,grids,plan", [(64, [(1, 48, 48)], 0), (64, [(1, 16, 16), (2, 10, 14)], 1),
-                                           (72, [(1, 32, 40)], 0)])
+@pytest.mark.parametrize("hd,grids,plan", [(64, [(1, 48, 48)], None), (64, [(1, 16, 16), (2, 10, 14)], (1, 1)),
+                                           (64, [(8, 32, 32)], (3, -1)), (64, [(1, 16, 16), (2, 10, 14)], (3, 1)),
+                                           (72, [(1, 32, 40)], None)])
 def test_qkv_rotary_ln_vs_reference(pkg, lib, hd, grids, plan):
     """qvl_dense_qkv_rotary_ln (norm1 folded into the fused qkv + rotary GEMM, the tower's path)
     against (a) the unfolded entries (qvl_layer_norm + qvl_dense_qkv_rotary) and (b) exact fp64
     LayerNorm + Dense + rotary + pre-scale, layouts undone; the per-position-table form equals the
-    per-token form bit for bit. plan 1 forces a tail split (head_dim 64)."""
+    per-token form bit for bit. plan (tile, split mode) pins a tile plan for every entry: (1, 1) a
+    288x256 tail split, (3, -1) / (3, 1) 256x128 tiles (three-stage ring, the position table in LDS
+    beside it; config 3's grid) without / with the split."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
     H = 16
@@ -224,7 +227,7 @@ def test_qkv_rotary_ln_vs_reference(pkg, lib, hd, grids, plan):
     outs = {}
     try:
         if plan:
-            cp.check(lib.qvl_set_gemm_plan(1, 1, 0))
+            cp.check(lib.qvl_set_gemm_plan(plan[0], plan[1], 0))
         parts = torch.from_numpy(host_parts(x)).to(DEV)
         for mode in ("unfolded", "folded", "folded_tab", "folded_parts"):
             if mode == "folded_tab" and hd != 64:
