@@ -226,8 +226,11 @@ def _split_list(pkg, cu, heads, hd, n_cus):
     return items, n_whole, base
 
 
-@pytest.mark.parametrize("cu,heads,hd,n_cus", [([0, 4096, 8192, 18432], 16, 64, 256),   # config 2: no split
+@pytest.mark.parametrize("cu,heads,hd,n_cus", [([0, 4096, 8192, 18432], 16, 64, 256),   # no split
                                                ([0, 4096, 8192, 18432], 16, 64, 280),   # 64-item tail, 8 parts
+                                               ([0] + [2304 * i for i in range(1, 9)], 16, 64, 256),   # config 2
+                                               ([0, 1024, 1984, 2240, 4544], 16, 64, 256),   # config 1
+                                               ([0] + [1024 * i for i in range(1, 9)], 16, 64, 256),   # config 3
                                                ([0, 7056], 16, 72, 256),                # config 4: 6 parts
                                                ([0, 1024, 2048, 6144], 16, 72, 256),    # 768 items, 768 slots
                                                ([0, 4096, 4100], 16, 72, 58),   # 1-tile items stay whole
@@ -266,6 +269,15 @@ def test_attention_worklist_split(pkg, cu, heads, hd, n_cus):
         n_kt = (key[1] - (key[0] & ~63) + 63) // 64
         bounds = [n_kt * p // npart for p in range(npart + 1)]
         assert bounds[0] == 0 and bounds[-1] == n_kt and min(np.diff(bounds)) >= 2
+    # every query row of every (segment, head) exactly once: a whole item's 128 rows, or those of a
+    # split item through its parts
+    count = {}
+    for it in list(real(whole)) + list(covered):
+        s0, s1, q0, h = (int(v) for v in it[:4])
+        for r in range(q0, min(s1, q0 + 128)):
+            count[(s0, s1, h & 0xFFF, r)] = count.get((s0, s1, h & 0xFFF, r), 0) + 1
+    want = {(s0, s1, h, r) for s0, s1 in zip(cu[:-1], cu[1:]) for h in range(heads) for r in range(s0, s1)}
+    assert set(count) == want and set(count.values()) == {1}
 
 
 def test_attention_worklist_split_checks(pkg):
