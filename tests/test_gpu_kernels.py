@@ -574,12 +574,14 @@ def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
 
 @pytest.mark.parametrize("epi", [0, 1, 2])
 @pytest.mark.parametrize("m,n,k", [(18432, 1024, 1024), (4600, 2048, 4096), (2304, 4096, 1024), (300, 192, 128),
-                                   (18000, 1152, 4352)])
+                                   (18000, 1152, 4352), (300, 192, 64), (1000, 640, 192)])
 def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
     """Every tile shape (288x256 / 256x256 / 256x128 / 288x128) gives bit-identical results without the
     tail split (same K order per output); with the split (fp32 partials summed by the reduce
     kernel) within rel-L2 2e-3 of them; all within rel-L2 4e-3 of torch fp32 on the same bf16
-    operands. Shapes include M not a multiple of any tile height and N not a multiple of 256."""
+    operands. Shapes include M not a multiple of any tile height and N not a multiple of 256, and
+    K of 1, 2 and 3 k-steps (the three-stage ring of the 128-column tiles with fewer k-steps than
+    stages; split units of one k-step)."""
     cp = pkg.capi
     g = torch.Generator(device="cpu").manual_seed(m + n + k + epi)
     x = torch.randn((m, k), generator=g).to(DEV).to(torch.bfloat16)
