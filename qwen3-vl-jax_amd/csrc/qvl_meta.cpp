@@ -104,8 +104,25 @@ int qvl_vision_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int
   int64_t off = 0;
   std::vector<double> hs, ws;
   std::vector<int32_t> hf, wf;
+  std::vector<std::array<int64_t, 4>> done;   // (t, h, w, first token) of the grids computed so far
   for (int64_t i = 0; i < n_grids; ++i) {
     const int t = grid[3 * i], h = grid[3 * i + 1], w = grid[3 * i + 2];
+    const int64_t n_tok = (int64_t)t * h * w;
+    // A grid equal to an earlier one has the same per-token metadata: copy it (a batch of
+    // same-size images builds one image's worth).
+    int64_t src = -1;
+    for (const auto& d : done)
+      if (d[0] == t && d[1] == h && d[2] == w) { src = d[3]; break; }
+    if (src >= 0) {
+      if (pos_hw) memcpy(pos_hw + 2 * off, pos_hw + 2 * src, (size_t)n_tok * 2 * sizeof(int32_t));
+      for (int j = 0; j < 4; ++j) {
+        if (tap_idx) memcpy(tap_idx + j * N + off, tap_idx + j * N + src, (size_t)n_tok * sizeof(int32_t));
+        if (tap_w) memcpy(tap_w + j * N + off, tap_w + j * N + src, (size_t)n_tok * sizeof(float));
+      }
+      off += n_tok;
+      continue;
+    }
+    done.push_back({t, h, w, off});
     const int bw = w / merge;
     // np.linspace(0, num_grid-1, n, dtype=float32): float64 k*step, last = stop, cast to f32.
     auto linspace = [&](int n, std::vector<double>& val, std::vector<int32_t>& fl) {
@@ -217,9 +234,9 @@ int qvl_window_metadata(const int32_t* grid, int64_t n_grids, int32_t merge, int
   return QVL_OK;
 }
 
-int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, int32_t* items, int64_t capacity,
-                           int64_t* n_items) {
-  if (!cu || !n_items) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens / n_items is NULL");
+// The plain work list of qvl_attention_worklist, built into `out` (4 ints per item).
+static int build_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, std::vector<int32_t>& out) {
+  if (!cu) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens is NULL");
   if (num_heads <= 0) return set_error(QVL_ERR_INVALID_ARG, "num_heads=%d", num_heads);
   std::vector<std::pair<int32_t, int32_t>> segs;
   for (int64_t i = 0; i < n_seg; ++i) {
@@ -248,17 +265,28 @@ int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, 
   size_t longest = 0;
   for (auto& q : queue) longest = std::max(longest, q.size());
   const int64_t n = (int64_t)longest * kAttnQueues;
-  *n_items = n;
-  if (!items) return QVL_OK;
-  if (capacity < n) return set_error(QVL_ERR_INVALID_ARG, "worklist capacity %lld < %lld", (long long)capacity, (long long)n);
   // Item k goes to the workgroup k, which the dispatcher places on XCD k % 8: queue k % 8,
   // position k / 8. Short queues are padded with empty items (start == end).
+  out.assign(4 * (size_t)n, 0);
   for (int64_t k = 0; k < n; ++k) {
     const auto& q = queue[k % kAttnQueues];
     const size_t pos = (size_t)(k / kAttnQueues);
-    const std::array<int32_t, 4> it = pos < q.size() ? q[pos] : std::array<int32_t, 4>{0, 0, 0, 0};
-    for (int c = 0; c < 4; ++c) items[4 * k + c] = it[c];
+    if (pos < q.size())
+      for (int c = 0; c < 4; ++c) out[4 * k + c] = q[pos][c];
   }
+  return QVL_OK;
+}
+
+int qvl_attention_worklist(const int32_t* cu, int64_t n_seg, int32_t num_heads, int32_t* items, int64_t capacity,
+                           int64_t* n_items) {
+  if (!cu || !n_items) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens / n_items is NULL");
+  std::vector<int32_t> list;
+  QVL_TRY_RC(build_worklist(cu, n_seg, num_heads, list));
+  const int64_t n = (int64_t)list.size() / 4;
+  *n_items = n;
+  if (!items) return QVL_OK;
+  if (capacity < n) return set_error(QVL_ERR_INVALID_ARG, "worklist capacity %lld < %lld", (long long)capacity, (long long)n);
+  std::copy(list.begin(), list.end(), items);
   return QVL_OK;
 }
 
@@ -270,10 +298,10 @@ int qvl_attention_worklist_split(const int32_t* cu, int64_t n_seg, int32_t num_h
     return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: head_dim=%d (supported: 64, 72, 80)", head_dim);
   if (n_cus <= 0) return set_error(QVL_ERR_INVALID_ARG, "worklist_split: n_cus=%d", n_cus);
   if (num_heads > kAttnHeadMask) return set_error(QVL_ERR_UNSUPPORTED, "worklist_split: num_heads=%d", num_heads);
-  int64_t n = 0;
-  QVL_TRY_RC(qvl_attention_worklist(cu, n_seg, num_heads, nullptr, 0, &n));
-  std::vector<int32_t> base(4 * (size_t)std::max<int64_t>(n, 1));
-  QVL_TRY_RC(qvl_attention_worklist(cu, n_seg, num_heads, base.data(), n, &n));
+  if (!cu) return set_error(QVL_ERR_INVALID_ARG, "cu_seqlens is NULL");
+  std::vector<int32_t> base;
+  QVL_TRY_RC(build_worklist(cu, n_seg, num_heads, base));
+  const int64_t n = (int64_t)base.size() / 4;
   // The last round of workgroup slots: the kernels run 4 (head_dim 64) or 3 (72, 80) workgroups per
   // CU. When that round's items leave at least half of the CUs idle, each is split along its key
   // tiles into up to 8 parts (at least 2 tiles each) so that the parts fill the slots. A round

@@ -264,13 +264,20 @@ class GridMetadata:
     n_positions: int = 0          # 1 + the largest rotary (h, w) id: max over grids of max(h, w)
 
 
+def _worklist_capacity(cu: np.ndarray, num_heads: int, extra: int = 0) -> int:
+    """An upper bound on a work list's length, so that one call fills it: the padded list holds
+    8 queues of at most every (segment, head) group's query tiles each, plus `extra` parts."""
+    lens = np.diff(cu.astype(np.int64))
+    tiles = int(((np.maximum(lens, 0) + 127) // 128).sum()) * num_heads
+    return 8 * max(tiles, 1) + extra
+
+
 def _worklist(lib, cu: np.ndarray, num_heads: int) -> np.ndarray:
     cu = np.ascontiguousarray(cu, np.int32)
     n = C.c_int64()
-    capi.check(lib.qvl_attention_worklist(_i32p(cu), len(cu) - 1, num_heads, None, 0, C.byref(n)),
-               "qvl_attention_worklist")
-    tiles = np.zeros((max(n.value, 1), 4), np.int32)
-    capi.check(lib.qvl_attention_worklist(_i32p(cu), len(cu) - 1, num_heads, _i32p(tiles), n.value, C.byref(n)),
+    cap = _worklist_capacity(cu, num_heads)
+    tiles = np.empty((cap, 4), np.int32)          # the first n items are written
+    capi.check(lib.qvl_attention_worklist(_i32p(cu), len(cu) - 1, num_heads, _i32p(tiles), cap, C.byref(n)),
                "qvl_attention_worklist")
     return tiles[: n.value]
 
@@ -281,11 +288,10 @@ def attention_worklist_split(cu: np.ndarray, num_heads: int, head_dim: int, n_cu
     lib = capi.load()
     cu = np.ascontiguousarray(cu, np.int32)
     n, nw = C.c_int64(), C.c_int64()
-    capi.check(lib.qvl_attention_worklist_split(_i32p(cu), len(cu) - 1, num_heads, head_dim, n_cus, None, 0,
-                                                C.byref(n), C.byref(nw)), "qvl_attention_worklist_split")
-    items = np.zeros((max(n.value, 1), 4), np.int32)
+    cap = _worklist_capacity(cu, num_heads, extra=4 * max(int(n_cus), 0))   # parts: at most one per slot
+    items = np.empty((cap, 4), np.int32)          # the first n items are written
     capi.check(lib.qvl_attention_worklist_split(_i32p(cu), len(cu) - 1, num_heads, head_dim, n_cus, _i32p(items),
-                                                n.value, C.byref(n), C.byref(nw)), "qvl_attention_worklist_split")
+                                                cap, C.byref(n), C.byref(nw)), "qvl_attention_worklist_split")
     return items[: n.value], nw.value
 
 
@@ -316,11 +322,13 @@ def grid_metadata(grid_thw, merge: int = 2, num_position_embeddings: Optional[in
     nt, ns = C.c_int64(), C.c_int64()
     capi.check(lib.qvl_grid_counts(_i32p(g), g.shape[0], merge, C.byref(nt), C.byref(ns)), "qvl_grid_counts")
     N, S = nt.value, ns.value
-    cu = np.zeros(S + 1, np.int32)
-    pos = np.zeros((N, 2), np.int32)
-    idx = np.zeros((4, N), np.int32)
-    w = np.zeros((4, N), np.float32)
     npos = int(num_position_embeddings or 0)
+    # (qvl_vision_metadata writes every entry of cu and pos, and of the taps when the spec has a
+    # pos-embed table; without one they stay zeros, unused)
+    cu = np.empty(S + 1, np.int32)
+    pos = np.empty((N, 2), np.int32)
+    idx = np.empty((4, N), np.int32) if npos else np.zeros((4, N), np.int32)
+    w = np.empty((4, N), np.float32) if npos else np.zeros((4, N), np.float32)
     capi.check(lib.qvl_vision_metadata(_i32p(g), g.shape[0], merge, npos, dtype, _i32p(cu), _i32p(pos),
                                        _i32p(idx) if npos else None, _f32p(w) if npos else None),
                "qvl_vision_metadata")
