@@ -134,8 +134,10 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
  * GEMMs inside qvl_encode_vision) launched afterwards FROM THE CALLING THREAD ONLY (thread-local;
  * other threads keep the cost model's choice). For tests and tuning sweeps, not needed by callers:
  *   tile       0 = cost model (default), 1 = 288x256, 2 = 256x256, 3 = 256x128, 4 = 288x128
- *                (the head_dim-64 rotary qkv epilogue takes 1-3 and maps 4 to 3; the
- *                head_dim-72 one always runs 256x288 tiles);
+ *                (the head_dim-64 rotary qkv epilogue takes 1-3 and maps 4 to 3; for the
+ *                head_dim-72 one, 0 = whole rounds of 256x288 tiles and the rest in 128x288
+ *                tiles where that fits one round, 1 = 256x288 tiles only, 2 = that row split
+ *                wherever there are two 256-row tiles);
  *   split_mode 0 = cost model decides the tail split-K, 1 = force it, -1 = forbid it;
  *   group_n    column tiles per panel of the tile order, 0 = default (4).
  * (0, 0, 0) restores the defaults. No counterpart in the reference (it has no tile plans). */

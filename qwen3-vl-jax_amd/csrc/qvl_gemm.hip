@@ -787,8 +787,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(GemmParams p
     kt1 = (s + 1) * KT / p.split;
   }
   int tm, tn;
-  tile_coords(tile, (max(p.M, p.Np) + BM - 1) / BM, tiles_n, p.group_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  tile_coords(tile, ((p.row1 ? p.row1 : max(p.M, p.Np)) - p.row0 + BM - 1) / BM, tiles_n, p.group_n, tm, tn);
+  const int m0 = p.row0 + tm * BM, n0 = tn * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1137,13 +1137,14 @@ static double round_fraction(int units, int cus) { return std::max((double)units
 
 template <int BM, int BN>
 static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_cu, int split_mode) {
-  const int rows = std::max(p.M, p.Np);      // the rotary epilogue also zero-fills [M, Np)
+  // (the rotary epilogue also zero-fills [M, Np))
+  const int rows = (p.row1 ? p.row1 : std::max(p.M, p.Np)) - p.row0;
   const int tiles = ((rows + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   const int KT = p.K / kBK;
   const double tile_us = (double)BM * BN * p.K / macs_per_us_per_cu;
   const int tail = tiles % cus;
   GemmPlan g{tiles, 1, 0, (tiles / cus) * tile_us + (tail ? round_fraction(tail, cus) * tile_us : 0.0)};
-  if (tail == 0 || !p.part || split_mode < 0) return g;
+  if (tail == 0 || !p.part || split_mode < 0 || p.row0 || p.row1) return g;
   int split = std::min(std::min(8, KT), cus / tail);
   while (split >= 2 && (int64_t)tail * split * BM * BN > p.part_elems) --split;   // what the workspace holds
   if (split < 2) return g;
@@ -1261,16 +1262,46 @@ int gemm_set_plan(int tile, int split_mode, int group_n) {
   return QVL_OK;
 }
 
-// head_dim-72 qkv GEMM: 256 x 288 tiles (4 heads each, 12 waves of 64 x 96). The last partial round
-// is split along K only when a plan forces it (gemm_splitk_reduce_rope72_kernel applies the
-// epilogue): at config 4 (336 tiles on 256 CUs) the split ran its GEMM in 76 us and the reduction of
-// the 47 MB of fp32 partials in 16 us, against 91-93 us unsplit (MI355X), so it is not the default.
+// head_dim-72 qkv GEMM: 256 x 288 tiles (4 heads each, 12 waves of 64 x 96). Where those tiles leave
+// a last round at most half full and the rows past the whole rounds fit one round of 128 x 288 tiles
+// (12 waves of 32 x 96), the rows run in two launches: whole rounds of 256-row tiles, then the rest
+// in 128-row tiles, so the last round does half a tile's work per CU (config 4: 336 tiles on 256
+// CUs become 252 + 168 half tiles; the outputs are the same bits, as the k order is). The last
+// partial round can instead be split along K when a plan forces it
+// (gemm_splitk_reduce_rope72_kernel applies the epilogue): at config 4 the split ran its GEMM in 76
+// us and the reduction of the 47 MB of fp32 partials in 16 us, against 91-93 us unsplit (MI355X).
+// Plan override (qvl_set_gemm_plan's tile): 1 = one launch of 256 x 288 tiles, 2 = the row split
+// wherever there are two row tiles (the 128-row launch alone when no whole round exists).
 constexpr double kRate256x288 = 1.50e6;
 
+template <bool LN>
+static int launch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
+  const int cus = gemm_device_cus();
+  const int rows = std::max(p.M, p.Np), tiles_n = (p.N + 287) / 288;
+  const int row_tiles = (rows + 255) / 256, tiles = row_tiles * tiles_n, tail = tiles % cus;
+  const int whole_rows = (tiles / cus) * cus / tiles_n * 256;          // rows in whole rounds
+  const int half_tiles = (rows - whole_rows + 127) / 128 * tiles_n;    // the rest in 128-row tiles
+  const bool row_split = t_plan.split_mode != 1 && t_plan.tile != 1 && row_tiles >= 2 &&
+                         (t_plan.tile == 2 || (tail && 2 * tail <= cus && half_tiles <= cus));
+  if (!row_split) {
+    const GemmPlan g = plan_gemm<256, 288>(p, cus, kRate256x288, t_plan.split_mode == 1 ? 1 : -1);
+    return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, LN>(p, g, stream);
+  }
+  GemmParams a = p, b = p;
+  a.row0 = 0;
+  a.row1 = whole_rows;
+  b.row0 = whole_rows;
+  b.row1 = rows;
+  if (whole_rows > 0) {
+    const int rc = launch_gemm<256, 288, 4, 3, kEpiQkvRope72, LN>(a, plan_gemm<256, 288>(a, cus, kRate256x288, -1), stream);
+    if (rc) return rc;
+  }
+  return launch_gemm<128, 288, 4, 3, kEpiQkvRope72, LN>(b, plan_gemm<128, 288>(b, cus, kRate256x288, -1), stream);
+}
+
 static int dispatch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
-  const GemmPlan g = plan_gemm<256, 288>(p, gemm_device_cus(), kRate256x288, t_plan.split_mode == 1 ? 1 : -1);
-  if (p.ln_stats || p.ln_part) return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, true>(p, g, stream);
-  return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, false>(p, g, stream);
+  if (p.ln_stats || p.ln_part) return launch_qkv_rope72<true>(p, stream);
+  return launch_qkv_rope72<false>(p, stream);
 }
 
 // A folded LayerNorm (p.ln_stats or p.ln_part) selects the kernels instantiated with the fold (bias, GELU and

@@ -38,6 +38,10 @@ struct GemmParams {
   int64_t part_elems;
   int full_tiles, split;
   int group_n;                   // tile order: panels of group_n column tiles (set by the launcher)
+  // Rows this launch covers: [row0, row1), row1 = 0 meaning max(M, Np) (zero-initialised params
+  // cover every row). The head_dim-72 qkv plan runs its rows in two launches of different tile
+  // heights; the outputs stay indexed by absolute row (no split-K tail with a row range).
+  int row0, row1;
   // LayerNorm folded into this Dense (ln_stats != NULL): x holds the un-normalised rows, w the
   // folded kernel W' = bf16(gamma W), ln_stats[m] = (mean, rstd) of row m and ln_cd[n] = (c, d);
   // the accumulator becomes rstd * acc - rstd * mean * c + d before the epilogue.

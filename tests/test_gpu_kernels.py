@@ -658,6 +658,73 @@ def vt_positions(n):
 
 
 @pytest.mark.parametrize("fold", [False, True])
+@pytest.mark.parametrize("grids", [[(1, 84, 84)], [(1, 50, 110)], [(1, 28, 26)], [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
+def test_qkv_rotary72_row_split(pkg, lib, grids, fold):
+    """The head_dim-72 qkv + rotary GEMM's row split (whole rounds of 256 x 288 tiles, the remaining
+    rows as 128 x 288 tiles in a second launch: the cost rule's choice at config 4's 7056 tokens
+    and at 5500, forced by plan 2 elsewhere, where the 128-row launch may run alone) against one
+    launch of 256 x 288 tiles (plan 1): Q, K and V^T bit-identical (the k order is the same), every
+    element written (the buffers start as NaN), padding rows and dims 72..87 zero; plain and with
+    norm1 folded from row partials (the tower's path)."""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids)
+    H, hd = 16, 72
+    N, D = m.n_tokens, H * hd
+    Np = -(-N // 64) * 64
+    rng = np.random.default_rng(N + 720)
+    x_h = vt.bf16_round((rng.standard_normal((N, D)) + 0.3).astype(np.float32))
+    w_h = (rng.standard_normal((D, 3 * D)) * 0.03).astype(np.float32)
+    b_h = vt.bf16_round((rng.standard_normal(3 * D) * 0.1).astype(np.float32))
+    x, w, bias = bf(x_h), pack(lib, cp, w_h), torch.from_numpy(b_h).to(DEV)
+    pos = torch.from_numpy(m.pos_hw).to(DEV)
+    tab = torch.empty((m.n_positions, hd // 4), dtype=torch.int32, device=DEV)
+    cp.check(lib.qvl_rotary_pos_table(stream(), hd, 10000.0, m.n_positions, tab.data_ptr()))
+    nb = C.c_size_t()
+    cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    if fold:
+        g = vt.bf16_round((1 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+        b = vt.bf16_round((0.1 * rng.standard_normal(D)).astype(np.float32))
+        wf = torch.empty_like(w)
+        cd = torch.empty((w.shape[0], 2), dtype=torch.float32, device=DEV)
+        cp.check(lib.qvl_fold_ln_weight(stream(), cp.QVL_DTYPE_BF16, w.data_ptr(), D, w.shape[0],
+                                        torch.from_numpy(g).to(DEV).data_ptr(), torch.from_numpy(b).to(DEV).data_ptr(),
+                                        wf.data_ptr(), cd.data_ptr()))
+        xg = x_h.astype(np.float64).reshape(N, D // 128, 128)
+        sg = xg.sum(-1)
+        parts = torch.from_numpy(np.stack([sg, ((xg - sg[..., None] / 128) ** 2).sum(-1)], -1).astype(np.float32)).to(DEV)
+    outs = {}
+    for tile in (1, 0, 2):
+        q = torch.full((H, Np, 88), float("nan"), dtype=torch.bfloat16, device=DEV)
+        k = q.clone()
+        vtm = torch.full((H, hd, Np), float("nan"), dtype=torch.bfloat16, device=DEV)
+        try:
+            cp.check(lib.qvl_set_gemm_plan(tile, -1, 0))
+            if fold:
+                cp.check(lib.qvl_dense_qkv_rotary_ln_parts(
+                    stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, wf.data_ptr(), cd.data_ptr(), parts.data_ptr(),
+                    D // 128, 1e-6, bias.data_ptr(), None, pos.data_ptr(), tab.data_ptr(), m.n_positions, q.data_ptr(),
+                    k.data_ptr(), vtm.data_ptr(), N, D, H, ws.data_ptr(), nb.value))
+            else:
+                cp.check(lib.qvl_dense_qkv_rotary_pos(stream(), cp.QVL_DTYPE_BF16, x.data_ptr(), D, w.data_ptr(),
+                                                      bias.data_ptr(), pos.data_ptr(), tab.data_ptr(), m.n_positions,
+                                                      q.data_ptr(), k.data_ptr(), vtm.data_ptr(), N, D, H,
+                                                      ws.data_ptr(), nb.value))
+        finally:
+            cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
+        torch.cuda.synchronize()
+        outs[tile] = (to_np(q), to_np(k), to_np(vtm))
+    for tile in (0, 2):
+        for name, a, b_ in zip("qkv", outs[tile], outs[1]):
+            assert np.isfinite(a).all(), (tile, name)
+            np.testing.assert_array_equal(a, b_, err_msg=f"plan {tile} {name}")
+    q, k, vtm = outs[2]
+    assert not q[:, N:].any() and not k[:, N:].any() and not q[:, :, hd:].any() and not k[:, :, hd:].any()
+    pad = np.arange(N, Np)
+    assert not vtm[:, :, pad[vt_positions(pad) >= N]].any()   # positions holding no token
+
+
+@pytest.mark.parametrize("fold", [False, True])
 @pytest.mark.parametrize("grids", [[(1, 84, 84)], [(1, 16, 16), (2, 10, 14), (1, 6, 8)]])
 def test_qkv_rotary72_split_tail(pkg, lib, grids, fold):
     """The head_dim-72 qkv + rotary GEMM with its last partial round of 256 x 288 tiles split along K
