@@ -1160,9 +1160,10 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 }
 
 // Tile-plan override of the calling thread (qvl_set_gemm_plan): tile 0 = the cost model's
-// choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128; split_mode -1 forbids, 1 forces, 0 lets
-// the cost model decide the tail split; group_n 0 = the default panel width. Thread-local, so a
-// test pinning a plan on one thread does not change another thread's launches.
+// choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128, 5 = the row split (whole rounds of 288x256,
+// the rest 256x128); split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
+// group_n 0 = the default panel width. Thread-local, so a test pinning a plan on one thread does
+// not change another thread's launches.
 struct ForcedPlan { int tile = 0, split_mode = 0, group_n = 0; };
 static thread_local ForcedPlan t_plan;
 
@@ -1234,13 +1235,32 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);
   const GemmPlan d = plan_gemm<288, 128>(p, cus, kRate288x128, f.split_mode);
+  // Row split: the rows that fill whole rounds of 288x256 tiles in one launch, the rest in 256x128
+  // tiles in a second launch that fits one round (GemmParams::row0 / row1; no split-K tail). The
+  // k order of every output is that of the other plans, so the outputs are the same bits.
+  const int rows = std::max(p.M, p.Np), tiles_n_a = (p.N + 255) / 256;
+  const int whole_rows = (((rows + 287) / 288) * tiles_n_a / cus) * cus / tiles_n_a * 288;
+  GemmParams ra = p, rb = p;
+  ra.row1 = whole_rows;
+  rb.row0 = whole_rows;
+  rb.row1 = rows;
+  const bool can_split = whole_rows > 0 && whole_rows < rows && !p.row0 && !p.row1;
+  const GemmPlan r_a = plan_gemm<288, 256>(ra, cus, kRate288x256, -1);
+  const GemmPlan r_b = plan_gemm<256, 128>(rb, cus, kRate256x128, -1);
+  const double r_cost = can_split && r_b.full <= cus ? r_a.cost_us + r_b.cost_us : 1e30;
   int pick = f.tile;
   if (EPI == kEpiQkvRope && pick == 4) pick = 3;     // 64-feature heads need TN % 64 == 0 (288x128: 32)
+  if (pick == 5 && !can_split) pick = 1;
   if (pick == 0) {
-    const double cost[4] = {a.cost_us, b.cost_us, c.cost_us, EPI == kEpiQkvRope ? 1e30 : d.cost_us};
+    const double cost[5] = {a.cost_us, b.cost_us, c.cost_us, EPI == kEpiQkvRope ? 1e30 : d.cost_us, r_cost};
     pick = 1;
-    for (int i = 1; i < 4; ++i)
+    for (int i = 1; i < 5; ++i)
       if (cost[i] < cost[pick - 1]) pick = i + 1;
+  }
+  if (pick == 5) {
+    const int rc = launch_gemm<288, 256, 3, 4, EPI, LN>(ra, r_a, stream);
+    if (rc) return rc;
+    return launch_gemm<256, 128, 4, 2, EPI, LN>(rb, r_b, stream);
   }
   if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI, LN>(p, a, stream);
   if constexpr (EPI == kEpiQkvRope) {
@@ -1254,7 +1274,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
 }
 
 int gemm_set_plan(int tile, int split_mode, int group_n) {
-  if (tile < 0 || tile > 4 || split_mode < -1 || split_mode > 1 || group_n < 0)
+  if (tile < 0 || tile > 5 || split_mode < -1 || split_mode > 1 || group_n < 0)
     return set_error(QVL_ERR_INVALID_ARG, "gemm plan: tile=%d split_mode=%d group_n=%d", tile, split_mode, group_n);
   t_plan.tile = tile;
   t_plan.split_mode = split_mode;
