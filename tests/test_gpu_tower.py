@@ -431,3 +431,45 @@ def test_mixed_block_folds_position_table(pkg):
         tok, ds = tower(px, g)
         assert rel_l2(to_np(tok), ref.tokens) <= TOL, mixed
         assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL, mixed
+
+
+def test_metadata_upload_streams(pkg, params2b):
+    """The per-grid device metadata, built and uploaded once per grid and cached: a forward on a side
+    stream that builds it, a forward on the default stream that hits the cache entry a side stream
+    built, and forwards that rebuild it every call for two grids in turn with no synchronisation in
+    between all give the outputs of a forward with the metadata built on the default stream, bit
+    for bit."""
+    s, _ = specs(pkg, depth=2, ds=(0, 1))
+    tower = pkg.Qwen3VisionTransformer(s, dtype="bfloat16").bind(params2b)
+    cases = [np.array([(1, 8, 8), (2, 4, 6)], np.int32), np.array([(1, 12, 10)], np.int32)]
+    pxs = [torch.from_numpy(pixels(g.tolist(), 40 + i)).cuda() for i, g in enumerate(cases)]
+    ref = []
+    for g, px in zip(cases, pxs):
+        tower.clear_metadata_cache()
+        tok, ds = tower(px, g)
+        ref.append([to_np(tok)] + [to_np(d) for d in ds])
+    torch.cuda.synchronize()
+
+    def same(got, want):
+        for a, b in zip([to_np(got[0])] + [to_np(d) for d in got[1]], want):
+            np.testing.assert_array_equal(a, b)
+
+    side = torch.cuda.Stream()
+    tower.clear_metadata_cache()
+    with torch.cuda.stream(side):
+        out = tower(pxs[0], cases[0])
+    side.synchronize()
+    same(out, ref[0])
+    tower.clear_metadata_cache()
+    with torch.cuda.stream(side):
+        tower.metadata(cases[1])                 # upload queued on the side stream, not waited for
+    out = tower(pxs[1], cases[1])                # default stream: a cache hit from another stream
+    torch.cuda.synchronize()
+    same(out, ref[1])
+    outs = []
+    for i in range(6):
+        tower.clear_metadata_cache()
+        outs.append(tower(pxs[i % 2], cases[i % 2]))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        same(o, ref[i % 2])
