@@ -1219,7 +1219,8 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 //   256x256 on 8 waves (two per SIMD, 64x128 each): the least LDS traffic per MFMA;
 //   256x128 on 8 waves (64x64 each): half the work per tile, for balancing small grids (its
 //     three-stage ring keeps it fed on cold weights; with it the 8192-token qkv's 3 rounds of
-//     these beat 1.5 rounds of 256x256: 70 against 74 us);
+//     these beat 1.5 rounds of 256x256: 70 against 74 us; the row split below, one round of
+//     288x256 and 216 tiles of these, is what that GEMM now runs);
 //   288x128 on 12 waves (96x32 each): fills the CUs where 288x256 tiles would cover only half
 //     of them (the merger's 4608 x 2048 output is exactly 256 such tiles).
 constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.42e6,
