@@ -119,10 +119,12 @@ int qvl_dense(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, in
               const void* d_w, const float* d_bias, const void* d_residual, int64_t ldr,
               void* d_y, int64_t ldc, int64_t m, int64_t n, int64_t k);
 
-/* qvl_dense with a workspace for tail split-K: when the tiles do not fill whole rounds of the
- * GPU's compute units, the last round's tiles are split along K into fp32 partials in
- * `d_workspace` and summed by a second kernel before the epilogue (same results up to fp32
- * summation order). Without enough workspace it behaves exactly like qvl_dense.
+/* qvl_dense with a workspace for split-K: bf16, when the tiles do not fill whole rounds of the
+ * GPU's compute units, the last round's tiles are split along K; fp32, when the 128 x 128 tiles
+ * fill at most half of the workgroup slots (two per compute unit), every tile is split along K
+ * into up to 8 parts. The parts' fp32 partials go to `d_workspace` and a second kernel sums them
+ * (in part order) before the epilogue: same results up to fp32 summation order. Without enough
+ * workspace it behaves exactly like qvl_dense.
  * qvl_dense_workspace_size gives the bytes that always suffice on the current device. */
 int qvl_dense_workspace_size(size_t* bytes);
 int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x, int64_t lda,

@@ -5,6 +5,8 @@
 // rotary + head-major relayout and weight packing are the fp32 counterparts of the bf16 kernels.
 #include <math.h>
 
+#include <algorithm>
+
 #include "qvl_kernels.h"
 
 namespace qvl {
@@ -31,7 +33,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32Params p) {
   __shared__ __attribute__((aligned(16))) float sm[2][2][kF32Tile * kF32BK];   // [stage][x | w] 64 KB
   const int tiles_n = (p.N + kF32Tile - 1) / kF32Tile;
   const int tiles = ((p.M + kF32Tile - 1) / kF32Tile) * tiles_n;
-  const int tile = xcd_remap(blockIdx.x, tiles);
+  // split-K: the units of one K part are consecutive, so one XCD's units share operand rows
+  const int unit = xcd_remap(blockIdx.x, tiles * p.split);
+  const int tile = unit % tiles, part_i = unit / tiles;
   const int m0 = (tile / tiles_n) * kF32Tile, n0 = (tile % tiles_n) * kF32Tile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -66,12 +70,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32Params p) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
 
-  const int KT = p.Kp / kF32BK;
-  gload(0);
+  const int KT_all = p.Kp / kF32BK;
+  const int kt0 = part_i * KT_all / p.split, KT = (part_i + 1) * KT_all / p.split;
+  gload(kt0);
   sstore(0);
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
+  for (int kt = kt0; kt < KT; ++kt) {
+    const int cur = (kt - kt0) & 1;
     if (kt + 1 < KT) gload(kt + 1);
     f32x4 wf[2][4], xf[2][4];
 #pragma unroll
@@ -97,7 +102,25 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32Params p) {
   }
 
   // Epilogue: block (a, b), register r: feature n0 + wn*64 + 32a + 8(r/4) + 4hh + r%4,
-  // token m0 + wm*64 + 32b + l32.
+  // token m0 + wm*64 + 32b + l32. A K part stores its raw sums instead.
+  if (p.split > 1) {
+    const int64_t npad = (int64_t)tiles_n * kF32Tile;
+    float* dst = p.part + (int64_t)part_i * p.M * npad;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int m = m0 + wm * 64 + b * 32 + l32;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * 64 + a * 32 + 8 * g + 4 * hh;
+          *reinterpret_cast<f32x4*>(dst + (int64_t)m * npad + n) =
+              f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -121,18 +144,60 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32Params p) {
     }
 }
 
-int gemm_f32(const GemmF32Params& p, int epi, hipStream_t stream) {
-  const int tiles = ((p.M + kF32Tile - 1) / kF32Tile) * ((p.N + kF32Tile - 1) / kF32Tile);
+// Sums the K parts of a split fp32 GEMM in part order and applies the epilogue, one thread per 4
+// consecutive outputs: y = epi(sum_s part[s] + bias).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_f32_reduce_kernel(GemmF32Params p, int64_t npad) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x, quads = (int64_t)p.M * (p.N / 4);
+  if (q >= quads) return;
+  const int m = (int)(q / (p.N / 4)), n = (int)(q % (p.N / 4)) * 4;
+  const float* src = p.part + (int64_t)m * npad + n;
+  const int64_t stride = (int64_t)p.M * npad;
+  f32x4 v = *reinterpret_cast<const f32x4*>(src);
+  for (int s = 1; s < p.split; ++s) v += *reinterpret_cast<const f32x4*>(src + s * stride);
+  const f32x4 bv = *reinterpret_cast<const f32x4*>(p.bias + n);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] += bv[e];
+    if constexpr (EPI == kEpiBiasGelu) v[e] = gelu_tanh(v[e]);
+  }
+  if constexpr (EPI == kEpiBiasResidual) v += *reinterpret_cast<const f32x4*>(p.res + (int64_t)m * p.ldr + n);
+  *reinterpret_cast<f32x4*>(p.y + (int64_t)m * p.ldc + n) = v;
+}
+
+// Plan: one 128 x 128 tile per workgroup, two workgroups per CU (64 KB of LDS each). Where the tiles
+// fill at most half of those slots and a workspace holds the partials, K is split into up to 8
+// parts (each at least 4 k-steps of 32) so the units fill about one round of slots.
+int gemm_f32(GemmF32Params p, int epi, hipStream_t stream) {
+  const int tiles_n = (p.N + kF32Tile - 1) / kF32Tile;
+  const int tiles = ((p.M + kF32Tile - 1) / kF32Tile) * tiles_n;
   if (tiles == 0) return QVL_OK;
+  const int slots = 2 * gemm_device_cus();
+  const int64_t npad = (int64_t)tiles_n * kF32Tile;
+  int split = 1;
+  if (p.part && 2 * tiles <= slots) {
+    split = std::min(std::min(8, slots / tiles), p.Kp / kF32BK / 4);
+    while (split > 1 && (int64_t)split * p.M * npad > p.part_elems) --split;
+  }
+  p.split = std::max(split, 1);
+  const int grid = tiles * p.split;
   switch (epi) {
-    case kEpiBias: hipLaunchKernelGGL(gemm_f32_kernel<kEpiBias>, dim3(tiles), dim3(256), 0, stream, p); break;
-    case kEpiBiasGelu: hipLaunchKernelGGL(gemm_f32_kernel<kEpiBiasGelu>, dim3(tiles), dim3(256), 0, stream, p); break;
+    case kEpiBias: hipLaunchKernelGGL(gemm_f32_kernel<kEpiBias>, dim3(grid), dim3(256), 0, stream, p); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL(gemm_f32_kernel<kEpiBiasGelu>, dim3(grid), dim3(256), 0, stream, p); break;
     case kEpiBiasResidual:
-      hipLaunchKernelGGL(gemm_f32_kernel<kEpiBiasResidual>, dim3(tiles), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(gemm_f32_kernel<kEpiBiasResidual>, dim3(grid), dim3(256), 0, stream, p);
       break;
     default: return set_error(QVL_ERR_INVALID_ARG, "gemm_f32: epilogue %d", epi);
   }
-  return check_launch("gemm_f32");
+  int rc = check_launch("gemm_f32");
+  if (rc || p.split == 1) return rc;
+  const int64_t blocks = ((int64_t)p.M * (p.N / 4) + 255) / 256;
+  switch (epi) {
+    case kEpiBias: hipLaunchKernelGGL(gemm_f32_reduce_kernel<kEpiBias>, dim3((unsigned)blocks), dim3(256), 0, stream, p, npad); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL(gemm_f32_reduce_kernel<kEpiBiasGelu>, dim3((unsigned)blocks), dim3(256), 0, stream, p, npad); break;
+    default: hipLaunchKernelGGL(gemm_f32_reduce_kernel<kEpiBiasResidual>, dim3((unsigned)blocks), dim3(256), 0, stream, p, npad); break;
+  }
+  return check_launch("gemm_f32_reduce");
 }
 
 // ---------------------------------------------------------------------------------------------

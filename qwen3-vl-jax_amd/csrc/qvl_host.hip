@@ -62,7 +62,7 @@ static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, i
   if (dtype == QVL_DTYPE_F32) {
     // fp32: x [m, lda], packed w [round_up(n, 64), k], y / res [m, ld] fp32, 16-byte rows
     if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || lda % 4 || ldc % 4 ||
-        (epi == QVL_EPI_BIAS_RESIDUAL && (!aligned16(res) || ldr % 4)))
+        (epi == QVL_EPI_BIAS_RESIDUAL && (!aligned16(res) || ldr % 4)) || (ws && !aligned16(ws)))
       return set_error(QVL_ERR_MISALIGNED, "dense: fp32 operands must be 16-byte aligned (lda, ldc, ldr % 4 == 0)");
     if (m * lda * 4 >= (int64_t)UINT32_MAX || round_up(n, 64) * k * 4 >= (int64_t)UINT32_MAX)
       return set_error(QVL_ERR_UNSUPPORTED, "dense: operand larger than 4 GiB");
@@ -70,6 +70,7 @@ static int dense_impl(void* stream, int32_t dtype, int32_t epi, const void* x, i
     p.x = (const float*)x; p.lda = lda; p.w = (const float*)w; p.ldw = k; p.n_rows_w = round_up(n, 64);
     p.bias = bias; p.res = (const float*)res; p.ldr = ldr; p.y = (float*)y; p.ldc = ldc;
     p.M = (int)m; p.N = (int)n; p.K = (int)k; p.Kp = (int)k;
+    p.part = (float*)ws; p.part_elems = ws ? (int64_t)(ws_bytes / sizeof(float)) : 0;
     return gemm_f32(p, epi, (hipStream_t)stream);
   }
   if (!aligned16(x) || !aligned16(w) || !aligned16(bias) || !aligned16(y) || lda % 8 || ldc % 4 ||
@@ -525,7 +526,7 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   L->off_vt = take((size_t)L->H * L->Np * vrows * e);
   L->off_h = take((size_t)N * hcols * e);
   L->off_cs = take((size_t)N * (hd / 2) * 8);
-  L->part_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float) : 0;
+  L->part_bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);   // split-K partials (both dtypes)
   L->off_part = take(L->part_bytes);
   // partial outputs of split attention items: at most one per workgroup slot (4 per CU)
   L->apart_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)attn_split_slots_bound() * attn_partial_floats((int)hd) * 4 : 0;

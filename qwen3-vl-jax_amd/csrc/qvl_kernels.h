@@ -71,6 +71,12 @@ struct GemmF32Params {
   const float* res; int64_t ldr;   // residual, may alias y
   float* y; int64_t ldc;
   int M, N, K, Kp;
+  // Split-K (part != NULL, set by gemm_f32 when the tiles leave most workgroup slots idle): unit u
+  // of the grid is K part u / tiles of tile u % tiles and stores its raw sums to
+  // part[(u / tiles) * M * Npad + m * Npad + n] (Npad = N rounded up to the tile); a reduction
+  // kernel sums the parts in order and applies the epilogue.
+  float* part; int64_t part_elems;
+  int split;
 };
 
 // Floats of split-K partial workspace that lets every GEMM of up to 256x256 tiles split its tail
@@ -118,7 +124,7 @@ int fold_ln_weight_bf16(const bf16* w, int64_t k, int64_t n_pad, const float* ga
 int rotary_table(const int* pos_hw, int n_tok, int head_dim, const float* inv_freq, int round16, f32x2* cs,
                  hipStream_t stream);
 int cast_f32_bf16(const float* x, bf16* y, int64_t n, hipStream_t stream);
-int gemm_f32(const GemmF32Params& p, int epi, hipStream_t stream);
+int gemm_f32(GemmF32Params p, int epi, hipStream_t stream);
 int layer_norm_f32(const float* x, int64_t ldx, const float* g, const float* b, float* y, int64_t ldy, int rows,
                    int cols, float eps, hipStream_t stream);
 int pos_embed_f32(const float* table, const int* idx, const float* wts, float* y, int n_tok, int dim,

@@ -51,11 +51,17 @@ def test_pack_weight_f32_is_exact_transpose(pkg, lib):
     assert not out[70:].any() and not out[:, 100:].any()
 
 
+@pytest.mark.parametrize("ws", [False, True])
 @pytest.mark.parametrize("epi", [0, 1, 2])
-@pytest.mark.parametrize("m,n,k", [(300, 192, 128), (784, 3072, 1024), (196, 2048, 4096), (257, 4352, 1152)])
-def test_dense_f32_vs_fp64(pkg, lib, epi, m, n, k):
+@pytest.mark.parametrize("m,n,k", [(300, 192, 128), (784, 3072, 1024), (196, 2048, 4096), (257, 4352, 1152),
+                                   (784, 1024, 4096), (784, 1024, 1024)])
+def test_dense_f32_vs_fp64(pkg, lib, epi, m, n, k, ws):
     """fp32 GEMM + epilogue vs float64 on the same fp32 operands: rel-L2 <= 2e-6 and every
-    element within 1e-5 of sum_k |x w| (the fp32 accumulation bound)."""
+    element within 1e-5 of sum_k |x w| (the fp32 accumulation bound). With a workspace
+    (qvl_dense_ws) the shapes whose 128 x 128 tiles leave most workgroup slots idle split K into
+    fp32 partials summed in order by a second kernel (config 0's fc2 and proj: 56 tiles, 8 parts;
+    its qkv: 3 parts; 300 x 192 x 128 has too few k-steps to split): same bounds; the residual
+    epilogue runs in place (y is the residual)."""
     cp = pkg.capi
     rng = np.random.default_rng(m + n + k + epi)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -64,8 +70,16 @@ def test_dense_f32_vs_fp64(pkg, lib, epi, m, n, k):
     r = rng.standard_normal((m, n)).astype(np.float32)
     xt, wp, bt = dev32(x), pack32(lib, cp, w), dev32(b)
     y = dev32(r) if epi == 2 else torch.empty((m, n), dtype=torch.float32, device=DEV)
-    cp.check(lib.qvl_dense(stream(), cp.QVL_DTYPE_F32, epi, xt.data_ptr(), k, wp.data_ptr(), bt.data_ptr(),
-                           y.data_ptr() if epi == 2 else None, n, y.data_ptr(), n, m, n, k))
+    if ws:
+        nb = C.c_size_t()
+        cp.check(lib.qvl_dense_workspace_size(C.byref(nb)))
+        wsb = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+        cp.check(lib.qvl_dense_ws(stream(), cp.QVL_DTYPE_F32, epi, xt.data_ptr(), k, wp.data_ptr(), bt.data_ptr(),
+                                  y.data_ptr() if epi == 2 else None, n, y.data_ptr(), n, m, n, k, wsb.data_ptr(),
+                                  nb.value))
+    else:
+        cp.check(lib.qvl_dense(stream(), cp.QVL_DTYPE_F32, epi, xt.data_ptr(), k, wp.data_ptr(), bt.data_ptr(),
+                               y.data_ptr() if epi == 2 else None, n, y.data_ptr(), n, m, n, k))
     ref = x.astype(np.float64) @ w.astype(np.float64) + b
     if epi == 1:
         ref = 0.5 * ref * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (ref + 0.044715 * ref ** 3)))
