@@ -85,8 +85,9 @@ int qvl_vision_metadata(const int32_t* h_grid_thw, int64_t n_grids, int32_t merg
 int qvl_attention_worklist(const int32_t* h_cu_seqlens, int64_t n_segments, int32_t num_heads,
                            int32_t* h_items, int64_t capacity, int64_t* n_items);
 
-/* The same work list balanced for the last round of workgroup slots (bf16 kernels, head_dim 64
- * or 72; `n_cus` compute units, 4 or 3 workgroups each): the items that would run in the last,
+/* The same work list balanced for the last round of workgroup slots (modelled on the bf16
+ * kernels, head_dim 64 or 72; `n_cus` compute units, 4 or 3 workgroups each; the fp32 kernel runs
+ * the same lists): the items that would run in the last,
  * partial round leave the list (their entries become empty items) and are appended as up to 8
  * parts each that split their key tiles (head field: head | part << 12 | parts << 20). Items
  * [0, *n_whole) are whole, [*n_whole, *n_items) parts, in item order. Same call convention as
@@ -298,10 +299,10 @@ int qvl_attention_headmajor(void* stream, int32_t dtype, const void* d_q, const 
                             const int32_t* d_tiles, int64_t n_tiles, int64_t n_tokens, int32_t num_heads,
                             int32_t head_dim, void* d_out, int64_t ld_out);
 
-/* qvl_attention_headmajor on a qvl_attention_worklist_split list (bf16): the parts write their
- * unnormalised outputs and softmax state to the workspace
- * (qvl_attention_split_workspace_size(head_dim, n_tiles, n_whole) bytes) and a combine kernel
- * writes those items' rows (model.py:585-600). */
+/* qvl_attention_headmajor on a qvl_attention_worklist_split list (bf16 or fp32, in
+ * qvl_attention_headmajor's layouts): the parts write their unnormalised outputs and softmax state
+ * to the workspace (qvl_attention_split_workspace_size(head_dim, n_tiles, n_whole) bytes) and a
+ * combine kernel writes those items' rows (model.py:585-600). */
 int qvl_attention_split_workspace_size(int32_t head_dim, int64_t n_tiles, int64_t n_whole, size_t* bytes);
 int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* d_q, const void* d_k,
                                   const void* d_vt, const int32_t* d_tiles, int64_t n_tiles, int64_t n_whole,

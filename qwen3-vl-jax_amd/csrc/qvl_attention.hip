@@ -35,7 +35,6 @@
 
 namespace qvl {
 
-constexpr int kAttnBM = 128;   // queries per workgroup
 constexpr int kAttnBN = 64;    // keys per K/V tile
 constexpr int kHD = 64;
 
@@ -585,9 +584,9 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_qk88_kernel(
 // (query, 4 dims) pairs of it: out = sum_i O_i 2^(m_i - M) / sum_i l_i 2^(m_i - M),
 // M = max_i m_i (scores in log2 units). All parts' loads issue before any use.
 // ---------------------------------------------------------------------------------------------
-template <int HD>
+template <int HD, typename OutT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict__ tiles, int n_whole, int n_slots,
-                                                           const float* __restrict__ part, bf16* __restrict__ O,
+                                                           const float* __restrict__ part, OutT* __restrict__ O,
                                                            int64_t ldo) {
   constexpr int kChunks = (kAttnBM * (HD / 4) + 255) / 256;
   const int slot = blockIdx.x / kChunks, chunk = blockIdx.x % kChunks;
@@ -627,18 +626,30 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict
     }
   }
   const float inv = 1.0f / L;
-  *reinterpret_cast<u32x2*>(O + (int64_t)(q0 + ql) * ldo + head * HD + d) =
-      u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+  if constexpr (sizeof(OutT) == 4)
+    *reinterpret_cast<f32x4*>(O + (int64_t)(q0 + ql) * ldo + head * HD + d) =
+        f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+  else
+    *reinterpret_cast<u32x2*>(O + (int64_t)(q0 + ql) * ldo + head * HD + d) =
+        u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
 }
 
-template <int HD>
-static int launch_combine(const int* d_tiles, int64_t n_tiles, int64_t n_whole, const float* part, bf16* out,
+template <int HD, typename OutT = bf16>
+static int launch_combine(const int* d_tiles, int64_t n_tiles, int64_t n_whole, const float* part, OutT* out,
                           int64_t ldo, hipStream_t stream) {
   constexpr int kChunks = (kAttnBM * (HD / 4) + 255) / 256;
   const int64_t n_slots = n_tiles - n_whole;
-  hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3((unsigned)(n_slots * kChunks)), dim3(256), 0, stream, d_tiles,
-                     (int)n_whole, (int)n_slots, part, out, ldo);
+  hipLaunchKernelGGL((attn_combine_kernel<HD, OutT>), dim3((unsigned)(n_slots * kChunks)), dim3(256), 0, stream,
+                     d_tiles, (int)n_whole, (int)n_slots, part, out, ldo);
   return check_launch("attn_combine");
+}
+
+// The combine of an fp32 split list (the fp32 attention kernel writes the same partials).
+int attention_combine_f32(const int* d_tiles, int64_t n_tiles, int64_t n_whole, const float* part, float* out,
+                          int64_t ldo, int hd, hipStream_t stream) {
+  if (hd == 64) return launch_combine<64, float>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
+  if (hd == 72) return launch_combine<72, float>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
+  return launch_combine<80, float>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);
 }
 
 // One rotary output x*cos + rotate_half(x)*sin in the reference's bf16 arithmetic (model.py:579-582):

@@ -401,12 +401,15 @@ int attention_relayout_f32(const float* q, const float* k, const float* v, int64
 // already in log2 units, rescale), and the probabilities feed the PV MFMA straight from
 // registers (step kk pairs the key of register kk in both lane halves with V^T read as 16-byte
 // runs of 4 keys). LDS rows are padded by 4 floats: 16 consecutive rows start in 16 distinct
-// 16-byte bank groups.
+// 16-byte bank groups. Items of a split list past n_whole are key parts (head | part << 12 | parts
+// << 20): a part runs its share of the key tiles and stores the unnormalised O, the running max
+// and the row sum (log2 units) for attn_combine_kernel.
 // ---------------------------------------------------------------------------------------------
 template <int HD>
 __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                                                            const float* __restrict__ Vt, const int* __restrict__ items,
-                                                           int Np, float* __restrict__ O, int64_t ldo) {
+                                                           int Np, float* __restrict__ O, int64_t ldo, int n_whole,
+                                                           float* __restrict__ part) {
   constexpr int NDB = (HD + 31) / 32, VR = 32 * NDB, KH = HD / 2;
   constexpr int KS = HD + 4, VS = 32 + 4;
   static_assert(HD % 8 == 0, "head_dim");
@@ -414,8 +417,11 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const float* __restri
   __shared__ __attribute__((aligned(16))) float sV[2][VR * VS];
 
   const int item = blockIdx.x;
-  const int seg_s = items[4 * item], seg_e = items[4 * item + 1], q0 = items[4 * item + 2], head = items[4 * item + 3];
-  if (seg_e <= seg_s) return;
+  const int seg_s = items[4 * item], seg_e = items[4 * item + 1], q0 = items[4 * item + 2];
+  const int hraw = items[4 * item + 3];
+  const int head = hraw & kAttnHeadMask;
+  const int part_i = (hraw >> kAttnSplitShift) & 0xff, parts = (hraw >> kAttnPartsShift) & 0xff;
+  if (seg_e <= seg_s || (parts && (!part || item < n_whole))) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
 
@@ -474,8 +480,11 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const float* __restri
   for (int db = 0; db < NDB; ++db) oacc[db] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int k_begin = seg_s & ~3;                  // 16-byte aligned V^T runs; keys < seg_s masked
-  const int n_kt = (seg_e - k_begin + 31) / 32;
+  const int k_first = seg_s & ~3;                  // 16-byte aligned V^T runs; keys < seg_s masked
+  const int n_all = (seg_e - k_first + 31) / 32;
+  const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
+  const int k_begin = k_first + 32 * t0;
+  const int n_kt = t1 - t0;
   gload(k_begin);
   sstore(0);
   __syncthreads();
@@ -527,6 +536,24 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const float* __restri
     }
   }
 
+  if (parts) {
+    // a key part: unnormalised O^T rows, (m, l) per query, in the layout attn_combine_kernel reads
+    if (qrow < seg_e) {
+      float* pp = part + (int64_t)(item - n_whole) * attn_partial_floats(HD);
+      const int ql = wave * 32 + l32;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = db * 32 + 8 * g + 4 * hh;
+          if (d < HD)
+            *reinterpret_cast<f32x4*>(pp + ql * HD + d) =
+                f32x4{oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]};
+        }
+      if (hh == 0) *reinterpret_cast<f32x2*>(pp + kAttnBM * HD + 2 * ql) = f32x2{m_run, l_run};
+    }
+    return;
+  }
   if (qrow < seg_e) {
     const float inv = 1.0f / l_run;
     float* orow = O + (int64_t)qrow * ldo + head * HD;
@@ -546,20 +573,23 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const float* __restri
 }
 
 int attention_f32(const float* Qb, const float* Kb, const float* Vtb, const int* d_items, int64_t n_items, int Np,
-                  int hd, float* out, int64_t ldo, hipStream_t stream) {
+                  int hd, float* out, int64_t ldo, hipStream_t stream, int64_t n_whole, float* part) {
   if (n_items == 0) return QVL_OK;
+  if (n_whole < 0) n_whole = n_items;
   if (hd == 64)
     hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, dim3((unsigned)n_items), dim3(256), 0, stream, Qb, Kb, Vtb, d_items,
-                       Np, out, ldo);
+                       Np, out, ldo, (int)n_whole, part);
   else if (hd == 72)
     hipLaunchKernelGGL(attn_fwd_f32_kernel<72>, dim3((unsigned)n_items), dim3(256), 0, stream, Qb, Kb, Vtb, d_items,
-                       Np, out, ldo);
+                       Np, out, ldo, (int)n_whole, part);
   else if (hd == 80)
     hipLaunchKernelGGL(attn_fwd_f32_kernel<80>, dim3((unsigned)n_items), dim3(256), 0, stream, Qb, Kb, Vtb, d_items,
-                       Np, out, ldo);
+                       Np, out, ldo, (int)n_whole, part);
   else
     return set_error(QVL_ERR_UNSUPPORTED, "attention f32: head_dim=%d (supported: 64, 72, 80)", hd);
-  return check_launch("attn_fwd_f32");
+  const int rc = check_launch("attn_fwd_f32");
+  if (rc || n_whole >= n_items || !part) return rc;
+  return attention_combine_f32(d_items, n_items, n_whole, part, out, ldo, hd, stream);
 }
 
 }  // namespace qvl

@@ -446,18 +446,25 @@ int qvl_attention_split_workspace_size(int32_t head_dim, int64_t n_tiles, int64_
 int qvl_attention_headmajor_split(void* stream, int32_t dtype, const void* q, const void* k, const void* vt,
                                   const int32_t* tiles, int64_t n_tiles, int64_t n_whole, int64_t n_tokens, int32_t H,
                                   int32_t hd, void* out, int64_t ld_out, void* ws, size_t ws_bytes) {
-  if (dtype != QVL_DTYPE_BF16) return set_error(QVL_ERR_UNSUPPORTED, "attention split: bf16 only");
+  if (dtype != QVL_DTYPE_BF16 && dtype != QVL_DTYPE_F32)
+    return set_error(QVL_ERR_UNSUPPORTED, "attention split: dtype %d", dtype);
   if (hd != 64 && hd != 72 && hd != 80) return set_error(QVL_ERR_UNSUPPORTED, "attention split: head_dim=%d", hd);
   if (n_tokens < 0 || H <= 0 || n_tiles < 0 || n_whole < 0 || n_whole > n_tiles || ld_out < (int64_t)H * hd ||
       ld_out % 4)
     return set_error(QVL_ERR_INVALID_ARG, "attention split: bad sizes");
   if (n_tokens == 0 || n_tiles == 0) return QVL_OK;
   if (!q || !k || !vt || !tiles || !out) return set_error(QVL_ERR_INVALID_ARG, "attention split: NULL operand");
-  if ((uintptr_t)out & 7) return set_error(QVL_ERR_MISALIGNED, "attention split: out alignment");
+  if ((uintptr_t)out & (dtype == QVL_DTYPE_F32 ? 15 : 7)) return set_error(QVL_ERR_MISALIGNED, "attention split: out alignment");
   const size_t need = (size_t)(n_tiles - n_whole) * attn_partial_floats(hd) * sizeof(float);
   if (need && (!ws || ws_bytes < need)) return set_error(QVL_ERR_WORKSPACE, "attention split: workspace %zu < %zu", ws_bytes, need);
   if (need && !aligned16(ws)) return set_error(QVL_ERR_MISALIGNED, "attention split: workspace alignment");
   const int Np = (int)attn_np(n_tokens);
+  if (dtype == QVL_DTYPE_F32) {
+    // fp32 operands in qvl_attention_headmajor's fp32 layout
+    if (!aligned16(q) || !aligned16(k) || !aligned16(vt)) return set_error(QVL_ERR_MISALIGNED, "attention split: fp32 operands");
+    return attention_f32((const float*)q, (const float*)k, (const float*)vt, tiles, n_tiles, Np, hd, (float*)out, ld_out,
+                         (hipStream_t)stream, n_whole, need ? (float*)ws : nullptr);
+  }
   if (hd == 64)
     return attention_hd64((const bf16*)q, (const bf16*)k, (const bf16*)vt, tiles, n_tiles, Np, H, (bf16*)out, ld_out,
                           (hipStream_t)stream, n_whole, need ? (float*)ws : nullptr);
@@ -529,7 +536,7 @@ static int tower_layout(const qvl_vision_config* c, int64_t N, TowerLayout* L) {
   L->part_bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);   // split-K partials (both dtypes)
   L->off_part = take(L->part_bytes);
   // partial outputs of split attention items: at most one per workgroup slot (4 per CU)
-  L->apart_bytes = c->dtype == QVL_DTYPE_BF16 ? (size_t)attn_split_slots_bound() * attn_partial_floats((int)hd) * 4 : 0;
+  L->apart_bytes = (size_t)attn_split_slots_bound() * attn_partial_floats((int)hd) * 4;   // split attention partials
   L->off_apart = take(L->apart_bytes);
   // row statistics of the LayerNorms folded into the following Dense (bf16): per-128-column partials
   // (sum, squared deviations) of each row of x, or (mean, rstd) per row when hidden % 128 != 0
@@ -734,7 +741,7 @@ int qvl_encode_vision(void* stream, const qvl_vision_config* c, const qvl_vision
     }
     // window mode: blocks outside fullatt_block_indexes attend within windows (model.py:838-839)
     const bool full = !win || ((c->fullatt_mask >> i) & 1ull);
-    if (full && !f32 && meta->split_tiles) {
+    if (full && meta->split_tiles) {
       void* apart = base + L.off_apart;
       QVL_TRY_RC(qvl_attention_headmajor_split(st, dt, Qb, Kb, Vb, meta->split_tiles, meta->n_split_tiles,
                                                meta->n_split_whole, N, (int)L.H, (int)L.hd, xn, D, apart,

@@ -85,7 +85,8 @@ inline int64_t gemm_partials_elems(int cus) { return (int64_t)cus * 256 * 256; }
 int gemm_device_cus();
 
 // (work item head-field layout: qvl_host_common.h)
-__host__ __device__ constexpr int64_t attn_partial_floats(int hd) { return 128 * (int64_t)(hd + 2); }   // per split slot
+constexpr int kAttnBM = 128;   // queries per attention work item (bf16 and fp32 kernels)
+__host__ __device__ constexpr int64_t attn_partial_floats(int hd) { return kAttnBM * (int64_t)(hd + 2); }   // per split slot
 
 // Position of key m in the V^T layout the attention kernel reads: within each 16-key group
 // (aligned to 16 in the token index) the middle two 4-key quads are swapped, so that the 8 keys a
@@ -133,8 +134,12 @@ int pack_weight_f32(const float* w, int64_t k_in, int64_t n_out, float* out, hip
 int attention_relayout_f32(const float* q, const float* k, const float* v, int64_t ld, const f32x2* cs, int N, int Np,
                            int H, int hd, int vrows, float qscale, float* Qo, float* Ko, float* Vto,
                            hipStream_t stream);
+// fp32 attention on a work list; a split list (items [n_whole, n_items) are key parts) writes the
+// parts' partials to `part` (attn_partial_floats(hd) per part) and combines them.
 int attention_f32(const float* Qb, const float* Kb, const float* Vtb, const int* d_items, int64_t n_items, int Np,
-                  int hd, float* out, int64_t ldo, hipStream_t stream);
+                  int hd, float* out, int64_t ldo, hipStream_t stream, int64_t n_whole = -1, float* part = nullptr);
+int attention_combine_f32(const int* d_tiles, int64_t n_tiles, int64_t n_whole, const float* part, float* out,
+                          int64_t ldo, int hd, hipStream_t stream);
 int pack_weight_bf16(const float* w, int64_t k_in, int64_t n_out, bf16* out, hipStream_t stream);
 // qvl_gather_rows with the identity order when idx is NULL and out columns [width, pad_to) zeroed.
 int gather_rows_pad(void* stream, int32_t src_dtype, const void* src, int64_t ld_src, int32_t dst_dtype, void* dst,

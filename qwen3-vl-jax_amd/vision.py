@@ -640,7 +640,7 @@ class Qwen3VisionTransformer:
             host["window_index"] = m.window_index if len(m.window_index) else np.zeros(1, np.int32)
             host["window_reverse"] = m.window_reverse if len(m.window_reverse) else np.zeros(1, np.int32)
         split = None
-        if self.split_attention and self.qdtype == capi.QVL_DTYPE_BF16 and s.head_dim in (64, 72, 80):
+        if self.split_attention and s.head_dim in (64, 72, 80):
             n_cus = torch.cuda.get_device_properties(torch.device(self.device)).multi_processor_count
             cu_full = m.cu_full if s.use_window else m.cu_seqlens
             split, n_whole = attention_worklist_split(cu_full, s.num_heads, s.head_dim, n_cus)

@@ -169,6 +169,60 @@ def test_attention_f32_ragged_vs_fp64(pkg, lib, hd):
         assert rel_l2(got[cu[i]:cu[i + 1]], ref[cu[i]:cu[i + 1]]) <= 1e-5, i
 
 
+@pytest.mark.parametrize("hd,H,grids", [(64, 16, [(1, 28, 28)]), (72, 16, [(1, 28, 28)]), (80, 16, [(1, 16, 16), (1, 10, 30)]),
+                                        (64, 4, [(1, 2, 2), (1, 4, 2), (3, 2, 6), (1, 10, 14), (1, 32, 32)])])
+def test_attention_f32_split_list(pkg, lib, hd, H, grids):
+    """fp32 attention on a qvl_attention_worklist_split list (config 0's 784-token image: 112 items for
+    256 CUs, each split into key parts whose partials attn_combine_kernel sums; ragged segments)
+    against the plain list (rel-L2 <= 1e-6: the same online softmax in another order) and fp64
+    (<= 1e-5), every output written; on head-major operands in qvl_attention_headmajor's fp32 layout.
+    (The ragged list runs 4 heads: with 16 its 208 items fill more than half the CUs, which the list
+    builder leaves whole.)"""
+    cp = pkg.capi
+    m = pkg.grid_metadata(grids, dtype=cp.QVL_DTYPE_F32, num_heads=H)
+    N = m.n_tokens
+    Np = -(-N // 64) * 64
+    vrows = -(-hd // 32) * 32
+    rng = np.random.default_rng(hd + N)
+    q = np.zeros((H, Np, hd), np.float32); k = np.zeros((H, Np, hd), np.float32); v = np.zeros((H, vrows, Np), np.float32)
+    q[:, :N] = rng.standard_normal((H, N, hd)) * 0.25
+    k[:, :N] = rng.standard_normal((H, N, hd))
+    v[:, :hd, :N] = rng.standard_normal((H, hd, N))
+    qt, kt, vt_ = dev32(q), dev32(k), dev32(v)
+    n_cus = torch.cuda.get_device_properties(0).multi_processor_count
+    split, n_whole = pkg.attention_worklist_split(m.cu_seqlens, H, hd, n_cus)
+    plain = torch.from_numpy(m.tiles).to(DEV)
+    st = torch.from_numpy(split).to(DEV)
+    nb = C.c_size_t()
+    cp.check(lib.qvl_attention_split_workspace_size(hd, len(split), n_whole, C.byref(nb)))
+    ws = torch.empty(max(nb.value, 256), dtype=torch.uint8, device=DEV)
+    outs = []
+    for lst in ("plain", "split"):
+        out = torch.full((N, H * hd), float("nan"), dtype=torch.float32, device=DEV)
+        if lst == "plain":
+            cp.check(lib.qvl_attention_headmajor(stream(), cp.QVL_DTYPE_F32, qt.data_ptr(), kt.data_ptr(), vt_.data_ptr(),
+                                                 plain.data_ptr(), len(m.tiles), N, H, hd, out.data_ptr(), H * hd))
+        else:
+            cp.check(lib.qvl_attention_headmajor_split(stream(), cp.QVL_DTYPE_F32, qt.data_ptr(), kt.data_ptr(),
+                                                       vt_.data_ptr(), st.data_ptr(), len(split), n_whole, N, H, hd,
+                                                       out.data_ptr(), H * hd, ws.data_ptr(), nb.value))
+        torch.cuda.synchronize()
+        outs.append(to_np(out))
+    assert len(split) > n_whole, "the list should have parts"
+    ref = np.zeros((N, H * hd))
+    cu = m.cu_seqlens
+    for i in range(len(cu) - 1):
+        a, b = cu[i], cu[i + 1]
+        for h in range(H):
+            sc = q[h, a:b].astype(np.float64) @ k[h, a:b].astype(np.float64).T
+            w = np.exp2(sc - sc.max(-1, keepdims=True))
+            ref[a:b, h * hd:(h + 1) * hd] = (w @ v[h, :hd, a:b].astype(np.float64).T) / w.sum(-1, keepdims=True)
+    for got in outs:
+        assert np.isfinite(got).all()
+        assert rel_l2(got, ref) <= 1e-5
+    assert rel_l2(outs[1], outs[0]) <= 1e-6
+
+
 @pytest.fixture(scope="module")
 def params2b(pkg):
     return pkg.random_params(pkg.spec_2b(), seed=21)
