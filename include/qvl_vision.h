@@ -417,8 +417,8 @@ typedef struct qvl_vision_metadata_dev {
   const int32_t* window_tiles;    /* [n_window_tiles, 4]                                     */
   const int32_t* window_index;    /* [n_tokens/4] merge group at each window-order position  */
   const int32_t* window_reverse;  /* [n_tokens/4] argsort(window_index)                      */
-  /* optional (bf16): a qvl_attention_worklist_split list of the full-attention segments, used
-   * instead of `tiles` when split_tiles is not NULL. */
+  /* optional (bf16 and fp32): a qvl_attention_worklist_split list of the full-attention
+   * segments, used instead of `tiles` when split_tiles is not NULL. */
   int64_t n_split_tiles;
   int64_t n_split_whole;
   const int32_t* split_tiles;     /* [n_split_tiles, 4]                                      */
