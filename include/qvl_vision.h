@@ -255,7 +255,9 @@ int qvl_dense_qkv_rotary_ln(void* stream, int32_t dtype, const void* d_x, int64_
  * over the group's bf16 outputs y (n % 128 == 0, ldc and ldr multiples of 8; d_parts
  * [m][n / 128][2] fp32). The folded Dense entries below combine a row's groups into its mean and
  * variance (Chan et al.'s pairwise update), which replaces the LayerNorm's statistics pass
- * (model.py:384-386): no LayerNorm and no statistics launch remain between the two GEMMs. bf16. */
+ * (model.py:384-386): no LayerNorm and no statistics launch remain between the two GEMMs. bf16.
+ * With a workspace the tail tiles may split along K (qvl_dense_ws); the split-K reduction then writes
+ * their rows' partials. */
 int qvl_dense_rowstats_ws(void* stream, int32_t dtype, const void* d_x, int64_t lda, const void* d_w,
                           const float* d_bias, const void* d_residual, int64_t ldr, void* d_y, int64_t ldc,
                           int64_t m, int64_t n, int64_t k, float* d_parts, void* d_workspace,

@@ -1013,8 +1013,40 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
     }
   }
   // (a folded LayerNorm is already in the partials: the tail units fold before storing)
-  if constexpr (EPI == kEpiQkvRope) epi_rope_pair(p, m, n, lo, hi);
-  else epi_store_quad<EPI>(p, m, n, lo);
+  if constexpr (EPI == kEpiQkvRope) {
+    epi_rope_pair(p, m, n, lo, hi);
+  } else if constexpr (EPI == kEpiBiasResidual) {
+    if (!p.rs_part) {
+      epi_store_quad<EPI>(p, m, n, lo);
+      return;
+    }
+    // With the row partials: the 32 lanes of each half wave hold the 32 quads of one 128-column
+    // group of one row (a tile row is BN / 4 = 32 or 64 consecutive items; N % 128 == 0), so the
+    // group's (sum, sum of squared deviations) of the bf16 outputs reduce across the half wave.
+    // Rows past M and groups past N skip as a whole half wave.
+    if (m >= p.M || n >= p.N) return;
+    const f32x4 bv = *reinterpret_cast<const f32x4*>(p.bias + n);
+    const u32x2 r = *reinterpret_cast<const u32x2*>(p.res + (int64_t)m * p.ldr + n);
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = epi_value<EPI>(lo[e], bv[e]);
+    v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
+    const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldc + n) = o;
+    const float y[4] = {bf16_lo(o.x), bf16_hi(o.x), bf16_lo(o.y), bf16_hi(o.y)};
+    float sum = (y[0] + y[1]) + (y[2] + y[3]);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum * (1.0f / 128.0f);
+    float q2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q2 = fmaf(y[e] - mean, y[e] - mean, q2);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) q2 += __shfl_xor(q2, off);
+    if ((threadIdx.x & 31) == 0) p.rs_part[(int64_t)m * (p.N / 128) + n / 128] = f32x2{sum, q2};
+  } else {
+    epi_store_quad<EPI>(p, m, n, lo);
+  }
 }
 
 // The split-K reduction of the head_dim-72 rotary qkv GEMM (256 x 288 tiles, 4 heads of one of q, k,
@@ -1230,8 +1262,8 @@ template <int EPI, bool LN>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const int cus = gemm_device_cus();
   ForcedPlan f = t_plan;
-  // the split-K reduction writes no row statistics and computes no pos-embed
-  if (p.rs_part || EPI == kEpiBiasPosEmbed) f.split_mode = -1;
+  // the split-K reduction computes no pos-embed
+  if (EPI == kEpiBiasPosEmbed) f.split_mode = -1;
   const GemmPlan a = plan_gemm<288, 256>(p, cus, kRate288x256, f.split_mode);
   const GemmPlan b = plan_gemm<256, 256>(p, cus, kRate256x256, f.split_mode);
   const GemmPlan c = plan_gemm<256, 128>(p, cus, kRate256x128, f.split_mode);

@@ -140,7 +140,7 @@ def test_workspace_sizes(pkg):
     assert 200e6 < nb.value < 600e6
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18430, C.byref(nb)) == -1   # not a multiple of 4
     bf16_bytes = nb.value
-    cfg.dtype = pkg.capi.QVL_DTYPE_F32        # fp32 activations, no split-K partials
+    cfg.dtype = pkg.capi.QVL_DTYPE_F32        # fp32 activations
     assert lib.qvl_encode_vision_workspace_size(C.byref(cfg), 18432, C.byref(nb)) == 0
     assert 1.5 * bf16_bytes < nb.value < 2.5 * bf16_bytes
     cfg.dtype = 5

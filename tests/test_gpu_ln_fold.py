@@ -293,14 +293,16 @@ def rowstats_dense(lib, cp, x, w, bias, res, n, k, ws, nb):
     return y, parts
 
 
+@pytest.mark.parametrize("split", [-1, 1])
 @pytest.mark.parametrize("m,n,k,plan", [(1000, 1024, 4096, 0), (517, 1152, 1152, 0), (600, 1024, 1024, 1),
-                                        (300, 1280, 1024, 3)])
-def test_dense_rowstats(pkg, lib, m, n, k, plan):
-    """qvl_dense_rowstats_ws: the residual Dense's output bit for bit as qvl_dense_ws gives it (under a
-    pinned tile plan when plan > 0: 288x256, or 256x128 for plan 3; the split-K tail is never used
-    with row statistics, so the comparison pins the split off too), and per 128-column group of each
-    row the sum and the sum of squared deviations of those bf16 outputs within fp32 summation error
-    of fp64 (rows with offsets up to 40 standard deviations)."""
+                                        (300, 1280, 1024, 3), (784, 1024, 4096, 0)])
+def test_dense_rowstats(pkg, lib, m, n, k, plan, split):
+    """qvl_dense_rowstats_ws: the residual Dense's output bit for bit as qvl_dense_ws gives it under the
+    same pinned plan (tile 288x256 for plan 1, 256x128 for plan 3, the cost model's for 0; split -1
+    forbids the tail split-K, 1 forces it: then the tail tiles' rows come from the split-K reduction,
+    which writes their partials too), and per 128-column group of each row the sum and the sum of
+    squared deviations of those bf16 outputs within fp32 summation error of fp64 (rows with offsets
+    up to 40 standard deviations)."""
     cp = pkg.capi
     rng = np.random.default_rng(m + n + k)
     x = torch.from_numpy(rows(rng, m, k)).to(DEV).to(torch.bfloat16)
@@ -312,7 +314,7 @@ def test_dense_rowstats(pkg, lib, m, n, k, plan):
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
     y_ws = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
     try:
-        cp.check(lib.qvl_set_gemm_plan(plan, -1, 0))
+        cp.check(lib.qvl_set_gemm_plan(plan, split, 0))
         y, parts = rowstats_dense(lib, cp, x, w, bias, res, n, k, ws, nb.value)
         cp.check(lib.qvl_dense_ws(stream(), cp.QVL_DTYPE_BF16, cp.QVL_EPI_BIAS_RESIDUAL, x.data_ptr(), k, w.data_ptr(),
                                   bias.data_ptr(), res.data_ptr(), n, y_ws.data_ptr(), n, m, n, k, ws.data_ptr(),
