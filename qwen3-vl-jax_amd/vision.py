@@ -387,6 +387,7 @@ class Qwen3VisionTransformer:
     reference module's does (model.py:661); "bfloat16" is the reference's bf16 tower."""
 
     META_CACHE_SIZE = 16   # grids whose device metadata stays cached (LRU)
+    SPLIT_MIN_KEYS_BF16 = 2048   # the bf16 tower runs split attention lists from this segment length
 
     def __init__(self, spec: VisionBackboneSpec, dtype: str = "float32", device: str = "cuda:0",
                  split_attention: bool = True, ln_fold: bool = True):
@@ -640,9 +641,15 @@ class Qwen3VisionTransformer:
             host["window_index"] = m.window_index if len(m.window_index) else np.zeros(1, np.int32)
             host["window_reverse"] = m.window_reverse if len(m.window_reverse) else np.zeros(1, np.int32)
         split = None
-        if self.split_attention and s.head_dim in (64, 72, 80):
+        cu_full = m.cu_full if s.use_window else m.cu_seqlens
+        longest = int(np.diff(cu_full).max()) if len(cu_full) > 1 else 0
+        # The bf16 kernels gain from key parts only on long segments (MI355X, attention alone: a lone
+        # 784- or 1024-token segment runs 12.0 / 13.7 us on the plain list against 21.0 / 29.0 us
+        # split; config 4's 7056-token one gains); the fp32 kernel, ~4x slower per key tile, gains
+        # from them at 784 tokens already.
+        if (self.split_attention and s.head_dim in (64, 72, 80) and
+                (self.qdtype == capi.QVL_DTYPE_F32 or longest >= self.SPLIT_MIN_KEYS_BF16)):
             n_cus = torch.cuda.get_device_properties(torch.device(self.device)).multi_processor_count
-            cu_full = m.cu_full if s.use_window else m.cu_seqlens
             split, n_whole = attention_worklist_split(cu_full, s.num_heads, s.head_dim, n_cus)
             host["split_tiles"] = nz(split)
         tens = _to_device_packed(host, self.device)
