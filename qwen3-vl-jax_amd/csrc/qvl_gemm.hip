@@ -1193,7 +1193,7 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 
 // Tile-plan override of the calling thread (qvl_set_gemm_plan): tile 0 = the cost model's
 // choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128, 5 = the row split (whole rounds of 288x256,
-// the rest 256x128); split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
+// the rest 256x128), 6 = 128x128 (never split); split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
 // group_n 0 = the default panel width. Thread-local, so a test pinning a plan on one thread does
 // not change another thread's launches.
 struct ForcedPlan { int tile = 0, split_mode = 0, group_n = 0; };
@@ -1257,6 +1257,7 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 //     of them (the merger's 4608 x 2048 output is exactly 256 such tiles).
 constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.42e6,
                  kRate288x128 = 1.36e6;   // MACs/us/CU
+constexpr int kSmallTileMaxK = 1536;
 
 template <int EPI, bool LN>
 static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
@@ -1284,6 +1285,12 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   int pick = f.tile;
   if (EPI == kEpiQkvRope && pick == 4) pick = 3;     // 64-feature heads need TN % 64 == 0 (288x128: 32)
   if (pick == 5 && !can_split) pick = 1;
+  // Small grids: where one round of 128x128 tiles (4 waves of 64x64, one per SIMD) covers between half
+  // and all of the CUs and K is short, they run ahead of every plan above, whose tiles then occupy
+  // at most half the CUs or need a split-K tail (one 784-token image: qkv 17.7 against 22.1 us,
+  // fc1 16.3 against 21.3 us; at K = 4096, or with fewer tiles, the split plans stay ahead).
+  const int tiles128 = ((rows + 127) / 128) * ((p.N + 127) / 128);
+  if (pick == 0 && p.K <= kSmallTileMaxK && 2 * tiles128 >= cus && tiles128 <= cus && !p.row0 && !p.row1) pick = 6;
   if (pick == 0) {
     const double cost[5] = {a.cost_us, b.cost_us, c.cost_us, EPI == kEpiQkvRope ? 1e30 : d.cost_us, r_cost};
     pick = 1;
@@ -1296,6 +1303,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
     return launch_gemm<256, 128, 4, 2, EPI, LN>(rb, r_b, stream);
   }
   if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI, LN>(p, a, stream);
+  if (pick == 6) return launch_gemm<128, 128, 2, 2, EPI, LN>(p, plan_gemm<128, 128>(p, cus, kRate256x128, -1), stream);
   if constexpr (EPI == kEpiQkvRope) {
     if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
     return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
@@ -1307,7 +1315,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
 }
 
 int gemm_set_plan(int tile, int split_mode, int group_n) {
-  if (tile < 0 || tile > 5 || split_mode < -1 || split_mode > 1 || group_n < 0)
+  if (tile < 0 || tile > 6 || split_mode < -1 || split_mode > 1 || group_n < 0)
     return set_error(QVL_ERR_INVALID_ARG, "gemm plan: tile=%d split_mode=%d group_n=%d", tile, split_mode, group_n);
   t_plan.tile = tile;
   t_plan.split_mode = split_mode;

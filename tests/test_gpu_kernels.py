@@ -548,7 +548,7 @@ def test_attention_exact_recompute_triggers(pkg, lib, hd, case):
         assert rel_l2(got[r], ref[r]) <= 1e-2, label
 
 
-_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4, "rowsplit": 5}
+_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4, "rowsplit": 5, "128x128": 6}
 
 
 def set_plan(lib, cp, plan):
@@ -561,7 +561,7 @@ def set_plan(lib, cp, plan):
 
 
 PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x128:nosplit", "rowsplit:nosplit",
-         "288x256:split", "256x256:split", "256x128:split", "288x128:split"]
+         "128x128:nosplit", "288x256:split", "256x256:split", "256x128:split", "288x128:split"]
 
 
 def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
@@ -574,9 +574,11 @@ def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
 
 @pytest.mark.parametrize("epi", [0, 1, 2])
 @pytest.mark.parametrize("m,n,k", [(18432, 1024, 1024), (4600, 2048, 4096), (2304, 4096, 1024), (300, 192, 128),
-                                   (18000, 1152, 4352), (300, 192, 64), (1000, 640, 192), (8192, 3072, 1024)])
+                                   (18000, 1152, 4352), (300, 192, 64), (1000, 640, 192), (8192, 3072, 1024),
+                                   (784, 4096, 1024)])
 def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
-    """Every tile shape (288x256 / 256x256 / 256x128 / 288x128) and the row split (whole rounds of
+    """Every tile shape (288x256 / 256x256 / 256x128 / 288x128 / 128x128, the last the cost model's
+    choice at 784 x 4096 x 1024) and the row split (whole rounds of
     288x256 tiles, the remaining rows as 256x128 tiles in a second launch: taken at 18000 and 8192
     rows, elsewhere it falls back to 288x256) gives bit-identical results without the tail split
     (same K order per output); with the split (fp32 partials summed by the reduce kernel) within
@@ -611,12 +613,14 @@ def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
         assert rel_l2(got, ref) <= 4e-3, plan
 
 
-@pytest.mark.parametrize("grids", [[(1, 48, 48)] * 8, [(1, 16, 16), (2, 10, 14), (1, 6, 8)], [(8, 32, 32)]])
+@pytest.mark.parametrize("grids", [[(1, 48, 48)] * 8, [(1, 16, 16), (2, 10, 14), (1, 6, 8)], [(8, 32, 32)],
+                                   [(1, 28, 28)]])
 def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     """The fused qkv+rotary GEMM writes bit-identical head-major Q/K/V^T (including the zeroed
-    padding rows [N, Np)) with 288x256, 256x256 and 256x128 tiles (the last with the three-stage
-    operand ring and one head per wave) and the row split (config 3's 8192 tokens: 252 tiles of
-    288x256, then 216 of 256x128); with the tail split within rel-L2 2e-3."""
+    padding rows [N, Np)) with 288x256, 256x256, 256x128 and 128x128 tiles (the last two with the
+    three-stage operand ring and one head per wave; 128x128 is the cost model's choice for one
+    784-token image) and the row split (config 3's 8192 tokens: 252 tiles of 288x256, then 216 of
+    256x128); with the tail split within rel-L2 2e-3."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
     N, D, H = m.n_tokens, 1024, 16
@@ -632,8 +636,8 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
     Np = -(-N // 64) * 64
     outs = {}
-    for plan in ["256x256:nosplit", "288x256:nosplit", "256x128:nosplit", "rowsplit:nosplit", "256x256:split",
-                 "288x256:split", "256x128:split", None]:
+    for plan in ["256x256:nosplit", "288x256:nosplit", "256x128:nosplit", "rowsplit:nosplit", "128x128:nosplit",
+                 "256x256:split", "288x256:split", "256x128:split", None]:
         set_plan(lib, cp, plan)
         q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
         k, vt = q.clone(), q.clone()

@@ -144,7 +144,8 @@ def ref_bf16_dense(xn, w_h, b_h, epi):
 def test_dense_ln_vs_reference(pkg, lib, epi, m, n, k, plan):
     """qvl_row_stats + qvl_fold_ln_weight + qvl_dense_ln_ws (bias / bias+GELU) against the
     reference's LayerNorm (bf16 output) + bf16 Dense, and against exact fp64; plan 1 forces the
-    288x256 tiles with a tail split (the split-K reduce applies the fold)."""
+    288x256 tiles with a tail split (the split-K reduce applies the fold); at 700 x 4096 x 1024 and
+    1000 x 3072 x 1024 the cost model takes 128x128 tiles."""
     cp = pkg.capi
     rng = np.random.default_rng(m + n + k + epi)
     x = rows(rng, m, k)
@@ -295,10 +296,11 @@ def rowstats_dense(lib, cp, x, w, bias, res, n, k, ws, nb):
 
 @pytest.mark.parametrize("split", [-1, 1])
 @pytest.mark.parametrize("m,n,k,plan", [(1000, 1024, 4096, 0), (517, 1152, 1152, 0), (600, 1024, 1024, 1),
-                                        (300, 1280, 1024, 3), (784, 1024, 4096, 0)])
+                                        (300, 1280, 1024, 3), (784, 1024, 4096, 0), (784, 1024, 1024, 6)])
 def test_dense_rowstats(pkg, lib, m, n, k, plan, split):
     """qvl_dense_rowstats_ws: the residual Dense's output bit for bit as qvl_dense_ws gives it under the
-    same pinned plan (tile 288x256 for plan 1, 256x128 for plan 3, the cost model's for 0; split -1
+    same pinned plan (tile 288x256 for plan 1, 256x128 for plan 3, 128x128 for plan 6, which never
+    splits, the cost model's for 0; split -1
     forbids the tail split-K, 1 forces it: then the tail tiles' rows come from the split-K reduction,
     which writes their partials too), and per 128-column group of each row the sum and the sum of
     squared deviations of those bf16 outputs within fp32 summation error of fp64 (rows with offsets
