@@ -1193,7 +1193,7 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 
 // Tile-plan override of the calling thread (qvl_set_gemm_plan): tile 0 = the cost model's
 // choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128, 5 = the row split (whole rounds of 288x256,
-// the rest 256x128), 6 = 128x128 (never split); split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
+// the rest 256x128), 6 = 128x128; split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
 // group_n 0 = the default panel width. Thread-local, so a test pinning a plan on one thread does
 // not change another thread's launches.
 struct ForcedPlan { int tile = 0, split_mode = 0, group_n = 0; };
@@ -1254,9 +1254,10 @@ static int launch_gemm(GemmParams p, const GemmPlan& g, hipStream_t stream) {
 //     these beat 1.5 rounds of 256x256: 70 against 74 us; the row split below, one round of
 //     288x256 and 216 tiles of these, is what that GEMM now runs);
 //   288x128 on 12 waves (96x32 each): fills the CUs where 288x256 tiles would cover only half
-//     of them (the merger's 4608 x 2048 output is exactly 256 such tiles).
+//     of them (the merger's 4608 x 2048 output is exactly 256 such tiles);
+//   128x128 on 4 waves (64x64 each, one per SIMD): small grids, by the rule in dispatch_gemm.
 constexpr double kRate288x256 = 1.50e6, kRate256x256 = 1.50e6, kRate256x128 = 1.42e6,
-                 kRate288x128 = 1.36e6;   // MACs/us/CU
+                 kRate288x128 = 1.36e6, kRate128x128 = 1.0e6;   // MACs/us/CU
 constexpr int kSmallTileMaxK = 1536;
 
 template <int EPI, bool LN>
@@ -1285,12 +1286,28 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   int pick = f.tile;
   if (EPI == kEpiQkvRope && pick == 4) pick = 3;     // 64-feature heads need TN % 64 == 0 (288x128: 32)
   if (pick == 5 && !can_split) pick = 1;
-  // Small grids: where one round of 128x128 tiles (4 waves of 64x64, one per SIMD) covers between half
-  // and all of the CUs and K is short, they run ahead of every plan above, whose tiles then occupy
-  // at most half the CUs or need a split-K tail (one 784-token image: qkv 17.7 against 22.1 us,
-  // fc1 16.3 against 21.3 us; at K = 4096, or with fewer tiles, the split plans stay ahead).
+  // Small grids, K <= 1536: 128x128 tiles (4 waves of 64x64, one per SIMD) unsplit where one round
+  // of them covers half to all of the CUs, or split along K where up to 8 parts of fewer tiles fill
+  // at least 7/8 of them. The larger tiles there leave most CUs idle or need long split-K tails.
+  // One 784-token image's forward: qkv 17.7 against 22.1 us (256x128), fc1 16.1 against 21.3;
+  // proj, 56 tiles in 4 parts, 15.4 against 18.9 us for 288x128 tiles in 8 parts. Cases the rule
+  // leaves to the cost model were measured slower on 128x128: 1568 rows' proj unsplit (104 tiles)
+  // 22.9 against 20.4 us; the mergers' K = 4096 GEMMs at 196 rows 25.2 / 26.8 against 20.3 / 24.2 us.
+  GemmPlan e{};
+  if (pick == 6) e = plan_gemm<128, 128>(p, cus, kRate128x128, f.split_mode);
   const int tiles128 = ((rows + 127) / 128) * ((p.N + 127) / 128);
-  if (pick == 0 && p.K <= kSmallTileMaxK && 2 * tiles128 >= cus && tiles128 <= cus && !p.row0 && !p.row1) pick = 6;
+  if (pick == 0 && p.K <= kSmallTileMaxK && !p.row0 && !p.row1) {
+    if (2 * tiles128 >= cus && tiles128 <= cus) {
+      pick = 6;
+      e = plan_gemm<128, 128>(p, cus, kRate128x128, -1);
+    } else if (f.split_mode >= 0 && 2 * tiles128 < cus) {
+      const GemmPlan sp = plan_gemm<128, 128>(p, cus, kRate128x128, 1);
+      if (8 * sp.tail * sp.split >= 7 * cus) {
+        pick = 6;
+        e = sp;
+      }
+    }
+  }
   if (pick == 0) {
     const double cost[5] = {a.cost_us, b.cost_us, c.cost_us, EPI == kEpiQkvRope ? 1e30 : d.cost_us, r_cost};
     pick = 1;
@@ -1303,7 +1320,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
     return launch_gemm<256, 128, 4, 2, EPI, LN>(rb, r_b, stream);
   }
   if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI, LN>(p, a, stream);
-  if (pick == 6) return launch_gemm<128, 128, 2, 2, EPI, LN>(p, plan_gemm<128, 128>(p, cus, kRate256x128, -1), stream);
+  if (pick == 6) return launch_gemm<128, 128, 2, 2, EPI, LN>(p, e, stream);
   if constexpr (EPI == kEpiQkvRope) {
     if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
     return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);

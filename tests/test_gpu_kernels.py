@@ -561,7 +561,7 @@ def set_plan(lib, cp, plan):
 
 
 PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x128:nosplit", "rowsplit:nosplit",
-         "128x128:nosplit", "288x256:split", "256x256:split", "256x128:split", "288x128:split"]
+         "128x128:nosplit", "288x256:split", "256x256:split", "256x128:split", "288x128:split", "128x128:split"]
 
 
 def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
@@ -637,7 +637,7 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     Np = -(-N // 64) * 64
     outs = {}
     for plan in ["256x256:nosplit", "288x256:nosplit", "256x128:nosplit", "rowsplit:nosplit", "128x128:nosplit",
-                 "256x256:split", "288x256:split", "256x128:split", None]:
+                 "256x256:split", "288x256:split", "256x128:split", "128x128:split", None]:
         set_plan(lib, cp, plan)
         q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
         k, vt = q.clone(), q.clone()
