@@ -142,8 +142,9 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
  *                6 = 128x128 tiles (chosen by the default plan on small grids with K <= 1536)
  *                (the head_dim-64 rotary qkv epilogue takes 1-3, 5 and 6 and maps 4 to 3; for the
  *                head_dim-72 one, 0 = whole rounds of 256x288 tiles and the rest in 128x288
- *                tiles where that fits one round, 1 = 256x288 tiles only, 2 = that row split
- *                wherever there are two 256-row tiles);
+ *                tiles where that fits one round (64x288 where those fill at most half of it),
+ *                1 = 256x288 tiles only, 2 = that row split wherever there are two 256-row
+ *                tiles, 3 = the same with the rest in 64x288 tiles);
  *   split_mode 0 = cost model decides the tail split-K, 1 = force it, -1 = forbid it;
  *   group_n    column tiles per panel of the tile order, 0 = default (4).
  * (0, 0, 0) restores the defaults. No counterpart in the reference (it has no tile plans). */

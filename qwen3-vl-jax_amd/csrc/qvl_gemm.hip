@@ -1348,8 +1348,11 @@ int gemm_set_plan(int tile, int split_mode, int group_n) {
 // partial round can instead be split along K when a plan forces it
 // (gemm_splitk_reduce_rope72_kernel applies the epilogue): at config 4 the split ran its GEMM in 76
 // us and the reduction of the 47 MB of fp32 partials in 16 us, against 91-93 us unsplit (MI355X).
-// Plan override (qvl_set_gemm_plan's tile): 1 = one launch of 256 x 288 tiles, 2 = the row split
-// wherever there are two row tiles (the 128-row launch alone when no whole round exists).
+// Small grids, where the 128-row launch would fill at most half of the CUs and 64-row tiles fit one
+// round, take 64 x 288 tiles (6 waves of 32 x 96) for those rows instead (one 784-token image: 156
+// tiles against 84). Plan override (qvl_set_gemm_plan's tile): 1 = one launch of 256 x 288 tiles,
+// 2 = the row split wherever there are two row tiles (the 128-row launch alone when no whole round
+// exists), 3 = the same with 64-row tiles for the rows past the whole rounds.
 constexpr double kRate256x288 = 1.50e6;
 
 template <bool LN>
@@ -1359,8 +1362,10 @@ static int launch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
   const int row_tiles = (rows + 255) / 256, tiles = row_tiles * tiles_n, tail = tiles % cus;
   const int whole_rows = (tiles / cus) * cus / tiles_n * 256;          // rows in whole rounds
   const int half_tiles = (rows - whole_rows + 127) / 128 * tiles_n;    // the rest in 128-row tiles
+  const int quarter_tiles = (rows - whole_rows + 63) / 64 * tiles_n;   // or in 64-row tiles
   const bool row_split = t_plan.split_mode != 1 && t_plan.tile != 1 && row_tiles >= 2 &&
-                         (t_plan.tile == 2 || (tail && 2 * tail <= cus && half_tiles <= cus));
+                         (t_plan.tile == 2 || t_plan.tile == 3 || (tail && 2 * tail <= cus && half_tiles <= cus));
+  const bool quarter = t_plan.tile == 3 || (t_plan.tile == 0 && 2 * half_tiles <= cus && quarter_tiles <= cus);
   if (!row_split) {
     const GemmPlan g = plan_gemm<256, 288>(p, cus, kRate256x288, t_plan.split_mode == 1 ? 1 : -1);
     return launch_gemm<256, 288, 4, 3, kEpiQkvRope72, LN>(p, g, stream);
@@ -1374,6 +1379,8 @@ static int launch_qkv_rope72(const GemmParams& p, hipStream_t stream) {
     const int rc = launch_gemm<256, 288, 4, 3, kEpiQkvRope72, LN>(a, plan_gemm<256, 288>(a, cus, kRate256x288, -1), stream);
     if (rc) return rc;
   }
+  if (quarter)
+    return launch_gemm<64, 288, 2, 3, kEpiQkvRope72, LN>(b, plan_gemm<64, 288>(b, cus, kRate256x288, -1), stream);
   return launch_gemm<128, 288, 4, 3, kEpiQkvRope72, LN>(b, plan_gemm<128, 288>(b, cus, kRate256x288, -1), stream);
 }
 

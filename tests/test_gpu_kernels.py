@@ -669,8 +669,9 @@ def vt_positions(n):
 def test_qkv_rotary72_row_split(pkg, lib, grids, fold):
     """The head_dim-72 qkv + rotary GEMM's row split (whole rounds of 256 x 288 tiles, the remaining
     rows as 128 x 288 tiles in a second launch: the cost rule's choice at config 4's 7056 tokens
-    and at 5500, forced by plan 2 elsewhere, where the 128-row launch may run alone) against one
-    launch of 256 x 288 tiles (plan 1): Q, K and V^T bit-identical (the k order is the same), every
+    and at 5500, forced by plan 2 elsewhere, where the 128-row launch may run alone; or as 64 x 288
+    tiles: the rule's choice at 728 tokens, forced by plan 3 elsewhere) against one launch of
+    256 x 288 tiles (plan 1): Q, K and V^T bit-identical (the k order is the same), every
     element written (the buffers start as NaN), padding rows and dims 72..87 zero; plain and with
     norm1 folded from row partials (the tower's path)."""
     cp = pkg.capi
@@ -701,7 +702,7 @@ def test_qkv_rotary72_row_split(pkg, lib, grids, fold):
         sg = xg.sum(-1)
         parts = torch.from_numpy(np.stack([sg, ((xg - sg[..., None] / 128) ** 2).sum(-1)], -1).astype(np.float32)).to(DEV)
     outs = {}
-    for tile in (1, 0, 2):
+    for tile in (1, 0, 2, 3):
         q = torch.full((H, Np, 88), float("nan"), dtype=torch.bfloat16, device=DEV)
         k = q.clone()
         vtm = torch.full((H, hd, Np), float("nan"), dtype=torch.bfloat16, device=DEV)
@@ -721,7 +722,7 @@ def test_qkv_rotary72_row_split(pkg, lib, grids, fold):
             cp.check(lib.qvl_set_gemm_plan(0, 0, 0))
         torch.cuda.synchronize()
         outs[tile] = (to_np(q), to_np(k), to_np(vtm))
-    for tile in (0, 2):
+    for tile in (0, 2, 3):
         for name, a, b_ in zip("qkv", outs[tile], outs[1]):
             assert np.isfinite(a).all(), (tile, name)
             np.testing.assert_array_equal(a, b_, err_msg=f"plan {tile} {name}")
