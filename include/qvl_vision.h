@@ -150,6 +150,13 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
  * (0, 0, 0) restores the defaults. No counterpart in the reference (it has no tile plans). */
 int qvl_set_gemm_plan(int32_t tile, int32_t split_mode, int32_t group_n);
 
+/* Key-group override for the head_dim-64 bf16 attention launched afterwards FROM THE CALLING THREAD
+ * ONLY (thread-local), for tests and tuning: 0 = the default rule (two groups of 4 waves per work
+ * item, each taking half of the item's key tiles and combined in LDS, where the items number at
+ * most 3x the compute units; else one group), 1 = one group, 2 = two groups. Outputs of 1 and 2 differ
+ * only in fp32 summation order. No counterpart in the reference. */
+int qvl_set_attention_plan(int32_t key_groups);
+
 /* LayerNorm over the last axis: fp32 mean / biased variance / rsqrt(var + eps), affine, cast
  * back (model.py:375-388). cols must be a multiple of 8 and <= 8192. bf16 or fp32. */
 int qvl_layer_norm(void* stream, int32_t dtype, const void* d_x, int64_t ldx, const float* d_gamma,

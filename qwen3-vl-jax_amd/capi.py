@@ -78,6 +78,7 @@ SIGNATURES = {
     "qvl_cast": (C.c_int, [_p, _i32, _p, _p, _i64]),
     "qvl_dense": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64]),
     "qvl_set_gemm_plan": (C.c_int, [_i32, _i32, _i32]),
+    "qvl_set_attention_plan": (C.c_int, [_i32]),
     "qvl_dense_workspace_size": (C.c_int, [C.POINTER(_sz)]),
     "qvl_dense_ws": (C.c_int, [_p, _i32, _i32, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _sz]),
     "qvl_layer_norm": (C.c_int, [_p, _i32, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _f32]),

@@ -57,12 +57,20 @@ __device__ __forceinline__ bf16x8 rowsum_selector(int lane) {
   return __builtin_bit_cast(bf16x8, u32x4{w, w, w, w});
 }
 
-__global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
+// KS = 2: a workgroup of 8 waves in two groups of 4; both groups take the same 128 queries, group g
+// the g-th half of the item's key tiles with a ring of its own, and group 1 hands its unnormalised
+// O, shift and row sums to group 0 through LDS at the end (O = O0 2^(m0 - m) + O1 2^(m1 - m), the
+// same for the sums), so short segments run half the key tiles per wave with no partial buffer
+// and no second launch. Both groups pass the same number of barriers: a group with one tile
+// fewer adds one.
+template <int KS>
+__global__ __launch_bounds__(256 * KS, 4) void attn_fwd_hd64_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ Vt,
     const int* __restrict__ tiles, int Np, int H, bf16* __restrict__ O, int64_t ldo, int n_whole,
     float* __restrict__ part) {
+  static_assert(KS == 1 || KS == 2, "one or two key groups");
   constexpr int kStage = 2 * kAttnBN * kHD;   // elements per stage: K [64][64] then V^T [64][64]
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
+  __shared__ __attribute__((aligned(16))) bf16 smem_all[KS * 2 * kStage];
 
   // Work item: (segment start, segment end, first query, head [| part, parts]); empty items pad
   // short queues.
@@ -74,8 +82,10 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   // parts live after the whole items and need the partial buffer
   if (seg_e <= seg_s || (parts && (!part || item < n_whole))) return;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = KS == 2 ? wave_all >> 2 : 0, wave = KS == 2 ? wave_all & 3 : wave_all;   // key group, wave in it
   const int l32 = lane & 31, hh = lane >> 5;
+  bf16* const smem = smem_all + grp * 2 * kStage;
 
   const size_t head_elems = (size_t)Np * kHD;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + head * head_elems, (uint32_t)(head_elems * 2));
@@ -122,9 +132,12 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   // Key tiles of 64 from the segment start rounded down to 64; a part of a split item takes its
   // share [t0, t1) of them.
   const int n_all = (seg_e - (seg_s & ~(kAttnBN - 1)) + kAttnBN - 1) / kAttnBN;
-  const int t0 = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
+  const int t0p = parts ? n_all * part_i / parts : 0, t1 = parts ? n_all * (part_i + 1) / parts : n_all;
+  // with two key groups: group 0 the first ceil(half) of them, group 1 the rest (possibly none)
+  const int n_steps = KS == 2 ? (t1 - t0p + 1) / 2 : t1 - t0p;
+  const int t0 = t0p + grp * n_steps;
+  const int n_kt = grp ? t1 - t0 : n_steps;
   const int k_begin = (seg_s & ~(kAttnBN - 1)) + t0 * kAttnBN;
-  const int n_kt = t1 - t0;
 
   // keys outside [seg_s, seg_e) -> -inf. Element r of a lane is key kb + 32 b + 4 hh + 8 (r / 4) + r % 4:
   // one unsigned range test against the lane's bounds per element (the offsets are constants).
@@ -220,21 +233,27 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
     __syncthreads();
   };
 
-  dma_tile(k_begin, 0);
+  if (KS == 1 || n_kt > 0) dma_tile(k_begin, 0);
   wait_dma();
   __syncthreads();
   // Tile it sits in stage it % 2: tile 0 (masked), then odd/even pairs so each stage is a constant.
-  step(std::true_type{}, int_c<0>{}, 0);
-  int it = 1;
-  for (; it + 2 < n_kt; it += 2) {
-    step(std::false_type{}, int_c<1>{}, it);
-    step(std::false_type{}, int_c<0>{}, it + 1);
+  // Every step ends in one barrier: n_kt of them, plus n_steps - n_kt for a group with fewer tiles.
+  if (KS == 1 || n_kt > 0) {
+    step(std::true_type{}, int_c<0>{}, 0);
+    int it = 1;
+    for (; it + 2 < n_kt; it += 2) {
+      step(std::false_type{}, int_c<1>{}, it);
+      step(std::false_type{}, int_c<0>{}, it + 1);
+    }
+    if (it == n_kt - 2) {
+      step(std::false_type{}, int_c<1>{}, it);
+      step(std::true_type{}, int_c<0>{}, it + 1);
+    } else if (it == n_kt - 1) {
+      step(std::true_type{}, int_c<1>{}, it);
+    }
   }
-  if (it == n_kt - 2) {
-    step(std::false_type{}, int_c<1>{}, it);
-    step(std::true_type{}, int_c<0>{}, it + 1);
-  } else if (it == n_kt - 1) {
-    step(std::true_type{}, int_c<1>{}, it);
+  if constexpr (KS == 2) {
+    for (int s = n_kt; s < n_steps; ++s) __syncthreads();
   }
 
   const float la = __shfl(lacc[0], lane & 15), lb = __shfl(lacc[1], lane & 15);
@@ -244,7 +263,9 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
   bool o_ok = true;
 #pragma unroll
   for (int r = 0; r < 16; ++r) o_ok = o_ok & (fabsf(oacc[0][r]) <= 0x1p120f) & (fabsf(oacc[1][r]) <= 0x1p120f);
-  if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !o_ok) != 0) {
+  if (KS == 2 && n_kt == 0) {
+    m_run = -INFINITY;   // an empty key group (KS = 2, one tile): weight 0 in the combine below
+  } else if (__builtin_amdgcn_ballot_w64(!(l_tot >= 0x1p-64f && l_tot <= 0x1p96f) || !o_ok) != 0) {
     // Some row's sum of 2^s left [2^-64, 2^96] (or O grew past 2^120, or anything overflowed):
     // recompute this wave's rows shifted by the exact row max, reading K and V^T from global
     // memory (the other waves may be done).
@@ -294,6 +315,34 @@ __global__ __launch_bounds__(256, 4) void attn_fwd_hd64_kernel(
       }
     }
     l_tot = l_run + __shfl_xor(l_run, 32);
+  }
+
+  if constexpr (KS == 2) {
+    // Group 1 hands (O, m, l) to the group 0 wave of the same queries through the free rings
+    // ([wave][register][lane] floats: consecutive lanes, consecutive banks); group 0 rescales both
+    // to the larger shift and adds (the shifts are 0 unless a group took the exact path).
+    float* const xo = reinterpret_cast<float*>(smem_all) + wave * (34 * 64);
+    if (grp == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        xo[r * 64 + lane] = oacc[0][r];
+        xo[(16 + r) * 64 + lane] = oacc[1][r];
+      }
+      xo[32 * 64 + lane] = m_run;
+      xo[33 * 64 + lane] = l_tot;
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = xo[32 * 64 + lane], l1 = xo[33 * 64 + lane];
+    const float m = fmaxf(m_run, m1);
+    const float w0 = exp2f(m_run - m), w1 = m1 == -INFINITY ? 0.f : exp2f(m1 - m);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      oacc[0][r] = oacc[0][r] * w0 + xo[r * 64 + lane] * w1;
+      oacc[1][r] = oacc[1][r] * w0 + xo[(16 + r) * 64 + lane] * w1;
+    }
+    l_tot = l_tot * w0 + l1 * w1;
+    m_run = m;
   }
 
   if (parts) {
@@ -767,12 +816,35 @@ __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
   }
 }
 
+// Key groups of the head_dim-64 kernel (thread-local override, qvl_set_attention_plan): 0 lets the
+// rule decide: two groups of 4 waves per item where the items number at most 3x the CUs (alone on
+// MI355X, 16 heads: one 784-token image 11.8 against 12.1 us, one of 1024 tokens 13.2 against 14.3,
+// config 1's four images 41.7 against 42.8), one group beyond (config 2's 2304 items: 166 against
+// 160 us, the combine and the extra barriers with no idle waves left to use).
+static thread_local int t_key_groups = 0;
+
+int attention_set_plan(int key_groups) {
+  if (key_groups < 0 || key_groups > 2)
+    return set_error(QVL_ERR_INVALID_ARG, "attention plan: key_groups=%d (0, 1 or 2)", key_groups);
+  t_key_groups = key_groups;
+  return QVL_OK;
+}
+
+static int attention_key_groups(int64_t n_items) {
+  if (t_key_groups) return t_key_groups;
+  return n_items <= 3 * (int64_t)gemm_device_cus() ? 2 : 1;
+}
+
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles,
                    int Np, int H, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole, float* part) {
   if (n_tiles == 0) return QVL_OK;
   if (n_whole < 0) n_whole = n_tiles;
-  hipLaunchKernelGGL(attn_fwd_hd64_kernel, dim3((unsigned)n_tiles), dim3(256), 0, stream,
-                     Qb, Kb, Vtb, d_tiles, Np, H, out, ldo, (int)n_whole, part);
+  if (attention_key_groups(n_tiles) == 2)
+    hipLaunchKernelGGL(attn_fwd_hd64_kernel<2>, dim3((unsigned)n_tiles), dim3(512), 0, stream,
+                       Qb, Kb, Vtb, d_tiles, Np, H, out, ldo, (int)n_whole, part);
+  else
+    hipLaunchKernelGGL(attn_fwd_hd64_kernel<1>, dim3((unsigned)n_tiles), dim3(256), 0, stream,
+                       Qb, Kb, Vtb, d_tiles, Np, H, out, ldo, (int)n_whole, part);
   int rc = check_launch("attn_fwd_hd64");
   if (rc || n_whole >= n_tiles || !part) return rc;
   return launch_combine<kHD>(d_tiles, n_tiles, n_whole, part, out, ldo, stream);

@@ -101,6 +101,8 @@ int qvl_set_gemm_plan(int32_t tile, int32_t split_mode, int32_t group_n) {
   return gemm_set_plan(tile, split_mode, group_n);
 }
 
+int qvl_set_attention_plan(int32_t key_groups) { return attention_set_plan(key_groups); }
+
 int qvl_dense_workspace_size(size_t* bytes) {
   if (!bytes) return set_error(QVL_ERR_INVALID_ARG, "bytes is NULL");
   *bytes = (size_t)gemm_partials_elems(gemm_device_cus()) * sizeof(float);

@@ -105,6 +105,7 @@ __host__ __device__ constexpr int rope_table_lds_bytes(int hd, bool ln = false) 
 }
 int rotary_pos_table(int n_pos, int head_dim, const float* inv_freq, uint32_t* table, hipStream_t stream);
 int gemm_set_plan(int tile, int split_mode, int group_n);
+int attention_set_plan(int key_groups);
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles, int Np,
                    int H, bf16* out, int64_t ldo, hipStream_t stream, int64_t n_whole = -1, float* part = nullptr);
 int attention_relayout_hd64(const bf16* q, const bf16* k, const bf16* v, int64_t ld, const f32x2* cs, int N, int Np,

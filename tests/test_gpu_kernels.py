@@ -478,7 +478,9 @@ def test_attention_late_score_spike(pkg, lib, hd, spike):
 
 def _run_attention_lists(pkg, lib, q, k, vt, cu, H, hd):
     """qvl_attention_headmajor on the plain work list and qvl_attention_headmajor_split on the
-    split list of 40 CUs (when it splits): [(label, bf16 output as fp32 numpy)]."""
+    split list of 40 CUs (when it splits), head_dim 64 under both key-group plans (one group of 4
+    waves per item; two, each taking half of the item's key tiles): [(label, bf16 output as fp32
+    numpy)]."""
     cp = pkg.capi
     N = int(cu[-1])
     lists = [(pkg.vision._worklist(lib, cu, H), None)]
@@ -486,22 +488,52 @@ def _run_attention_lists(pkg, lib, q, k, vt, cu, H, hd):
     if len(split) > n_whole:
         lists.append((split, n_whole))
     outs = []
-    for items, nw in lists:
-        t = torch.from_numpy(np.ascontiguousarray(items)).to(DEV)
-        out = torch.full((N, H * hd), float("nan"), dtype=torch.bfloat16, device=DEV)
-        if nw is None:
-            cp.check(lib.qvl_attention_headmajor(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(), vt.data_ptr(),
-                                                 t.data_ptr(), len(items), N, H, hd, out.data_ptr(), H * hd))
-        else:
-            nb = C.c_size_t()
-            cp.check(lib.qvl_attention_split_workspace_size(hd, len(items), nw, C.byref(nb)))
-            ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=DEV)
-            cp.check(lib.qvl_attention_headmajor_split(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(),
-                                                       vt.data_ptr(), t.data_ptr(), len(items), nw, N, H, hd,
-                                                       out.data_ptr(), H * hd, ws.data_ptr(), nb.value))
-        torch.cuda.synchronize()
-        outs.append(("whole" if nw is None else "split", to_np(out)))
+    for groups in ((1, 2) if hd == 64 else (0,)):
+        for items, nw in lists:
+            t = torch.from_numpy(np.ascontiguousarray(items)).to(DEV)
+            out = torch.full((N, H * hd), float("nan"), dtype=torch.bfloat16, device=DEV)
+            try:
+                cp.check(lib.qvl_set_attention_plan(groups))
+                if nw is None:
+                    cp.check(lib.qvl_attention_headmajor(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(),
+                                                         vt.data_ptr(), t.data_ptr(), len(items), N, H, hd,
+                                                         out.data_ptr(), H * hd))
+                else:
+                    nb = C.c_size_t()
+                    cp.check(lib.qvl_attention_split_workspace_size(hd, len(items), nw, C.byref(nb)))
+                    ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=DEV)
+                    cp.check(lib.qvl_attention_headmajor_split(stream(), cp.QVL_DTYPE_BF16, q.data_ptr(), k.data_ptr(),
+                                                               vt.data_ptr(), t.data_ptr(), len(items), nw, N, H, hd,
+                                                               out.data_ptr(), H * hd, ws.data_ptr(), nb.value))
+            finally:
+                cp.check(lib.qvl_set_attention_plan(0))
+            torch.cuda.synchronize()
+            outs.append((("whole" if nw is None else "split") + f"/groups{groups}", to_np(out)))
     return outs
+
+
+@pytest.mark.parametrize("cu,H", [([0, 784], 16),                                   # one 448x448 image
+                                  ([0, 1024, 1984, 2240, 4544], 16),                # config 1's segments
+                                  ([0, 1, 65, 129, 130, 300, 1000], 4),              # 1 / 1 / 2 / 1 / 3 / 11 key tiles
+                                  ([0, 4096, 8192, 18432], 2)])
+def test_attention_key_groups_match(pkg, lib, cu, H):
+    """Head_dim-64 attention with two key groups per work item (8 waves: group 1 takes the second
+    half of the item's key tiles and hands its O, shift and row sums to group 0 through LDS; a
+    1-tile item leaves group 1 empty) against one group, on the plain and the split work lists:
+    every row finite, rel-L2 <= 3e-3 against one group (the bf16 rounding of the output and the
+    fp32 order of the two halves' sums differ) and <= 1e-2 against an fp32 reference per
+    segment. The default rule takes two groups where the items number at most 3x the CUs."""
+    cu = np.array(cu, np.int32)
+    N = int(cu[-1])
+    q, k, vt, ref = _headmajor_operands(H, 64, cu, seed=N + H)
+    outs = dict(_run_attention_lists(pkg, lib, q, k, vt, cu, H, 64))
+    for label, got in outs.items():
+        assert np.isfinite(got).all(), label
+        for s, e in zip(cu[:-1], cu[1:]):
+            assert rel_l2(got[s:e], ref[s:e]) <= 1e-2, (label, s, e)
+    for lst in ("whole", "split"):
+        if f"{lst}/groups1" in outs:
+            assert rel_l2(outs[f"{lst}/groups2"], outs[f"{lst}/groups1"]) <= 3e-3, lst
 
 
 @pytest.mark.parametrize("hd", [64, 72])
