@@ -60,7 +60,10 @@ def patchify_frames(frames, patch_size: int, spatial_merge_size: int, temporal_p
     if isinstance(frames, np.ndarray):
         if frames.dtype != np.uint8:
             raise TypeError("frames must be uint8 (the reference converts through PIL RGB, sample.py:62-76)")
-        t = torch.from_numpy(np.ascontiguousarray(frames)).to(device)
+        arr = np.ascontiguousarray(frames)
+        if not arr.flags.writeable:        # e.g. np.asarray of a PIL image; torch wants a writable buffer
+            arr = arr.copy()
+        t = torch.from_numpy(arr).to(device)
     else:
         if frames.dtype != torch.uint8:
             raise TypeError("frames must be uint8")
