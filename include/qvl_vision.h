@@ -153,7 +153,7 @@ int qvl_set_gemm_plan(int32_t tile, int32_t split_mode, int32_t group_n);
 /* Key-group override for the head_dim-64 bf16 attention launched afterwards FROM THE CALLING THREAD
  * ONLY (thread-local), for tests and tuning: 0 = the default rule (two groups of 4 waves per work
  * item, each taking half of the item's key tiles and combined in LDS, where the items number at
- * most 3x the compute units; else one group), 1 = one group, 2 = two groups. Outputs of 1 and 2 differ
+ * most 2x the compute units; else one group), 1 = one group, 2 = two groups. Outputs of 1 and 2 differ
  * only in fp32 summation order. No counterpart in the reference. */
 int qvl_set_attention_plan(int32_t key_groups);
 

@@ -817,10 +817,12 @@ __global__ __launch_bounds__(256) void attn_relayout_hd64_kernel(
 }
 
 // Key groups of the head_dim-64 kernel (thread-local override, qvl_set_attention_plan): 0 lets the
-// rule decide: two groups of 4 waves per item where the items number at most 3x the CUs (alone on
-// MI355X, 16 heads: one 784-token image 11.8 against 12.1 us, one of 1024 tokens 13.2 against 14.3,
-// config 1's four images 41.7 against 42.8), one group beyond (config 2's 2304 items: 166 against
-// 160 us, the combine and the extra barriers with no idle waves left to use).
+// rule decide: two groups of 4 waves per item where the items number at most 2x the CUs, so every
+// item starts at once either way (two 8-wave workgroups per CU against four of 4 waves). Alone on
+// MI355X, 16 heads: one 784-token image 11.8 against 12.1 us, one of 1024 tokens 13.2 against 14.3.
+// Past that, part of the items wait for a slot: six 1024-token images (768 items) 36.1 against
+// 32.5 us, config 3's 1024 items 49.3 against 41.6, config 2's 2304 items 166 against 160 (config
+// 1's 576 uneven items were the exception, 42.5 against 43.7).
 static thread_local int t_key_groups = 0;
 
 int attention_set_plan(int key_groups) {
@@ -832,7 +834,7 @@ int attention_set_plan(int key_groups) {
 
 static int attention_key_groups(int64_t n_items) {
   if (t_key_groups) return t_key_groups;
-  return n_items <= 3 * (int64_t)gemm_device_cus() ? 2 : 1;
+  return n_items <= 2 * (int64_t)gemm_device_cus() ? 2 : 1;
 }
 
 int attention_hd64(const bf16* Qb, const bf16* Kb, const bf16* Vtb, const int* d_tiles, int64_t n_tiles,

@@ -522,7 +522,7 @@ def test_attention_key_groups_match(pkg, lib, cu, H):
     1-tile item leaves group 1 empty) against one group, on the plain and the split work lists:
     every row finite, rel-L2 <= 3e-3 against one group (the bf16 rounding of the output and the
     fp32 order of the two halves' sums differ) and <= 1e-2 against an fp32 reference per
-    segment. The default rule takes two groups where the items number at most 3x the CUs."""
+    segment. The default rule takes two groups where the items number at most 2x the CUs."""
     cu = np.array(cu, np.int32)
     N = int(cu[-1])
     q, k, vt, ref = _headmajor_operands(H, 64, cu, seed=N + H)
