@@ -132,13 +132,15 @@ def test_pos_embed_vs_oracle(pkg, lib, grids):
 
 
 @pytest.mark.parametrize("grids,k,parts", [([(1, 48, 48), (1, 48, 48)], 1536, True), ([(1, 84, 84), (3, 10, 6)], 1536, True),
-                                           ([(8, 32, 32)], 1216, False), ([(1, 20, 36)], 64, True)])
+                                           ([(8, 32, 32)], 1216, False), ([(1, 20, 36)], 64, True),
+                                           ([(1, 48, 48)], 1536, True)])
 def test_dense_pos_embed_equals_pos_embed_then_residual(pkg, lib, grids, k, parts):
     """qvl_dense_pos_embed_ws (the patch embed with the pos-embed gathered in its epilogue, the
     tower's bf16 path) against qvl_pos_embed followed by the residual Dense (qvl_dense_rowstats_ws,
     or qvl_dense_ws with the split-K tail off): the output and the row partials bit for bit, on
     config 2's two-image grid (48 x 48: single-tap rows), config 4's grid with a ragged image
-    (four live taps per row), config 3's video (the jnp.repeat frame quirk) and a short K."""
+    (four live taps per row), config 3's video (the jnp.repeat frame quirk), a short K and one
+    768 x 768 image (2304 rows: 128 x 128 tiles by the small-grid rule)."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
     N, D = m.n_tokens, 1024
