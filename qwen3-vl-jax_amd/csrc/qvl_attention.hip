@@ -7,8 +7,9 @@
 //   Vt[H][64][Np]  V transposed, token axis contiguous, keys at positions vt_pos(key)
 // Rows / positions [n_tokens, Np) are zero.
 //
-// Each workgroup (4 waves) owns one 128-query tile of one segment and one head; each wave owns
-// 32 queries. Key tiles of 64 start at the segment start rounded down to 64, so every K / V^T
+// Each workgroup (4 waves; 8 waves in two key groups on small lists, attn_fwd_hd64_kernel<2>) owns
+// one 128-query tile of one segment and one head; each wave owns 32 queries. Key tiles of 64 start
+// at the segment start rounded down to 64, so every K / V^T
 // tile is 64-aligned and arrives by LDS DMA (16-byte chunks, XOR swizzle folded into the
 // source address); only the first and last tiles carry keys outside the segment and they are
 // peeled off the steady-state loop, which has no masking.
