@@ -201,6 +201,32 @@ def test_config3_video_reduced_depth(pkg, params2b):
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
 
 
+@pytest.mark.parametrize("shape", ["2b", "8b"])
+def test_random_small_grids_vs_oracle(pkg, params2b, params8b, shape):
+    """Seeded random small batches (1-3 images or short videos, even h and w up to 48, at most 2500
+    patches): the small-grid paths (128x128 GEMM tiles unsplit and split along K, the head_dim-72
+    qkv's 64-row tiles, two key groups per attention item) take part alongside the larger tiles.
+    The first 2 blocks + a deepstack tap after block 1 + the merger: tokens and deepstack within
+    rel-L2 1e-2 of the oracle's bf16 restatement, every value finite."""
+    rng = np.random.default_rng(2027 if shape == "2b" else 2028)
+    spec, ospec = specs(pkg, depth=2, ds=(1,), shape=shape)
+    params = params2b if shape == "2b" else params8b
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="bfloat16").bind(params)
+    for case in range(5):
+        while True:
+            grids = [(int(rng.choice([1, 1, 1, 2, 3])), 2 * int(rng.integers(1, 25)), 2 * int(rng.integers(1, 25)))
+                     for _ in range(int(rng.integers(1, 4)))]
+            if sum(t * h * w for t, h, w in grids) <= 2500:
+                break
+        px = pixels(grids, 100 + case)
+        ref = vt.encode_vision(params, px, grids, ospec, "bf16")
+        tok, ds = tower(px, np.array(grids, np.int32))
+        tok, ds0 = to_np(tok), to_np(ds[0])
+        assert np.isfinite(tok).all() and np.isfinite(ds0).all(), grids
+        assert rel_l2(tok, ref.tokens) <= TOL, (grids, rel_l2(tok, ref.tokens))
+        assert rel_l2(ds0, ref.deepstack[0]) <= TOL, (grids, rel_l2(ds0, ref.deepstack[0]))
+
+
 def test_config4_grid_reduced_depth(pkg, params8b):
     """BASELINE config 4's input (one 1344x1344 image, grid 1x84x84 = 7056 patches, one segment) on
     the 8B-shape tower, first 2 blocks + a deepstack tap after block 1 + the merger: rel-L2 <= 1e-2."""
