@@ -288,3 +288,31 @@ def test_fp32_8b_shape_reduced_depth(pkg):
     tok, ds = tower(px, np.array(grids, np.int32))
     assert rel_l2(to_np(tok), ref.tokens) <= TOL
     assert rel_l2(to_np(ds[0]), ref.deepstack[0]) <= TOL
+
+
+@pytest.mark.parametrize("shape", ["2b", "8b"])
+def test_fp32_random_small_grids_vs_fp64(pkg, shape):
+    """Seeded random small batches (1-3 images or short videos, even h and w up to 40, at most 2000
+    patches) through the fp32 tower: the split-K GEMM plans and the split attention lists at
+    varied sizes. The first 2 blocks + a deepstack tap after block 1 + the merger: tokens and
+    deepstack within rel-L2 1e-4 of the fp64 oracle, every value finite."""
+    spec = pkg.spec_2b() if shape == "2b" else pkg.spec_8b()
+    spec.depth = 2
+    spec.deepstack_visual_indexes = (1,)
+    params = pkg.random_params(spec, seed=23 if shape == "2b" else 24)
+    tower = pkg.Qwen3VisionTransformer(spec, dtype="float32").bind(params)
+    rng = np.random.default_rng(2029 if shape == "2b" else 2030)
+    for case in range(4):
+        while True:
+            grids = [(int(rng.choice([1, 1, 1, 2])), 2 * int(rng.integers(1, 21)), 2 * int(rng.integers(1, 21)))
+                     for _ in range(int(rng.integers(1, 4)))]
+            if sum(t * h * w for t, h, w in grids) <= 2000:
+                break
+        n = sum(t * h * w for t, h, w in grids)
+        px = np.random.default_rng(200 + case).standard_normal((n, 1536)).astype(np.float32)
+        ref = vt.encode_vision(params, px, grids, _ospec(spec), "fp64")
+        tok, ds = tower(px, np.array(grids, np.int32))
+        tok, ds0 = to_np(tok), to_np(ds[0])
+        assert np.isfinite(tok).all() and np.isfinite(ds0).all(), grids
+        assert rel_l2(tok, ref.tokens) <= TOL, (grids, rel_l2(tok, ref.tokens))
+        assert rel_l2(ds0, ref.deepstack[0]) <= TOL, (grids, rel_l2(ds0, ref.deepstack[0]))
