@@ -139,8 +139,10 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
  *   tile       0 = cost model (default), 1 = 288x256, 2 = 256x256, 3 = 256x128, 4 = 288x128,
  *                5 = row split (the rows of whole rounds of 288x256 tiles, then the rest as
  *                256x128 tiles in a second launch; 288x256 where no such split exists),
- *                6 = 128x128 tiles (chosen by the default plan on small grids with K <= 1536)
- *                (the head_dim-64 rotary qkv epilogue takes 1-3, 5 and 6 and maps 4 to 3; for the
+ *                6 = 128x128 tiles (chosen by the default plan on small grids with K <= 1536),
+ *                7 = 64x192 tiles (the head_dim-64 rotary qkv GEMM only: its default where one
+ *                round of them fits the compute units)
+ *                (the head_dim-64 rotary qkv epilogue takes 1-3 and 5-7 and maps 4 to 3; for the
  *                head_dim-72 one, 0 = whole rounds of 256x288 tiles and the rest in 128x288
  *                tiles where that fits one round (64x288 where those fill at most half of it),
  *                1 = 256x288 tiles only, 2 = that row split wherever there are two 256-row

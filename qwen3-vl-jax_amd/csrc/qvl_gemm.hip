@@ -1193,7 +1193,7 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 
 // Tile-plan override of the calling thread (qvl_set_gemm_plan): tile 0 = the cost model's
 // choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128, 5 = the row split (whole rounds of 288x256,
-// the rest 256x128), 6 = 128x128; split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
+// the rest 256x128), 6 = 128x128, 7 = 64x192 (the head_dim-64 rotary qkv GEMM only); split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
 // group_n 0 = the default panel width. Thread-local, so a test pinning a plan on one thread does
 // not change another thread's launches.
 struct ForcedPlan { int tile = 0, split_mode = 0, group_n = 0; };
@@ -1293,8 +1293,17 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   // proj, 56 tiles in 4 parts, 15.4 against 18.9 us for 288x128 tiles in 8 parts. Cases the rule
   // leaves to the cost model were measured slower on 128x128: 1568 rows' proj unsplit (104 tiles)
   // 22.9 against 20.4 us; the mergers' K = 4096 GEMMs at 196 rows 25.2 / 26.8 against 20.3 / 24.2 us.
+  // The head_dim-64 rotary qkv GEMM takes 64x192 tiles (6 waves of 32x64, whole heads; tiles may
+  // straddle the q | k | v boundary, the epilogue picks the target per head) wherever one round of
+  // them fits the CUs: alone on MI355X (1024 x 3072 x 1024 with norm1 folded), 196 / 400 / 576 /
+  // 784 / 1024 tokens 14.3 / 14.5 / 14.7 / 15.3 / 15.4 us against 19.8 / 20.2 / 20.2 / 17.0 / 17.5
+  // for the plans below; at 1568 tokens and more (two rounds) the plans below stay ahead.
   GemmPlan e{};
   if (pick == 6) e = plan_gemm<128, 128>(p, cus, kRate128x128, f.split_mode);
+  if constexpr (EPI == kEpiQkvRope) {
+    const int tiles64 = ((rows + 63) / 64) * ((p.N + 191) / 192);
+    if (pick == 0 && p.K <= kSmallTileMaxK && tiles64 <= cus && !p.row0 && !p.row1) pick = 7;
+  }
   const int tiles128 = ((rows + 127) / 128) * ((p.N + 127) / 128);
   if (pick == 0 && p.K <= kSmallTileMaxK && !p.row0 && !p.row1) {
     if (2 * tiles128 >= cus && tiles128 <= cus) {
@@ -1322,6 +1331,9 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   if (pick == 1) return launch_gemm<288, 256, 3, 4, EPI, LN>(p, a, stream);
   if (pick == 6) return launch_gemm<128, 128, 2, 2, EPI, LN>(p, e, stream);
   if constexpr (EPI == kEpiQkvRope) {
+    if (pick == 7) return launch_gemm<64, 192, 2, 3, EPI, LN>(p, plan_gemm<64, 192>(p, cus, kRate128x128, -1), stream);
+  }
+  if constexpr (EPI == kEpiQkvRope) {
     if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
     return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
   } else {
@@ -1332,7 +1344,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
 }
 
 int gemm_set_plan(int tile, int split_mode, int group_n) {
-  if (tile < 0 || tile > 6 || split_mode < -1 || split_mode > 1 || group_n < 0)
+  if (tile < 0 || tile > 7 || split_mode < -1 || split_mode > 1 || group_n < 0)
     return set_error(QVL_ERR_INVALID_ARG, "gemm plan: tile=%d split_mode=%d group_n=%d", tile, split_mode, group_n);
   t_plan.tile = tile;
   t_plan.split_mode = split_mode;

@@ -582,7 +582,7 @@ def test_attention_exact_recompute_triggers(pkg, lib, hd, case):
         assert rel_l2(got[r], ref[r]) <= 1e-2, label
 
 
-_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4, "rowsplit": 5, "128x128": 6}
+_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4, "rowsplit": 5, "128x128": 6, "64x192": 7}
 
 
 def set_plan(lib, cp, plan):
@@ -651,10 +651,11 @@ def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
                                    [(1, 28, 28)]])
 def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     """The fused qkv+rotary GEMM writes bit-identical head-major Q/K/V^T (including the zeroed
-    padding rows [N, Np)) with 288x256, 256x256, 256x128 and 128x128 tiles (the last two with the
-    three-stage operand ring and one head per wave; 128x128 is the cost model's choice for one
-    784-token image) and the row split (config 3's 8192 tokens: 252 tiles of 288x256, then 216 of
-    256x128); with the tail split within rel-L2 2e-3."""
+    padding rows [N, Np)) with 288x256, 256x256, 256x128, 128x128 and 64x192 tiles (the last three
+    with the three-stage operand ring and one head per wave; 64x192 tiles straddle the q | k
+    boundary at D = 1024 and are the default for one 784-token image and the mixed small grid)
+    and the row split (config 3's 8192 tokens: 252 tiles of 288x256, then 216 of 256x128); with
+    the tail split within rel-L2 2e-3."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
     N, D, H = m.n_tokens, 1024, 16
@@ -671,7 +672,7 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     Np = -(-N // 64) * 64
     outs = {}
     for plan in ["256x256:nosplit", "288x256:nosplit", "256x128:nosplit", "rowsplit:nosplit", "128x128:nosplit",
-                 "256x256:split", "288x256:split", "256x128:split", "128x128:split", None]:
+                 "64x192:nosplit", "256x256:split", "288x256:split", "256x128:split", "128x128:split", None]:
         set_plan(lib, cp, plan)
         q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
         k, vt = q.clone(), q.clone()
