@@ -141,8 +141,9 @@ int qvl_dense_ws(void* stream, int32_t dtype, int32_t epilogue, const void* d_x,
  *                256x128 tiles in a second launch; 288x256 where no such split exists),
  *                6 = 128x128 tiles (chosen by the default plan on small grids with K <= 1536),
  *                7 = 64x192 tiles (the head_dim-64 rotary qkv GEMM only: its default where one
- *                round of them fits the compute units)
- *                (the head_dim-64 rotary qkv epilogue takes 1-3 and 5-7 and maps 4 to 3; for the
+ *                round of them fits the compute units), 8 = 64x128 tiles (the patch embed's
+ *                default on small grids)
+ *                (the head_dim-64 rotary qkv epilogue takes 1-3 and 5-8 and maps 4 to 3; for the
  *                head_dim-72 one, 0 = whole rounds of 256x288 tiles and the rest in 128x288
  *                tiles where that fits one round (64x288 where those fill at most half of it),
  *                1 = 256x288 tiles only, 2 = that row split wherever there are two 256-row

@@ -1193,7 +1193,8 @@ static GemmPlan plan_gemm(const GemmParams& p, int cus, double macs_per_us_per_c
 
 // Tile-plan override of the calling thread (qvl_set_gemm_plan): tile 0 = the cost model's
 // choice, 1..4 = 288x256 | 256x256 | 256x128 | 288x128, 5 = the row split (whole rounds of 288x256,
-// the rest 256x128), 6 = 128x128, 7 = 64x192 (the head_dim-64 rotary qkv GEMM only); split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
+// the rest 256x128), 6 = 128x128, 7 = 64x192 (the head_dim-64 rotary qkv GEMM only), 8 = 64x128;
+// split_mode -1 forbids, 1 forces, 0 lets the cost model decide the tail split;
 // group_n 0 = the default panel width. Thread-local, so a test pinning a plan on one thread does
 // not change another thread's launches.
 struct ForcedPlan { int tile = 0, split_mode = 0, group_n = 0; };
@@ -1315,6 +1316,10 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
         pick = 6;
         e = sp;
       }
+    } else if (EPI == kEpiBiasPosEmbed && ((rows + 63) / 64) * ((p.N + 127) / 128) <= cus) {
+      // the patch embed cannot split K: its small grids take 64x128 tiles (4 waves of 32x64) that
+      // fit one round (one 784-token image: 104 tiles, 23.5 against 37.9 us for 32 of 256x128)
+      pick = 8;
     }
   }
   if (pick == 0) {
@@ -1333,6 +1338,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   if constexpr (EPI == kEpiQkvRope) {
     if (pick == 7) return launch_gemm<64, 192, 2, 3, EPI, LN>(p, plan_gemm<64, 192>(p, cus, kRate128x128, -1), stream);
   }
+  if (pick == 8) return launch_gemm<64, 128, 2, 2, EPI, LN>(p, plan_gemm<64, 128>(p, cus, kRate128x128, f.split_mode), stream);
   if constexpr (EPI == kEpiQkvRope) {
     if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
     return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
@@ -1344,7 +1350,7 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
 }
 
 int gemm_set_plan(int tile, int split_mode, int group_n) {
-  if (tile < 0 || tile > 7 || split_mode < -1 || split_mode > 1 || group_n < 0)
+  if (tile < 0 || tile > 8 || split_mode < -1 || split_mode > 1 || group_n < 0)
     return set_error(QVL_ERR_INVALID_ARG, "gemm plan: tile=%d split_mode=%d group_n=%d", tile, split_mode, group_n);
   t_plan.tile = tile;
   t_plan.split_mode = split_mode;

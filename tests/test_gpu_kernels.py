@@ -133,14 +133,15 @@ def test_pos_embed_vs_oracle(pkg, lib, grids):
 
 @pytest.mark.parametrize("grids,k,parts", [([(1, 48, 48), (1, 48, 48)], 1536, True), ([(1, 84, 84), (3, 10, 6)], 1536, True),
                                            ([(8, 32, 32)], 1216, False), ([(1, 20, 36)], 64, True),
-                                           ([(1, 48, 48)], 1536, True)])
+                                           ([(1, 48, 48)], 1536, True), ([(1, 28, 28)], 1536, True)])
 def test_dense_pos_embed_equals_pos_embed_then_residual(pkg, lib, grids, k, parts):
     """qvl_dense_pos_embed_ws (the patch embed with the pos-embed gathered in its epilogue, the
     tower's bf16 path) against qvl_pos_embed followed by the residual Dense (qvl_dense_rowstats_ws,
     or qvl_dense_ws with the split-K tail off): the output and the row partials bit for bit, on
     config 2's two-image grid (48 x 48: single-tap rows), config 4's grid with a ragged image
     (four live taps per row), config 3's video (the jnp.repeat frame quirk), a short K and one
-    768 x 768 image (2304 rows: 128 x 128 tiles by the small-grid rule)."""
+    768 x 768 image (2304 rows: 128 x 128 tiles by the small-grid rule) and a 448 x 448 one (784 rows:
+    64 x 128 tiles)."""
     cp = pkg.capi
     m = pkg.grid_metadata(grids)
     N, D = m.n_tokens, 1024
@@ -582,7 +583,8 @@ def test_attention_exact_recompute_triggers(pkg, lib, hd, case):
         assert rel_l2(got[r], ref[r]) <= 1e-2, label
 
 
-_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4, "rowsplit": 5, "128x128": 6, "64x192": 7}
+_TILES = {"288x256": 1, "256x256": 2, "256x128": 3, "288x128": 4, "rowsplit": 5, "128x128": 6, "64x192": 7,
+          "64x128": 8}
 
 
 def set_plan(lib, cp, plan):
@@ -595,7 +597,8 @@ def set_plan(lib, cp, plan):
 
 
 PLANS = ["288x256:nosplit", "256x256:nosplit", "256x128:nosplit", "288x128:nosplit", "rowsplit:nosplit",
-         "128x128:nosplit", "288x256:split", "256x256:split", "256x128:split", "288x128:split", "128x128:split"]
+         "128x128:nosplit", "64x128:nosplit", "288x256:split", "256x256:split", "256x128:split", "288x128:split",
+         "128x128:split", "64x128:split"]
 
 
 def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
@@ -611,8 +614,8 @@ def dense_ws(lib, cp, epi, x, w, bias, res, m, n, k, ws):
                                    (18000, 1152, 4352), (300, 192, 64), (1000, 640, 192), (8192, 3072, 1024),
                                    (784, 4096, 1024)])
 def test_dense_tile_plans_agree(pkg, lib, epi, m, n, k):
-    """Every tile shape (288x256 / 256x256 / 256x128 / 288x128 / 128x128, the last the cost model's
-    choice at 784 x 4096 x 1024) and the row split (whole rounds of
+    """Every tile shape (288x256 / 256x256 / 256x128 / 288x128 / 128x128 / 64x128, 128x128 the
+    default at 784 x 4096 x 1024) and the row split (whole rounds of
     288x256 tiles, the remaining rows as 256x128 tiles in a second launch: taken at 18000 and 8192
     rows, elsewhere it falls back to 288x256) gives bit-identical results without the tail split
     (same K order per output); with the split (fp32 partials summed by the reduce kernel) within
@@ -672,7 +675,8 @@ def test_qkv_rotary_tile_plans_agree(pkg, lib, grids):
     Np = -(-N // 64) * 64
     outs = {}
     for plan in ["256x256:nosplit", "288x256:nosplit", "256x128:nosplit", "rowsplit:nosplit", "128x128:nosplit",
-                 "64x192:nosplit", "256x256:split", "288x256:split", "256x128:split", "128x128:split", None]:
+                 "64x192:nosplit", "64x128:nosplit", "256x256:split", "288x256:split", "256x128:split", "128x128:split",
+                 "64x128:split", None]:
         set_plan(lib, cp, plan)
         q = torch.full((H, Np, 64), 7.0, dtype=torch.bfloat16, device=DEV)      # padding must be overwritten
         k, vt = q.clone(), q.clone()

@@ -297,11 +297,11 @@ def rowstats_dense(lib, cp, x, w, bias, res, n, k, ws, nb):
 @pytest.mark.parametrize("split", [-1, 1])
 @pytest.mark.parametrize("m,n,k,plan", [(1000, 1024, 4096, 0), (517, 1152, 1152, 0), (600, 1024, 1024, 1),
                                         (300, 1280, 1024, 3), (784, 1024, 4096, 0), (784, 1024, 1024, 6),
-                                        (784, 1024, 1024, 0)])
+                                        (784, 1024, 1024, 0), (784, 1024, 1024, 8)])
 def test_dense_rowstats(pkg, lib, m, n, k, plan, split):
     """qvl_dense_rowstats_ws: the residual Dense's output bit for bit as qvl_dense_ws gives it under the
-    same pinned plan (tile 288x256 for plan 1, 256x128 for plan 3, 128x128 for plan 6, the cost
-    model's for 0; split -1
+    same pinned plan (tile 288x256 for plan 1, 256x128 for plan 3, 128x128 for plan 6, 64x128 for
+    plan 8, the default for 0; split -1
     forbids the tail split-K, 1 forces it: then the tail tiles' rows come from the split-K reduction,
     which writes their partials too), and per 128-column group of each row the sum and the sum of
     squared deviations of those bf16 outputs within fp32 summation error of fp64 (rows with offsets
