@@ -1322,6 +1322,18 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
       pick = 8;
     }
   }
+  // A folded LayerNorm over more than 16 row groups (the deepstack mergers' 4-token rows: 32 or 36)
+  // combines each row's partials in the workgroup's prologue; on small grids 64-row tiles split
+  // along K spread that over 4x the workgroups (one 784-token image's deepstack fc1, K = 4096:
+  // 27.2 against 33.4 us for 256x128 tiles split 8 ways).
+  if (pick == 0 && LN && p.ln_part && p.ln_groups > 16 && f.split_mode >= 0 && !p.row0 && !p.row1 &&
+      2 * ((rows + 63) / 64) * ((p.N + 127) / 128) <= cus) {
+    const GemmPlan sp = plan_gemm<64, 128>(p, cus, kRate128x128, 1);
+    if (8 * sp.tail * sp.split >= 7 * cus) {
+      pick = 8;
+      e = sp;
+    }
+  }
   if (pick == 0) {
     const double cost[5] = {a.cost_us, b.cost_us, c.cost_us, EPI == kEpiQkvRope ? 1e30 : d.cost_us, r_cost};
     pick = 1;
@@ -1338,7 +1350,9 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   if constexpr (EPI == kEpiQkvRope) {
     if (pick == 7) return launch_gemm<64, 192, 2, 3, EPI, LN>(p, plan_gemm<64, 192>(p, cus, kRate128x128, -1), stream);
   }
-  if (pick == 8) return launch_gemm<64, 128, 2, 2, EPI, LN>(p, plan_gemm<64, 128>(p, cus, kRate128x128, f.split_mode), stream);
+  if (pick == 8)
+    return launch_gemm<64, 128, 2, 2, EPI, LN>(p, e.full || e.tail ? e : plan_gemm<64, 128>(p, cus, kRate128x128, f.split_mode),
+                                               stream);
   if constexpr (EPI == kEpiQkvRope) {
     if (pick == 3) return launch_gemm<256, 128, 4, 2, EPI, LN>(p, c, stream);
     return launch_gemm<256, 256, 4, 2, EPI, LN>(p, b, stream);
