@@ -1287,13 +1287,14 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   int pick = f.tile;
   if (EPI == kEpiQkvRope && pick == 4) pick = 3;     // 64-feature heads need TN % 64 == 0 (288x128: 32)
   if (pick == 5 && !can_split) pick = 1;
-  // Small grids, K <= 1536: 128x128 tiles (4 waves of 64x64, one per SIMD) unsplit where one round
-  // of them covers half to all of the CUs, or split along K where up to 8 parts of fewer tiles fill
-  // at least 7/8 of them. The larger tiles there leave most CUs idle or need long split-K tails.
-  // One 784-token image's forward: qkv 17.7 against 22.1 us (256x128), fc1 16.1 against 21.3;
-  // proj, 56 tiles in 4 parts, 15.4 against 18.9 us for 288x128 tiles in 8 parts. Cases the rule
-  // leaves to the cost model were measured slower on 128x128: 1568 rows' proj unsplit (104 tiles)
-  // 22.9 against 20.4 us; the mergers' K = 4096 GEMMs at 196 rows 25.2 / 26.8 against 20.3 / 24.2 us.
+  // Small grids, K <= 1536: where one round of 128x128 tiles would cover half to all of the CUs,
+  // 64x128 tiles unsplit (4 waves of 32x64); where fewer 128x128 tiles split along K in up to 8
+  // parts fill at least 7/8 of the CUs, those (4 waves of 64x64). The larger tiles there leave most
+  // CUs idle or need long split-K tails. One 784-token image's forward: fc1 16.1 us on 128x128
+  // against 21.3 on 256x128 (64x128: below); proj, 56 tiles in 4 parts, 15.4 against 18.9 us for
+  // 288x128 tiles in 8 parts. Cases the rules leave to the cost model were measured slower on
+  // 128x128: 1568 rows' proj unsplit (104 tiles) 22.9 against 20.4 us; the mergers' K = 4096 GEMMs
+  // at 196 rows 25.2 / 26.8 against 20.3 / 24.2 us.
   // The head_dim-64 rotary qkv GEMM takes 64x192 tiles (6 waves of 32x64, whole heads; tiles may
   // straddle the q | k | v boundary, the epilogue picks the target per head) wherever one round of
   // them fits the CUs: alone on MI355X (1024 x 3072 x 1024 with norm1 folded), 196 / 400 / 576 /
@@ -1308,8 +1309,17 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
   const int tiles128 = ((rows + 127) / 128) * ((p.N + 127) / 128);
   if (pick == 0 && p.K <= kSmallTileMaxK && !p.row0 && !p.row1) {
     if (2 * tiles128 >= cus && tiles128 <= cus) {
-      pick = 6;
-      e = plan_gemm<128, 128>(p, cus, kRate128x128, -1);
+      // below a full round of 128x128 tiles, one to two rounds of 64x128 run ahead (alone: fc1 at
+      // 784 rows 14.8 against 15.8 us, the 8B fc1 16.3 against 17.2, proj at 2304 rows 16.1 against
+      // 20.6; in the forward a 2304-patch image 4.013 -> 3.889 ms); a full round stays on 128x128
+      // (fc1 at 1024 rows: two full rounds of 64x128 made the forward 0.9 % slower)
+      if (tiles128 < cus) {
+        pick = 8;
+        e = plan_gemm<64, 128>(p, cus, kRate128x128, -1);
+      } else {
+        pick = 6;
+        e = plan_gemm<128, 128>(p, cus, kRate128x128, -1);
+      }
     } else if (f.split_mode >= 0 && 2 * tiles128 < cus) {
       const GemmPlan sp = plan_gemm<128, 128>(p, cus, kRate128x128, 1);
       if (8 * sp.tail * sp.split >= 7 * cus) {
