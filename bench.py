@@ -206,12 +206,69 @@ def attention_config1(args):
     print(json.dumps(out_line), flush=True)
 
 
+def single_image_config0(args):
+    """one 448x448 image (grid 1x28x28 = 784 patches) through the full 2B tower, the
+    reference's CPU-runnable case, in fp32 (its default dtype: `value`) and in bf16, each with its
+    grid metadata cached and pixels resident in HBM, --steps forwards after --warmup timed with HIP
+    events; beside it the torch-CPU fp32 restatement of the reference on the same image (1 warm-up +
+    3 timed reps, median). A secondary line: config 2 is the headline."""
+    import torch
+    from __graft_entry__ import load_package
+    from oracle import torch_tower as tt
+    from oracle import vision_tower as vt
+    pkg = load_package()
+    pkg.capi.load()
+    spec = pkg.spec_2b()
+    grid = [(1, 28, 28)]
+    grids = np.array(grid, np.int32)
+    N = 784
+    params = pkg.random_params(spec, seed=0)
+    px_host = np.random.default_rng(7).standard_normal((N, spec.patch_volume), dtype=np.float32)
+    px = torch.from_numpy(px_host).to("cuda:0")
+    flops = tower_flops(N, [N])
+    res = {}
+    for dtype, peak in (("float32", 157.3), ("bfloat16", 2516.6)):
+        tower = pkg.Qwen3VisionTransformer(spec, dtype=dtype).bind(params)
+        tower.metadata(grids)
+        for _ in range(args.warmup):
+            tower(px, grids)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            tower(px, grids)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        res[dtype] = {"patches_per_s": round(N / ms * 1e3, 1), "ms_per_step": round(ms, 4),
+                      "tflops": round(flops / ms / 1e9, 1), "frac_peak": round(flops / ms / 1e9 / peak, 4),
+                      "peak_tflops": peak}
+        del tower
+    out = {"metric": "vision patches/sec for encode_vision, BASELINE config 0 (one 448x448 image, 2B tower, 1 GPU)",
+           "value": res["float32"]["patches_per_s"], "unit": "patches/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": res["float32"]["ms_per_step"], "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic (random-init weights N(0,0.02), patches N(0,1))",
+           "config": {"workload": "BASELINE config 0: 2B vision tower, one 448x448 image, grid (1,28,28) = 784 "
+                                  "patches in one segment, deepstack after blocks 5/11/17"},
+           "float32": res["float32"], "bfloat16": res["bfloat16"],
+           "secondary": "BASELINE config 0: the reference's CPU-runnable case, not the headline bench line"}
+    if not args.no_cpu:
+        eager32 = tt.TorchTower(params, vt.VisionSpec(depth=24), "fp32")
+        med, ts = _median_time(lambda: eager32(px_host, grid))
+        out["cpu_baseline"] = {"value": round(N / med, 2), "unit": "patches/s", "cores": int(torch.get_num_threads()),
+                               "kind": "port", "sample": f"the same 784-patch image through the torch-CPU eager fp32 "
+                                                         f"restatement, 1 warm-up + 3 timed reps, median {med:.2f} s"}
+        out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=2, choices=[1] + sorted(WORKLOADS),
+    ap.add_argument("--config", type=int, default=2, choices=[0, 1] + sorted(WORKLOADS),
                     help="BASELINE config to run (2 = the headline metric's workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cpu-compiled", action="store_true", help="skip the torch.compile CPU variant (~35 s)")
@@ -228,6 +285,8 @@ def main():
         sys.exit(2)
     if args.config == 1:
         return attention_config1(args)
+    if args.config == 0:
+        return single_image_config0(args)
 
     import torch
     from __graft_entry__ import load_package
