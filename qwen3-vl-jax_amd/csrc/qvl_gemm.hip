@@ -1312,8 +1312,9 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
       // below a full round of 128x128 tiles, one to two rounds of 64x128 run ahead (alone: fc1 at
       // 784 rows 14.8 against 15.8 us, the 8B fc1 16.3 against 17.2, proj at 2304 rows 16.1 against
       // 20.6; in the forward a 2304-patch image 4.013 -> 3.889 ms); a full round stays on 128x128
-      // (fc1 at 1024 rows: two full rounds of 64x128 made the forward 0.9 % slower)
-      if (tiles128 < cus) {
+      // (fc1 at 1024 rows: two full rounds of 64x128 made the forward 0.9 % slower); the head_dim-64
+      // rotary qkv stays on 128x128 (64x128: 24-26 against 17.7 us at 784 tokens)
+      if (tiles128 < cus && EPI != kEpiQkvRope) {
         pick = 8;
         e = plan_gemm<64, 128>(p, cus, kRate128x128, -1);
       } else {
