@@ -1333,6 +1333,18 @@ static int dispatch_gemm(const GemmParams& p, hipStream_t stream) {
       pick = 8;
     }
   }
+  // Long K (fc2, K = 4096 / 4352) from 512 rows: 128x128 tiles split along K where up to 8 parts fill
+  // at least 7/8 of the CUs (one 784-token image's fc2: 23.9 against 25.2 us for 288x128 tiles in 8
+  // parts); at the mergers' 196 rows the cost model's plans stay ahead (25.2 / 26.8 against 20.3 /
+  // 24.2 us on 128x128).
+  if (pick == 0 && p.K > kSmallTileMaxK && rows >= 512 && f.split_mode >= 0 && !p.row0 && !p.row1 &&
+      EPI != kEpiBiasPosEmbed && 2 * tiles128 < cus) {
+    const GemmPlan sp = plan_gemm<128, 128>(p, cus, kRate128x128, 1);
+    if (8 * sp.tail * sp.split >= 7 * cus) {
+      pick = 6;
+      e = sp;
+    }
+  }
   // A folded LayerNorm over more than 16 row groups (the deepstack mergers' 4-token rows: 32 or 36)
   // combines each row's partials in the workgroup's prologue; on small grids 64-row tiles split
   // along K spread that over 4x the workgroups (one 784-token image's deepstack fc1, K = 4096:
